@@ -1,0 +1,125 @@
+/*
+ * mi_qmm.h -- C ABI of the MI355X (gfx950) affine quantized-matmul library.
+ *
+ * Drop-in boundary for the mlx-c calls that ddalcu/mlx-serve makes for every
+ * quantized linear layer and MoE expert. Each entry point names the mlx-c
+ * function it replaces (declared in the reference at src/mlx.zig). The argument
+ * order follows the mlx-c call; mlx_array handles become raw device pointers
+ * plus explicit shapes, and mlx_stream becomes a hipStream_t passed as void*.
+ *
+ * Conventions
+ *   - All tensor arguments are DEVICE pointers to row-contiguous memory.
+ *     Packed weights are uint32 [.., N, K*bits/32]; scales/biases [.., N, K/group_size].
+ *   - Calls are asynchronous on `stream` (NULL = the default stream) and never
+ *     synchronize the host. Indices may stay GPU-resident.
+ *   - Return 0 on success. MI_ERR_UNSUPPORTED means "this library declines the
+ *     call; use your fallback" (the reference expresses this by returning null
+ *     from its kernel wrappers, src/transformer.zig:20317-20358). Other non-zero
+ *     codes are errors, like mlx.check()'s error.MlxError (src/mlx.zig:547-550).
+ *     mi_last_error() returns a thread-local message for the last failure.
+ *   - dtype codes are mlx_dtype's values (src/mlx.zig:20-35).
+ */
+#ifndef MI_QMM_H
+#define MI_QMM_H
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MI_OK = 0,
+  MI_ERR_UNSUPPORTED = 1, /* decline: valid request outside this library's scope */
+  MI_ERR_INVALID = 2,     /* bad pointer / shape / argument */
+  MI_ERR_HIP = 3,         /* HIP runtime error (launch, allocation) */
+};
+
+/* Values match mlx_dtype (src/mlx.zig:20-35). */
+enum {
+  MI_DTYPE_UINT32 = 3,
+  MI_DTYPE_FLOAT16 = 9,
+  MI_DTYPE_FLOAT32 = 10,
+  MI_DTYPE_BFLOAT16 = 12,
+};
+
+/* Mirrors mlx_optional_int (src/mlx.zig:40-50). has_value=false -> MLX default
+ * (group_size 64, bits 4). */
+typedef struct {
+  int value;
+  bool has_value;
+} mi_optional_int;
+
+/* Replaces mlx_quantized_matmul (src/mlx.zig:262), mode "affine", transpose=true:
+ *   y[M,N] = x[M,K] @ dequant(w)[N,K]^T, dequant(w) = scale*q + bias per group.
+ * x: x_dtype in {bfloat16, float32}; y has x's dtype. scales/biases: sb_dtype
+ * bfloat16. bits in {4,8}; group_size in {32,64,128}; K % group_size == 0.
+ * transpose=false and other modes return MI_ERR_UNSUPPORTED. */
+int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
+                        const void* biases, int64_t M, int64_t N, int64_t K, bool transpose,
+                        mi_optional_int group_size, mi_optional_int bits, const char* mode,
+                        int x_dtype, int sb_dtype, void* stream);
+
+/* Replaces mlx_gather_qmm (src/mlx.zig:265), transpose=true, mode "affine":
+ *   y[i] = x[lhs(i)] @ dequant(w[rhs(i)])^T      for i in [0, n_idx)
+ * x: [x_batch, M, K]; w: [n_experts, N, K*bits/32]; scales/biases [n_experts, N, K/gs];
+ * y: [n_idx, M, N]. lhs_indices may be NULL: lhs(i) = i / lhs_div (lhs_div=1 is MLX's
+ * default arange; lhs_div=top_k is one token broadcast over its top-k slots, the
+ * reference's decode call). rhs_indices may be NULL: rhs(i) = i.
+ * Indices are uint32 device arrays. sorted_indices=true groups consecutive equal
+ * rhs values into one weight pass per run (any order stays correct; sorted order
+ * is what makes it fast). Out-of-range indices write NaN rows, never read out of
+ * bounds. Uses a per-stream device workspace when sorted_indices=true. */
+int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
+                  const void* biases, const uint32_t* lhs_indices, const uint32_t* rhs_indices,
+                  int64_t n_idx, int64_t lhs_div, int64_t x_batch, int64_t M, int64_t N, int64_t K,
+                  int64_t n_experts, bool transpose, mi_optional_int group_size,
+                  mi_optional_int bits, const char* mode, bool sorted_indices, int x_dtype,
+                  int sb_dtype, void* stream);
+
+/* Replaces mlx_dequantize (src/mlx.zig:271), mode "affine", no global scale:
+ *   out[r,k] = scale[r,k/gs] * q[r,k] + bias[r,k/gs]
+ * out_dtype float32: exact fp32 result. out_dtype bfloat16: rounded like MLX's
+ * composed dequantize (a bf16 multiply then a bf16 add). */
+int mi_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,
+                  int64_t rows, int64_t K, mi_optional_int group_size, mi_optional_int bits,
+                  const char* mode, int sb_dtype, int out_dtype, void* stream);
+
+/* Same as mi_dequantize with an explicit bf16 rounding: rounding 0 = one rounding
+ * of s*q+b, 1 = op-by-op (the mi_dequantize default). No mlx-c counterpart: MLX's
+ * rounding of a bf16 dequantize is not pinned by any data available to this
+ * build, so both are offered. */
+int mi_dequantize_rounding(void* out, const uint32_t* w, const void* scales, const void* biases,
+                           int64_t rows, int64_t K, mi_optional_int group_size,
+                           mi_optional_int bits, const char* mode, int sb_dtype, int out_dtype,
+                           int rounding, void* stream);
+
+/* Replaces mlx_quantize (src/mlx.zig:275), mode "affine": w [rows,K] (bfloat16 or
+ * float32) -> packed uint32 wq, scales/biases in w's dtype (bfloat16 only here). */
+int mi_quantize(uint32_t* wq, void* scales, void* biases, const void* w, int64_t rows, int64_t K,
+                mi_optional_int group_size, mi_optional_int bits, const char* mode, int w_dtype,
+                void* stream);
+
+/* Solve (bits, group_size) from packed geometry, as affineParamsFromGeometry
+ * (src/transformer.zig:16763-16782): bits = w_cols*32/in_dim, gs = in_dim/s_cols.
+ * Returns 0, or MI_ERR_INVALID when the geometry is not an affine layout. Host only. */
+int mi_affine_params_from_geometry(int64_t w_cols, int64_t s_cols, int64_t in_dim, int* bits,
+                                   int* group_size);
+
+/* Synthetic-input generator used by the benchmark (no reference counterpart):
+ * out[i] = mean + std * N(0,1) as bfloat16 (dtype bfloat16) or float32, from a
+ * counter-based SplitMix64 + Box-Muller stream keyed by seed. */
+int mi_fill_randn(void* out, int64_t n, uint64_t seed, float mean, float stddev, int dtype,
+                  void* stream);
+
+/* Thread-local text of the last non-zero return on this thread ("" if none). */
+const char* mi_last_error(void);
+
+/* Library version string. */
+const char* mi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,64 @@
+// Internal (host + device) declarations shared by the kernels and the C ABI layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi {
+
+// Small-M / gather kernel parameters (qmv.hip).
+struct QmvParams {
+  const uint32_t* w;       // [E, N, K*bits/32]
+  const uint16_t* scales;  // [E, N, K/gs] bf16 bits
+  const uint16_t* biases;  // [E, N, K/gs] bf16 bits
+  const void* x;           // [x_batch, M, K] bf16 or f32
+  void* y;                 // [n_pairs, M, N] same dtype as x
+  const uint32_t* lhs;     // nullable: lhs(i) = i / lhs_div
+  const uint32_t* rhs;     // nullable: rhs(i) = i
+  const uint32_t* items;   // nullable: sorted work list, 4 u32 per item (expert, pos0, cnt, 0)
+  const uint32_t* item_count;  // device count for `items`
+  int64_t n_pairs, lhs_div, x_batch, n_experts;
+  int M, N, K;
+  int bits, group_size, x_f32;
+  int rows_per_item;   // 16*MT rows covered per item
+  int items_per_pair;  // unsorted: ceil(M / rows_per_item)
+  int n_items_fixed;   // unsorted: n_pairs * items_per_pair
+};
+
+struct QmvConfig {
+  int row_groups;  // grid.x: ceil(N / (16*rt))
+  int grid_y;      // grid.y (items, capped; the kernel strides over the rest)
+  int waves;       // waves per block = split-K factor
+  int rt;          // 16-row weight tiles per wave
+  int rows;        // max activation rows per item (selects MT/R4)
+};
+
+hipError_t launch_qmv(const QmvParams& P, const QmvConfig& C, hipStream_t s);
+
+// Sorted gather: runs of equal rhs -> work items (moe.hip / segments.hip).
+hipError_t launch_build_items(const uint32_t* rhs, int64_t n_pairs, int M, int rows_per_item,
+                              uint32_t* items, uint32_t* item_count, int64_t max_items,
+                              hipStream_t s);
+
+// Prefill GEMM (qmm.hip). Returns hipErrorNotSupported if the shape is not handled.
+struct QmmParams {
+  const uint32_t* w;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  const uint16_t* x;  // bf16 [M, K]
+  uint16_t* y;        // bf16 [M, N]
+  int M, N, K;
+  int bits, group_size;
+};
+hipError_t launch_qmm(const QmmParams& P, hipStream_t s);
+bool qmm_supported(int M, int N, int K, int bits, int gs);
+
+// Quantize / dequantize / generator (quant.hip).
+hipError_t launch_dequantize(void* out, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                             int64_t rows, int64_t K, int gs, int bits, int out_f32, int rounding,
+                             hipStream_t st);
+hipError_t launch_quantize(uint32_t* wq, uint16_t* s, uint16_t* b, const void* w, int w_f32,
+                           int64_t rows, int64_t K, int gs, int bits, hipStream_t st);
+hipError_t launch_randn(void* out, int64_t n, uint64_t seed, float mean, float stddev,
+                        int out_f32, hipStream_t st);
+
+}  // namespace mi

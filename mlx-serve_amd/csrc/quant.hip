@@ -1,0 +1,263 @@
+// Affine quantize / dequantize kernels, the sorted-gather work-list builder and the
+// synthetic input generator.
+#include "mi_common.h"
+#include "mi_internal.h"
+
+namespace mi {
+
+namespace {
+
+// ---------------------------------------------------------------- dequantize --
+// One thread per packed word: w = scale*q + bias (scale*q is exact in fp32).
+// rounding 0: bf16(s*q + b); 1: bf16(bf16(s*q) + b) (a bf16 multiply then a bf16 add).
+template <int BITS>
+__global__ void dequant_kernel(void* __restrict__ out, const uint32_t* __restrict__ w,
+                               const uint16_t* __restrict__ s, const uint16_t* __restrict__ b,
+                               int64_t n_words, int64_t K, int gs, int out_f32, int rounding) {
+  constexpr int PF = 32 / BITS;
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  const int64_t wpr = K / PF;
+  const int64_t G = K / gs;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_words;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / wpr;
+    const int64_t k0 = (i - row * wpr) * PF;
+    const int64_t gi = row * G + k0 / gs;
+    const float sc = bf16_bits_to_f32(s[gi]);
+    const float bi = bf16_bits_to_f32(b[gi]);
+    const uint32_t word = w[i];
+    float v[PF];
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const float sq = sc * (float)((word >> (j * BITS)) & MASK);
+      v[j] = rounding ? bf16_bits_to_f32(f32_to_bf16_bits(sq)) + bi : sq + bi;
+    }
+    const int64_t o = row * K + k0;
+    if (out_f32) {
+      float* op = (float*)out + o;
+#pragma unroll
+      for (int j = 0; j < PF; j += 4) *(float4*)(op + j) = float4{v[j], v[j + 1], v[j + 2], v[j + 3]};
+    } else {
+      uint32_t* op = (uint32_t*)((uint16_t*)out + o);
+#pragma unroll
+      for (int j = 0; j < PF; j += 2)
+        op[j / 2] = f32_to_bf16_bits(v[j]) | (f32_to_bf16_bits(v[j + 1]) << 16);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ quantize --
+// One thread per group. Same fp32 steps as the MLX affine group quantizer:
+// scale = max((max-min)/(2^bits-1), 1e-7) signed toward the larger-magnitude edge,
+// q0 = rint(edge/scale); if q0 != 0: scale = edge/q0, bias = edge; else bias = 0.
+// Codes clamp(rint((w-bias)/scale), 0, 2^bits-1) with the fp32 scale.
+__global__ void quant_kernel(uint32_t* __restrict__ wq, uint16_t* __restrict__ so,
+                             uint16_t* __restrict__ bo, const void* __restrict__ w, int w_f32,
+                             int64_t n_groups, int gs, int bits) {
+  const float n_bins = (float)((1 << bits) - 1);
+  const int pf = 32 / bits;
+  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < n_groups;
+       gi += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t base = gi * gs;
+    auto ld = [&](int j) -> float {
+      return w_f32 ? ((const float*)w)[base + j]
+                   : bf16_bits_to_f32(((const uint16_t*)w)[base + j]);
+    };
+    float wmax = -INFINITY, wmin = INFINITY;
+    for (int j = 0; j < gs; ++j) {
+      const float v = ld(j);
+      wmax = fmaxf(wmax, v);
+      wmin = fminf(wmin, v);
+    }
+    const bool mask = fabsf(wmin) > fabsf(wmax);
+    float scale = fmaxf(__fdiv_rn(wmax - wmin, n_bins), 1e-7f);
+    scale = mask ? scale : -scale;
+    const float edge = mask ? wmin : wmax;
+    const float q0 = rintf(__fdiv_rn(edge, scale));
+    float bias = 0.f;
+    if (q0 != 0.f) {
+      scale = __fdiv_rn(edge, q0);
+      bias = edge;
+    }
+    uint32_t* out = wq + gi * (gs / pf);
+    for (int c = 0; c < gs / pf; ++c) {
+      uint32_t word = 0;
+      for (int j = 0; j < pf; ++j) {
+        float qv = rintf(__fdiv_rn(__fsub_rn(ld(c * pf + j), bias), scale));
+        qv = fminf(fmaxf(qv, 0.f), n_bins);
+        word |= (uint32_t)qv << (j * bits);
+      }
+      out[c] = word;
+    }
+    so[gi] = (uint16_t)f32_to_bf16_bits(scale);
+    bo[gi] = (uint16_t)f32_to_bf16_bits(bias);
+  }
+}
+
+// ----------------------------------------------------------------- generator --
+__device__ uint64_t splitmix64(uint64_t seed, uint64_t counter) {
+  uint64_t z = seed + (counter + 1) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__global__ void randn_kernel(void* out, int64_t n, uint64_t seed, float mean, float stddev,
+                             int out_f32) {
+  const int64_t pairs = (n + 1) / 2;
+  for (int64_t j = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; j < pairs;
+       j += (int64_t)gridDim.x * blockDim.x) {
+    const uint64_t a = splitmix64(seed, 2 * j), b = splitmix64(seed, 2 * j + 1);
+    const double u1 = ((double)(a >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+    const double u2 = (double)(b >> 11) * (1.0 / 9007199254740992.0);
+    const double r = sqrt(-2.0 * log(u1));
+    double sn, cs;
+    sincos(6.283185307179586476925286766559 * u2, &sn, &cs);
+    const float z0 = (float)(mean + stddev * (r * cs));
+    const float z1 = (float)(mean + stddev * (r * sn));
+    if (out_f32) {
+      ((float*)out)[2 * j] = z0;
+      if (2 * j + 1 < n) ((float*)out)[2 * j + 1] = z1;
+    } else {
+      ((uint16_t*)out)[2 * j] = (uint16_t)f32_to_bf16_bits(z0);
+      if (2 * j + 1 < n) ((uint16_t*)out)[2 * j + 1] = (uint16_t)f32_to_bf16_bits(z1);
+    }
+  }
+}
+
+// ------------------------------------------------------------ sorted items --
+// One 1024-thread block. For every run of equal rhs values (pairs [a, b)), the
+// flattened positions [a*M, b*M) are cut into chunks of R rows; each chunk start
+// becomes an item (expert, pos0, limit, 0) with limit = min(R, total - pos0). The
+// consumer keeps a row only while its pair's rhs equals the item's expert, so the
+// run end is never needed here. Pair j owns the chunk starts that fall in its own
+// positions: ceil((o+1)M/R) - ceil(oM/R) with o = j - a.
+constexpr int kBT = 1024;
+
+template <bool MAX>
+__device__ int64_t block_scan_incl(int64_t v, int64_t* sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t o = __shfl_up(v, d, 64);
+    if (lane >= d) v = MAX ? (o > v ? o : v) : v + o;
+  }
+  if (lane == 63) sh[wave] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < kBT / 64; ++i) sh[i] = MAX ? (sh[i - 1] > sh[i] ? sh[i - 1] : sh[i]) : sh[i - 1] + sh[i];
+  }
+  __syncthreads();
+  if (wave > 0) {
+    const int64_t p = sh[wave - 1];
+    v = MAX ? (p > v ? p : v) : v + p;
+  }
+  __syncthreads();
+  return v;
+}
+
+__global__ void __launch_bounds__(kBT) build_items_kernel(const uint32_t* __restrict__ rhs,
+                                                          int64_t n_pairs, int M, int R,
+                                                          uint32_t* __restrict__ items,
+                                                          uint32_t* __restrict__ count,
+                                                          int64_t max_items) {
+  __shared__ int64_t sh[kBT / 64];
+  __shared__ int64_t carry_a, carry_n;
+  if (threadIdx.x == 0) { carry_a = 0; carry_n = 0; }
+  __syncthreads();
+  const int64_t total = n_pairs * M;
+  for (int64_t t0 = 0; t0 < n_pairs; t0 += kBT) {
+    const int64_t j = t0 + threadIdx.x;
+    const bool in = j < n_pairs;
+    const bool start = in && (j == 0 || rhs[j] != rhs[j - 1]);
+    int64_t a = block_scan_incl<true>(start ? j : -1, sh);
+    const int64_t ca = carry_a;
+    if (a < ca) a = ca;
+    int64_t c = 0;
+    if (in) {
+      const int64_t o = j - a;
+      c = ((o + 1) * M + R - 1) / R - (o * M + R - 1) / R;
+    }
+    const int64_t incl = block_scan_incl<false>(c, sh);
+    const int64_t off = carry_n + incl - c;
+    if (in) {
+      const int64_t o = j - a;
+      int64_t first = (o * M + R - 1) / R;
+      for (int64_t t = 0; t < c; ++t) {
+        const int64_t idx = off + t;
+        if (idx < max_items) {
+          const int64_t pos0 = a * M + (first + t) * R;
+          const int64_t lim = total - pos0 < R ? total - pos0 : R;
+          items[4 * idx + 0] = rhs[j];
+          items[4 * idx + 1] = (uint32_t)pos0;
+          items[4 * idx + 2] = (uint32_t)lim;
+          items[4 * idx + 3] = 0u;
+        }
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x == kBT - 1) {
+      carry_a = a;
+      carry_n = off + c;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const int64_t n = carry_n < max_items ? carry_n : max_items;
+    *count = (uint32_t)n;
+  }
+}
+
+inline unsigned grid_for(int64_t n, int bs) {
+  int64_t g = (n + bs - 1) / bs;
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return (unsigned)g;
+}
+
+}  // namespace
+
+hipError_t launch_dequantize(void* out, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                             int64_t rows, int64_t K, int gs, int bits, int out_f32, int rounding,
+                             hipStream_t st) {
+  const int64_t n_words = rows * (K * bits / 32);
+  if (n_words == 0) return hipSuccess;
+  if (out_f32) rounding = 0;  // the fp32 result is exact; rounding applies to bf16 only
+  const int bs = 256;
+  if (bits == 4)
+    hipLaunchKernelGGL(dequant_kernel<4>, dim3(grid_for(n_words, bs)), dim3(bs), 0, st, out, w, s,
+                       b, n_words, K, gs, out_f32, rounding);
+  else
+    hipLaunchKernelGGL(dequant_kernel<8>, dim3(grid_for(n_words, bs)), dim3(bs), 0, st, out, w, s,
+                       b, n_words, K, gs, out_f32, rounding);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize(uint32_t* wq, uint16_t* s, uint16_t* b, const void* w, int w_f32,
+                           int64_t rows, int64_t K, int gs, int bits, hipStream_t st) {
+  const int64_t ng = rows * (K / gs);
+  if (ng == 0) return hipSuccess;
+  const int bs = 256;
+  hipLaunchKernelGGL(quant_kernel, dim3(grid_for(ng, bs)), dim3(bs), 0, st, wq, s, b, w, w_f32, ng,
+                     gs, bits);
+  return hipGetLastError();
+}
+
+hipError_t launch_randn(void* out, int64_t n, uint64_t seed, float mean, float stddev,
+                        int out_f32, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  const int bs = 256;
+  hipLaunchKernelGGL(randn_kernel, dim3(grid_for((n + 1) / 2, bs)), dim3(bs), 0, st, out, n, seed,
+                     mean, stddev, out_f32);
+  return hipGetLastError();
+}
+
+hipError_t launch_build_items(const uint32_t* rhs, int64_t n_pairs, int M, int rows_per_item,
+                              uint32_t* items, uint32_t* item_count, int64_t max_items,
+                              hipStream_t s) {
+  hipLaunchKernelGGL(build_items_kernel, dim3(1), dim3(kBT), 0, s, rhs, n_pairs, M, rows_per_item,
+                     items, item_count, max_items);
+  return hipGetLastError();
+}
+
+}  // namespace mi

@@ -1,0 +1,191 @@
+"""MLX-shaped ops over torch device tensors, each one call into libmi_qmm.so.
+
+Argument names, defaults and shape rules follow the mlx-c functions that
+ddalcu/mlx-serve binds in src/mlx.zig:262-275 (MLX's Python API has the same
+signatures): transpose=True, group_size 64 and bits 4 by default, mode "affine".
+torch is used only for device memory and the current HIP stream.
+"""
+import ctypes
+import math
+
+import torch
+
+from ._lib import (DT_BFLOAT16, DT_FLOAT32, MI_ERR_INVALID, MiError, check, lib, opt)
+
+_DT = {torch.bfloat16: DT_BFLOAT16, torch.float32: DT_FLOAT32}
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _dtype_code(t, what):
+    if t.dtype not in _DT:
+        raise MiError(MI_ERR_INVALID, f"{what} dtype {t.dtype} not supported")
+    return _DT[t.dtype]
+
+
+def _packed(w):
+    if w.dtype not in (torch.int32, torch.uint32):
+        raise MiError(MI_ERR_INVALID, f"packed weights must be 32-bit, got {w.dtype}")
+    return w
+
+
+def _require(cond, msg):
+    if not cond:
+        raise MiError(MI_ERR_INVALID, msg)
+
+
+def _resolve(w, scales, group_size, bits, K):
+    """MLX defaults (64, 4); validate against the packed geometry."""
+    gs = 64 if group_size is None else int(group_size)
+    nb = 4 if bits is None else int(bits)
+    _require(w.shape[-1] * 32 == K * nb,
+             f"packed width {w.shape[-1]} does not match K={K} at bits={nb}")
+    _require(scales.shape[-1] * gs == K,
+             f"scales width {scales.shape[-1]} does not match K={K} at group_size={gs}")
+    return gs, nb
+
+
+def _contig(*ts):
+    for t in ts:
+        if t is not None:
+            _require(t.is_contiguous(), "tensors must be row-contiguous")
+            _require(t.is_cuda, "tensors must be on the GPU")
+
+
+def quantized_matmul(x, w, scales, biases, transpose=True, group_size=None, bits=None,
+                     mode="affine"):
+    """y = x @ dequantize(w).T (mlx_quantized_matmul, src/mlx.zig:262). x [..., K]."""
+    _contig(x, w, scales, biases)
+    K = x.shape[-1]
+    gs, nb = _resolve(_packed(w), scales, group_size, bits, K)
+    _require(w.dim() == 2, "w must be [N, K*bits/32]")
+    N = w.shape[0]
+    M = x.numel() // K if K else 0
+    y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=x.device)
+    check(lib().mi_quantized_matmul(_ptr(y), _ptr(x), _ptr(w), _ptr(scales), _ptr(biases), M, N,
+                                    K, bool(transpose), opt(gs), opt(nb),
+                                    mode.encode() if mode else None, _dtype_code(x, "x"),
+                                    _dtype_code(scales, "scales"), _stream(x)))
+    return y
+
+
+def _broadcast_indices(x, w, lhs_indices, rhs_indices):
+    """MLX gather_qmm index rules: defaults are aranges over the batch dims of x and
+    w, both broadcast together. Returns (lhs or None, lhs_div, rhs or None, shape)."""
+    xb = tuple(x.shape[:-2])
+    wb = tuple(w.shape[:-2])
+    dev = x.device
+    lhs_shape = tuple(lhs_indices.shape) if lhs_indices is not None else xb
+    rhs_shape = tuple(rhs_indices.shape) if rhs_indices is not None else wb
+    shape = torch.broadcast_shapes(lhs_shape, rhs_shape)
+    n = math.prod(shape)
+
+    def as_u32(t):
+        t = t.to(dev)
+        if t.dtype not in (torch.int32, torch.uint32):
+            t = t.to(torch.int32)
+        return t.contiguous()
+
+    wb_full = (1,) * (len(shape) - len(wb)) + wb
+    if rhs_indices is None:
+        rhs = None if wb_full == shape else as_u32(
+            torch.arange(math.prod(wb), device=dev, dtype=torch.int32).reshape(wb_full)
+            .expand(shape))
+    else:
+        rhs = as_u32(rhs_indices.expand(shape) if tuple(rhs_indices.shape) != shape
+                     else rhs_indices)
+
+    if lhs_indices is not None:
+        lhs = lhs_indices
+        lhs = as_u32(lhs.expand(shape) if tuple(lhs.shape) != shape else lhs)
+        return lhs, 1, rhs, shape
+    # Default lhs = arange over x's batch dims. Common patterns need no index array:
+    # x batch == shape (one row per pair) or x batch == shape[:-1] + (1,) (one token
+    # broadcast over the trailing top-k axis).
+    xb_full = (1,) * (len(shape) - len(xb)) + xb
+    if xb_full == shape:
+        return None, 1, rhs, shape
+    if len(shape) >= 1 and xb_full[:-1] == shape[:-1] and xb_full[-1] == 1:
+        return None, shape[-1], rhs, shape
+    lhs = torch.arange(math.prod(xb), device=dev, dtype=torch.int32).reshape(xb_full)
+    return as_u32(lhs.expand(shape)), 1, rhs, shape
+
+
+def gather_qmm(x, w, scales, biases, lhs_indices=None, rhs_indices=None, transpose=True,
+               group_size=None, bits=None, mode="affine", sorted_indices=False):
+    """out[i] = x[lhs[i]] @ dequantize(w[rhs[i]]).T (mlx_gather_qmm, src/mlx.zig:265).
+    x [..., M, K], w [..., N, K*bits/32]; out shape = broadcast(lhs, rhs) + [M, N]."""
+    _contig(x, w, scales, biases)
+    _require(x.dim() >= 2 and w.dim() >= 2, "x and w need at least 2 dims")
+    K = x.shape[-1]
+    M = x.shape[-2]
+    gs, nb = _resolve(_packed(w), scales, group_size, bits, K)
+    N = w.shape[-2]
+    lhs, lhs_div, rhs, shape = _broadcast_indices(x, w, lhs_indices, rhs_indices)
+    n_idx = math.prod(shape)
+    x_batch = x.numel() // (M * K) if M * K else 0
+    n_exp = w.numel() // (N * w.shape[-1]) if N * w.shape[-1] else 0
+    y = torch.empty(tuple(shape) + (M, N), dtype=x.dtype, device=x.device)
+    check(lib().mi_gather_qmm(_ptr(y), _ptr(x), _ptr(w), _ptr(scales), _ptr(biases), _ptr(lhs),
+                              _ptr(rhs), n_idx, lhs_div, x_batch, M, N, K, n_exp,
+                              bool(transpose), opt(gs), opt(nb),
+                              mode.encode() if mode else None, bool(sorted_indices),
+                              _dtype_code(x, "x"), _dtype_code(scales, "scales"), _stream(x)))
+    return y
+
+
+def dequantize(w, scales, biases, group_size=None, bits=None, mode="affine", dtype=None,
+               rounding=None):
+    """mlx_dequantize (src/mlx.zig:271). dtype defaults to the scales dtype.
+    rounding (bf16 output only): None/1 = op-by-op bf16, 0 = single rounding."""
+    _contig(w, scales, biases)
+    K = w.shape[-1] * 32 // (4 if bits is None else int(bits))
+    gs, nb = _resolve(_packed(w), scales, group_size, bits, K)
+    dtype = scales.dtype if dtype is None else dtype
+    rows = w.numel() // w.shape[-1] if w.shape[-1] else 0
+    out = torch.empty(tuple(w.shape[:-1]) + (K,), dtype=dtype, device=w.device)
+    check(lib().mi_dequantize_rounding(_ptr(out), _ptr(w), _ptr(scales), _ptr(biases), rows, K,
+                                       opt(gs), opt(nb), mode.encode() if mode else None,
+                                       _dtype_code(scales, "scales"), _dtype_code(out, "out"),
+                                       1 if rounding is None else int(rounding), _stream(w)))
+    return out
+
+
+def quantize(w, group_size=None, bits=None, mode="affine"):
+    """mlx_quantize (src/mlx.zig:275): returns (wq int32-bits, scales, biases)."""
+    _contig(w)
+    gs = 64 if group_size is None else int(group_size)
+    nb = 4 if bits is None else int(bits)
+    K = w.shape[-1]
+    _require(K % gs == 0, f"K={K} not a multiple of group_size={gs}")
+    rows = w.numel() // K if K else 0
+    lead = tuple(w.shape[:-1])
+    wq = torch.empty(lead + (K * nb // 32,), dtype=torch.int32, device=w.device)
+    sdt = torch.bfloat16
+    s = torch.empty(lead + (K // gs,), dtype=sdt, device=w.device)
+    b = torch.empty(lead + (K // gs,), dtype=sdt, device=w.device)
+    check(lib().mi_quantize(_ptr(wq), _ptr(s), _ptr(b), _ptr(w), rows, K, opt(gs), opt(nb),
+                            mode.encode() if mode else None, _dtype_code(w, "w"), _stream(w)))
+    return wq, s, b
+
+
+def fill_randn(t, seed, mean=0.0, std=1.0):
+    """Fill a bf16/f32 device tensor from the library's counter-based normal stream."""
+    _contig(t)
+    check(lib().mi_fill_randn(_ptr(t), t.numel(), int(seed) & ((1 << 64) - 1), float(mean),
+                              float(std), _dtype_code(t, "t"), _stream(t)))
+    return t
+
+
+def affine_params_from_geometry(w_cols, s_cols, in_dim):
+    """(bits, group_size) from packed geometry, or None (src/transformer.zig:16763)."""
+    b, g = ctypes.c_int(0), ctypes.c_int(0)
+    rc = lib().mi_affine_params_from_geometry(int(w_cols), int(s_cols), int(in_dim),
+                                              ctypes.byref(b), ctypes.byref(g))
+    return None if rc != 0 else (b.value, g.value)

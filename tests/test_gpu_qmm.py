@@ -1,0 +1,188 @@
+"""GPU parity of libmi_qmm.so against the CPU oracle (calls go through the C ABI via
+mi_qmm's ctypes binding). Tolerances: bf16 output max-abs-err <= 1e-2*||y||inf,
+fp32 output <= 1e-3*||y||inf, both against fp64 truth on exactly dequantized
+weights; dequantize/quantize/indices are bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import (BF16_TOL, F32_TOL, bf16_bits, max_err_ratio, to_dev_bf16, to_dev_u32,
+                     to_f64, weights)
+import mi_qmm
+
+pytestmark = pytest.mark.gpu
+
+
+def _print_case(**kw):
+    print("CASE", kw, flush=True)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_dequantize_bit_exact(dev, bits, gs):
+    _print_case(t="dequant", bits=bits, gs=gs)
+    wq, s, b = weights(1, 96, 512, bits, gs, 11)
+    wq, s, b = wq[0], s[0], b[0]
+    W, S, B = to_dev_u32(wq, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev)
+    f32 = mi_qmm.dequantize(W, S, B, gs, bits, dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(f32.view(np.uint32),
+                          O.dequantize(wq, s, b, gs, bits, O.DQ_F32).view(np.uint32))
+    for rounding, kind in ((1, O.DQ_BF16_OPWISE), (0, O.DQ_BF16_FUSED)):
+        got = bf16_bits(mi_qmm.dequantize(W, S, B, gs, bits, dtype=torch.bfloat16,
+                                          rounding=rounding))
+        assert np.array_equal(got, O.dequantize(wq, s, b, gs, bits, kind))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_quantize_bit_exact(dev, bits, gs):
+    _print_case(t="quant", bits=bits, gs=gs)
+    w = O.f32_to_bf16(O.randn(64 * 512, 21, 0.0, 0.02).reshape(64, 512))
+    # a few adversarial groups: constant, all-zero, one outlier, exact grid
+    w[0, :gs] = O.f32_to_bf16(np.full(gs, 0.5, np.float32))
+    w[1, :gs] = 0
+    w[2, :gs] = O.f32_to_bf16(np.r_[np.zeros(gs - 1), [3.0]].astype(np.float32))
+    w[3, :gs] = O.f32_to_bf16((np.arange(gs) % 16 - 5).astype(np.float32) * 0.125)
+    wq, s, b = mi_qmm.quantize(to_dev_bf16(w, dev), gs, bits)
+    rq, rs, rb = O.quantize(w, gs, bits)
+    assert np.array_equal(wq.cpu().numpy().view(np.uint32), rq)
+    assert np.array_equal(bf16_bits(s), rs)
+    assert np.array_equal(bf16_bits(b), rb)
+
+
+QMM_CASES = [(1, 4096, 512), (1, 100, 1024), (2, 64, 256), (3, 48, 512), (4, 80, 256),
+             (5, 32, 384), (8, 64, 512), (16, 64, 256), (17, 40, 256), (32, 96, 512),
+             (33, 64, 256), (64, 48, 256)]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("M,N,K", QMM_CASES)
+def test_qmm_bf16(dev, M, N, K, bits, gs):
+    if K % gs:
+        pytest.skip("K not a multiple of gs")
+    _print_case(t="qmm_bf16", M=M, N=N, K=K, bits=bits, gs=gs)
+    wq, s, b = weights(1, N, K, bits, gs, 1000 + M)
+    x = O.make_x_bf16(M, K, 2000 + N)
+    y = mi_qmm.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(wq[0], dev),
+                                to_dev_bf16(s[0], dev), to_dev_bf16(b[0], dev), True, gs, bits)
+    truth = O.qmm_f64(x, wq[0], s[0], b[0], gs, bits)
+    assert y.shape == (M, N) and y.dtype == torch.bfloat16
+    assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 1024), (3, 64, 512), (20, 48, 256)])
+def test_qmm_f32(dev, M, N, K, bits):
+    _print_case(t="qmm_f32", M=M, N=N, K=K, bits=bits)
+    wq, s, b = weights(1, N, K, bits, 64, 3000 + M)
+    x = O.randn(M * K, 4000 + N).reshape(M, K)
+    y = mi_qmm.quantized_matmul(torch.from_numpy(x).to(dev), to_dev_u32(wq[0], dev),
+                                to_dev_bf16(s[0], dev), to_dev_bf16(b[0], dev), True, 64, bits)
+    truth = O.qmm_f64(x, wq[0], s[0], b[0], 64, bits)
+    assert y.dtype == torch.float32
+    assert max_err_ratio(y.cpu().numpy().astype(np.float64), truth) <= F32_TOL
+
+
+def test_qmm_special_cases(dev):
+    """One-hot x reads out one dequantized column; scale 1 / bias 0 integer weights
+    give an exact integer matmul."""
+    _print_case(t="special")
+    N, K = 64, 256
+    q = (np.arange(N * K) * 7 % 16).astype(np.uint8).reshape(N, K)
+    wq = O.pack(q, 4)
+    one = O.f32_to_bf16(np.ones((N, K // 64), np.float32))
+    zero = np.zeros((N, K // 64), np.uint16)
+    x = np.zeros((4, K), np.float32)
+    x[0, 5] = 1.0
+    x[1, :] = 1.0
+    x[2, ::3] = 2.0
+    x[3] = (np.arange(K) % 5).astype(np.float32)
+    xb = O.f32_to_bf16(x)
+    y = mi_qmm.quantized_matmul(to_dev_bf16(xb, dev), to_dev_u32(wq, dev), to_dev_bf16(one, dev),
+                                to_dev_bf16(zero, dev), True, 64, 4)
+    exact = x.astype(np.float64) @ q.T.astype(np.float64)
+    got = to_f64(y)
+    # bf16 output holds integers up to 256 exactly; compare after bf16 rounding
+    assert np.array_equal(got, O.bf16_to_f32(O.f32_to_bf16(exact.astype(np.float32))))
+    assert np.array_equal(got[0], q[:, 5].astype(np.float64))
+
+
+def test_gather_decode_broadcast(dev):
+    """Reference decode call: x [B,S,1,1,D] with inds [B,S,K], no lhs (lhs = i / K)."""
+    _print_case(t="gather_decode")
+    E, N, K, topk = 16, 96, 512, 4
+    wq, s, b = weights(E, N, K, 4, 64, 55)
+    x = O.make_x_bf16(2, K, 56)  # B*S = 2 tokens
+    inds = np.array([[3, 0, 15, 7], [7, 7, 2, 9]], np.uint32)
+    xd = to_dev_bf16(x, dev).reshape(1, 2, 1, 1, K)
+    y = mi_qmm.gather_qmm(xd, to_dev_u32(wq, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev),
+                          rhs_indices=to_dev_u32(inds.reshape(1, 2, topk), dev), group_size=64,
+                          bits=4)
+    assert y.shape == (1, 2, topk, 1, N)
+    truth = O.gather_qmm_f64(x.reshape(2, 1, K), wq, s, b, None, inds.reshape(-1), 2 * topk,
+                             lhs_div=topk)
+    assert max_err_ratio(to_f64(y).reshape(2 * topk, 1, N), truth) <= BF16_TOL
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_gather_sorted_matches_unsorted(dev, M):
+    """Sorted (grouped) path == unsorted path bit-for-bit per pair, and both match truth."""
+    _print_case(t="gather_sorted", M=M)
+    E, N, K, T, topk = 8, 64, 256, 40, 3
+    wq, s, b = weights(E, N, K, 4, 64, 77)
+    rng = np.random.default_rng(5)
+    flat = rng.integers(0, E, size=T * topk).astype(np.uint32)
+    order, inv, srt, lhs = O.sort_dispatch(flat, topk)
+    x = O.make_x_bf16(T * M, K, 78).reshape(T, M, K)
+    Wd, Sd, Bd = to_dev_u32(wq, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev)
+    xd = to_dev_bf16(x, dev)
+    ys = mi_qmm.gather_qmm(xd, Wd, Sd, Bd, lhs_indices=to_dev_u32(lhs, dev),
+                           rhs_indices=to_dev_u32(srt, dev), group_size=64, bits=4,
+                           sorted_indices=True)
+    yu = mi_qmm.gather_qmm(xd, Wd, Sd, Bd, lhs_indices=to_dev_u32(lhs, dev),
+                           rhs_indices=to_dev_u32(srt, dev), group_size=64, bits=4,
+                           sorted_indices=False)
+    truth = O.gather_qmm_f64(x, wq, s, b, lhs, srt, T * topk)
+    assert max_err_ratio(to_f64(ys), truth) <= BF16_TOL
+    assert max_err_ratio(to_f64(yu), truth) <= BF16_TOL
+    # permuting back gives the per-(token, slot) result
+    back = to_f64(ys)[inv]
+    t2 = O.gather_qmm_f64(x, wq, s, b, None, flat, T * topk, lhs_div=topk)
+    assert max_err_ratio(back, t2) <= BF16_TOL
+
+
+def test_gather_out_of_range_is_nan(dev):
+    _print_case(t="gather_oob")
+    E, N, K = 4, 32, 128
+    wq, s, b = weights(E, N, K, 4, 64, 90)
+    x = O.make_x_bf16(3, K, 91).reshape(3, 1, K)
+    rhs = np.array([0, 9, 2], np.uint32)
+    lhs = np.array([0, 1, 7], np.uint32)
+    y = mi_qmm.gather_qmm(to_dev_bf16(x, dev), to_dev_u32(wq, dev), to_dev_bf16(s, dev),
+                          to_dev_bf16(b, dev), lhs_indices=to_dev_u32(lhs, dev),
+                          rhs_indices=to_dev_u32(rhs, dev), group_size=64, bits=4)
+    yf = to_f64(y)
+    assert np.isnan(yf[1]).all() and np.isnan(yf[2]).all()
+    truth = O.gather_qmm_f64(x, wq, s, b, lhs[:1], rhs[:1], 1)
+    assert max_err_ratio(yf[:1], truth) <= BF16_TOL
+
+
+def test_deterministic(dev):
+    _print_case(t="determinism")
+    wq, s, b = weights(1, 512, 4096, 4, 64, 99)
+    x = to_dev_bf16(O.make_x_bf16(1, 4096, 98), dev)
+    args = (to_dev_u32(wq[0], dev), to_dev_bf16(s[0], dev), to_dev_bf16(b[0], dev))
+    y0 = bf16_bits(mi_qmm.quantized_matmul(x, *args))
+    for _ in range(3):
+        assert np.array_equal(bf16_bits(mi_qmm.quantized_matmul(x, *args)), y0)
+
+
+def test_fill_randn_matches_oracle_stream(dev):
+    _print_case(t="randn")
+    t = torch.empty(4097, dtype=torch.float32, device=dev)
+    mi_qmm.fill_randn(t, 1234, 0.0, 1.0)
+    ref = O.randn(4097, 1234)
+    got = t.cpu().numpy()
+    assert np.max(np.abs(got - ref)) <= 1e-6
