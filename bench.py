@@ -1,0 +1,195 @@
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+Headline (the `value`): configs[1] of BASELINE.json at M=1, 4-bit g64 -- decode over
+32 distinct Llama-3-8B MLP layers (gate, up [14336,4096] and down [4096,14336]),
+one step = the 96 qmv launches of one token. value = algorithmic HBM bytes moved
+per second (TB/s), weights resident in HBM, synthetic data from the library's
+generator. The JSON line also carries the roofline of the dominant kernel, the
+timed CPU baseline (the C oracle, not MLX) and the secondary configs.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--full]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mlx-serve_amd"))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+SEED_BASE = 0x4D49333500000000
+
+
+def seed(cfg, stream, extra=0):
+    return (SEED_BASE + 16 * cfg + stream + (extra << 20)) & ((1 << 64) - 1)
+
+
+def qbytes(N, K, bits, gs, M):
+    """Algorithmic bytes of one qmm call: packed W + bf16 scales/biases + x + y."""
+    return N * K * bits // 8 + 2 * (N * K // gs) * 2 + M * K * 2 + M * N * 2
+
+
+def make_layer_weights(torch, mi, N, K, bits, gs, sd, tmp):
+    w = tmp[: N * K].view(N, K)
+    mi.fill_randn(w, sd, 0.0, 0.02)
+    return mi.quantize(w, gs, bits)
+
+
+def build_mlp_layers(torch, mi, n_layers, bits, gs, dev, hidden=4096, inter=14336, cfg=2):
+    tmp = torch.empty(hidden * inter, dtype=torch.bfloat16, device=dev)
+    layers = []
+    for l in range(n_layers):
+        g = make_layer_weights(torch, mi, inter, hidden, bits, gs, seed(cfg, 1, 3 * l), tmp)
+        u = make_layer_weights(torch, mi, inter, hidden, bits, gs, seed(cfg, 1, 3 * l + 1), tmp)
+        d = make_layer_weights(torch, mi, hidden, inter, bits, gs, seed(cfg, 1, 3 * l + 2), tmp)
+        layers.append((g, u, d))
+    del tmp
+    torch.cuda.synchronize()
+    return layers
+
+
+def time_region(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / 1000.0
+
+
+def decode_mlp(torch, mi, layers, M, bits, gs, dev, steps, warmup, hidden=4096, inter=14336):
+    x = torch.empty(M, hidden, dtype=torch.bfloat16, device=dev)
+    h = torch.empty(M, inter, dtype=torch.bfloat16, device=dev)
+    mi.fill_randn(x, seed(2, 0), 0.0, 1.0)
+    mi.fill_randn(h, seed(2, 0, 1), 0.0, 1.0)
+
+    def step():
+        for (g, u, d) in layers:
+            mi.quantized_matmul(x, *g, True, gs, bits)
+            mi.quantized_matmul(x, *u, True, gs, bits)
+            mi.quantized_matmul(h, *d, True, gs, bits)
+
+    # The 96 launches of one token are captured once in a HIP graph and replayed, so
+    # the timed region measures the GPU, not Python's per-call launch overhead.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    t = time_region(torch, graph.replay, steps, warmup)
+    launches = 3 * len(layers) * steps
+    per_launch = qbytes(inter, hidden, bits, gs, M)  # gate/up/down move the same bytes
+    return {"seconds": t, "launches": launches, "bytes_per_launch": per_launch,
+            "avg_launch_us": t / launches * 1e6,
+            "GBs": per_launch * launches / t / 1e9,
+            "tokens_per_s": M * steps / t}
+
+
+def cpu_baseline(torch, layers, bits, gs, hidden=4096, inter=14336, budget_s=10.0):
+    """Time the C oracle's fp32 qmv (a C restatement of MLX CPU semantics, not MLX)
+    on host cores over a bounded sample: the first layers' weights copied to host."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as O
+    threads = min(16, os.cpu_count() or 1)
+    n_l = min(2, len(layers))
+    host = []
+    for (g, u, d) in layers[:n_l]:
+        host.append([tuple(t.cpu().view(torch.int16 if t.element_size() == 2 else torch.int32)
+                           .numpy() for t in m) for m in (g, u, d)])
+    host = [[(wq.view(np.uint32), s.view(np.uint16), b.view(np.uint16)) for (wq, s, b) in L]
+            for L in host]
+    x = O.make_x_bf16(1, hidden, seed(2, 0))
+    h = O.make_x_bf16(1, inter, seed(2, 0, 1))
+    O.qmm_f32(x, *host[0][0], gs, bits, threads)  # warm
+    done, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        for L in host:
+            O.qmm_f32(x, *L[0], gs, bits, threads)
+            O.qmm_f32(x, *L[1], gs, bits, threads)
+            O.qmm_f32(h, *L[2], gs, bits, threads)
+            done += 3
+    t = time.perf_counter() - t0
+    per = qbytes(inter, hidden, bits, gs, 1)
+    return {"value": per * done / t / 1e12, "unit": "TB/s", "cores": threads, "kind": "port",
+            "sample": f"{done} qmv calls (M=1, 4-bit g64, Llama-3-8B MLP shapes) over the first "
+                      f"{n_l} layers' weights, {t:.1f} s, C oracle mo_qmm_f32 with OpenMP"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build's path runs on a single MI355X "
+              "(multi-GPU sharding is a design note, not a measured configuration).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import mi_qmm as mi
+    dev = torch.device("cuda:0")
+    bits, gs = 4, 64
+    layers = build_mlp_layers(torch, mi, args.layers, bits, gs, dev)
+    head = decode_mlp(torch, mi, layers, 1, bits, gs, dev, args.steps, args.warmup)
+
+    extra = {}
+    if not args.no_extra:
+        for M in (2, 4, 8, 16, 32):
+            r = decode_mlp(torch, mi, layers, M, bits, gs, dev, max(5, args.steps // 5), 2)
+            extra[f"q4_M{M}_GBs"] = round(r["GBs"], 1)
+            extra[f"q4_M{M}_tok_s"] = round(r["tokens_per_s"], 1)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(torch, layers, bits, gs, budget_s=args.cpu_seconds)
+
+    ms_per_step = head["seconds"] / args.steps * 1e3
+    achieved = head["bytes_per_launch"] / (head["avg_launch_us"] * 1e-6) / 1e9
+    out = {
+        "metric": "4-bit qmv/gather_qmm HBM TB/s (% of peak) at M=1; prefill qmm TFLOP/s",
+        "value": round(head["GBs"] / 1000.0, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4 weights, bf16 activations, fp32 accumulate",
+        "data": "synthetic (counter-based SplitMix64 normal, quantized on device)",
+        "config": {"workload": "configs[1]: Llama-3-8B MLP decode, 32 distinct layers "
+                               "(gate/up [14336,4096], down [4096,14336]), 4-bit g64, M=1",
+                   "global_batch": 1, "layers": args.layers, "pct_of_hbm_peak":
+                   round(100.0 * head["GBs"] / HBM_PEAK_GBS, 2),
+                   "tokens_per_s": round(head["tokens_per_s"], 1)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "qmv_kernel<4,64,1,1,*,false>",
+                     "bytes_per_launch": head["bytes_per_launch"],
+                     "avg_launch_us": round(head["avg_launch_us"], 3)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -34,6 +34,7 @@ enum {
   MI_ERR_UNSUPPORTED = 1, /* decline: valid request outside this library's scope */
   MI_ERR_INVALID = 2,     /* bad pointer / shape / argument */
   MI_ERR_HIP = 3,         /* HIP runtime error (launch, allocation) */
+  MI_ERR_WORKSPACE = 4,   /* workspace must grow but the stream is capturing */
 };
 
 /* Values match mlx_dtype (src/mlx.zig:20-35). */
@@ -70,7 +71,8 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
  * Indices are uint32 device arrays. sorted_indices=true groups consecutive equal
  * rhs values into one weight pass per run (any order stays correct; sorted order
  * is what makes it fast). Out-of-range indices write NaN rows, never read out of
- * bounds. Uses a per-stream device workspace when sorted_indices=true. */
+* bounds. Uses the per-device workspace (mi_workspace_reserve) for sorted work lists
+ * and split-K partials. */
 int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
                   const void* biases, const uint32_t* lhs_indices, const uint32_t* rhs_indices,
                   int64_t n_idx, int64_t lhs_div, int64_t x_batch, int64_t M, int64_t N, int64_t K,
@@ -112,6 +114,11 @@ int mi_affine_params_from_geometry(int64_t w_cols, int64_t s_cols, int64_t in_di
  * counter-based SplitMix64 + Box-Muller stream keyed by seed. */
 int mi_fill_randn(void* out, int64_t n, uint64_t seed, float mean, float stddev, int dtype,
                   void* stream);
+
+/* Grow the per-device workspace (sorted work lists, K-split partials) to at least
+ * `bytes` ahead of HIP graph capture; calls that fit never allocate. No mlx-c
+ * counterpart (MLX owns its allocator). Synchronizes the device when it grows. */
+int mi_workspace_reserve(int64_t bytes, void* stream);
 
 /* Thread-local text of the last non-zero return on this thread ("" if none). */
 const char* mi_last_error(void);

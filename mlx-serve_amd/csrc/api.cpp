@@ -52,62 +52,82 @@ int resolve_common(mi_optional_int gs_in, mi_optional_int bits_in, const char* m
   return MI_OK;
 }
 
-// Per (device, stream) device workspace, grown on demand. Calls on one stream are
-// ordered, so a buffer reused by later calls on the same stream is safe.
+// Per-device scratch for sorted work lists and K-split partials. Calls on one
+// stream are ordered, so reuse by later calls is safe; calls that overlap on
+// different streams of one device must not both use it. It only grows outside
+// stream capture (mi_workspace_reserve sizes it up front).
 struct Workspace {
-  void* ptr = nullptr;
+  void* data = nullptr;
   size_t size = 0;
 };
 std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+std::map<int, Workspace> g_ws;
 
-int workspace(hipStream_t s, size_t bytes, void** out) {
+int workspace(hipStream_t s, size_t bytes, void** data) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   std::lock_guard<std::mutex> lk(g_ws_mu);
-  Workspace& w = g_ws[{dev, s}];
+  Workspace& w = g_ws[dev];
   if (w.size < bytes) {
-    if (w.ptr) {
-      e = hipStreamSynchronize(s);  // the old buffer may still be read by queued work
-      if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-      (void)hipFree(w.ptr);
-      w.ptr = nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return fail(MI_ERR_WORKSPACE, "workspace too small during stream capture "
+                  "(call mi_workspace_reserve before capturing)");
+    if (w.data) {
+      e = hipDeviceSynchronize();  // queued work may still use the old buffer
+      if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+      (void)hipFree(w.data);
+      w.data = nullptr;
       w.size = 0;
     }
-    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-    e = hipMalloc(&w.ptr, want);
+    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes + bytes / 4;
+    e = hipMalloc(&w.data, want);
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
     w.size = want;
   }
-  *out = w.ptr;
+  *data = w.data;
   return MI_OK;
 }
 
 int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
-// Launch shape for the small-M kernel: enough row tiles per wave to amortise the
-// activation fragments, enough waves (split-K) to keep ~16 waves per CU in flight.
-mi::QmvConfig qmv_config(int N, int K, int gs, int rows, int64_t n_items, int x_f32) {
-  mi::QmvConfig c;
-  c.rows = rows;
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v ? atoi(v) : dflt;
+}
+
+// Launch shape for the small-M kernel: one block per (32-row tile, K range, item).
+// K ranges: as few as keep the staged activations within the LDS budget. Waves per
+// block: enough to keep ~16 waves per CU streaming, at least 2 groups per wave.
+struct QmvPlan {
+  mi::QmvConfig cfg;
+  int row_blocks, ks, gps;
+};
+
+QmvPlan qmv_plan(int N, int K, int gs, int rows, int64_t n_items, int x_f32) {
+  static const int env_w = env_int("MI_QMM_QMV_WAVES", 0);
+  static const int env_ks = env_int("MI_QMM_QMV_KS", 0);
+  static const int env_target = env_int("MI_QMM_QMV_TARGET_WAVES", 4096);
+  const size_t lds_max = 64 * 1024;
+  QmvPlan p;
+  p.cfg.rows = rows;
+  p.cfg.grid_z = (int)(n_items < 65535 ? n_items : 65535);
+  p.row_blocks = ceil_div(N, 32);
   const int G = K / gs;
-  const int64_t items = n_items < 65535 ? n_items : 65535;
-  int rt = 4;
-  while (rt > 1 && (int64_t)ceil_div(N, 16 * rt) * items < 1024) rt >>= 1;
-  c.rt = rt;
-  c.row_groups = ceil_div(N, 16 * rt);
-  c.grid_y = (int)items;
-  const int64_t blocks = (int64_t)c.row_groups * items;
-  int w = 1;
-  while (w < 8 && blocks * w < 4096 && G / (2 * w) >= 2) w <<= 1;
-  const int mt = rows > 16 ? 2 : 1;
-  const int r4 = rows <= 1 ? 1 : rows <= 2 ? 2 : 4;
-  const int slots = rt * mt * r4;
-  while (w > 1 && (size_t)w * slots * 64 * 4 > 64 * 1024) w >>= 1;
-  (void)x_f32;
-  c.waves = w;
-  return c;
+  const int mr = mi::qmv_mr_for_rows(rows);
+  int ks = 1;
+  while (ks < G && mi::qmv_lds_bytes(ceil_div(G, ks), gs, mr, x_f32, 1) > lds_max) ++ks;
+  if (env_ks > 0) ks = env_ks < G ? env_ks : G;
+  p.gps = ceil_div(G, ks);
+  p.ks = ceil_div(G, p.gps);
+  const int64_t blocks = (int64_t)p.row_blocks * p.cfg.grid_z * p.ks;
+  int w = 4;
+  while (w < 8 && blocks * w < env_target && p.gps / (2 * w) >= 1) w <<= 1;
+  if (env_w >= 1 && env_w <= 8) w = env_w;
+  while (w > 1 && mi::qmv_lds_bytes(p.gps, gs, mr, x_f32, w) > lds_max) w >>= 1;
+  p.cfg.waves = w;
+  return p;
 }
 
 bool valid_x_dtype(int d) { return d == MI_DTYPE_BFLOAT16 || d == MI_DTYPE_FLOAT32; }
@@ -117,6 +137,12 @@ bool valid_x_dtype(int d) { return d == MI_DTYPE_BFLOAT16 || d == MI_DTYPE_FLOAT
 extern "C" {
 
 const char* mi_last_error(void) { return g_err.c_str(); }
+
+int mi_workspace_reserve(int64_t bytes, void* stream) {
+  if (bytes < 0) return fail(MI_ERR_INVALID, "negative size");
+  void* d = nullptr;
+  return workspace((hipStream_t)stream, (size_t)bytes, &d);
+}
 
 const char* mi_version(void) { return "mi_qmm 0.1 gfx950"; }
 
@@ -178,38 +204,45 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
   P.x_f32 = x_dtype == MI_DTYPE_FLOAT32;
 
   const bool use_items = sorted_indices && rhs_indices != nullptr && n_idx > 1;
+  const int64_t PT = n_idx * M;
+  const int rows = M <= 32 ? (int)M : 32;
+  int64_t n_items, max_items = 0;
   if (!use_items) {
-    const int rows = M <= 32 ? (int)M : 32;
-    P.rows_per_item = rows <= 16 ? 16 : 32;
-    P.items_per_pair = ceil_div(M, P.rows_per_item);
-    const int64_t n_items = n_idx * P.items_per_pair;
+    P.items_per_pair = ceil_div(M, 32);
+    n_items = n_idx * P.items_per_pair;
     if (n_items > INT32_MAX) return fail(MI_ERR_INVALID, "too many work items");
     P.n_items_fixed = (int)n_items;
-    mi::QmvConfig c = qmv_config(P.N, P.K, gs, rows, n_items, P.x_f32);
-    hipError_t e = mi::launch_qmv(P, c, s);
-    return e == hipSuccess ? MI_OK : hip_fail(e, "qmv launch");
+  } else {
+    // Runs of equal rhs, cut into 32-row chunks; bound valid for any input order.
+    max_items = (PT + 31) / 32 + n_idx;
+    const int64_t runs_bound = n_idx < n_experts ? n_idx : n_experts;
+    n_items = (PT + 31) / 32 + runs_bound;
+    P.items_per_pair = 1;
+    P.n_items_fixed = 0;
   }
-
-  // Sorted: build (expert run, 32-row chunk) work items on the device.
-  P.rows_per_item = 32;
-  const int64_t total = n_idx * M;
-  const int64_t runs_bound = n_idx < n_experts ? n_idx : n_experts;
-  const int64_t max_items = (total + 31) / 32 + n_idx;  // any input order fits
-  void* ws = nullptr;
-  rc = workspace(s, (size_t)max_items * 16 + 256, &ws);
-  if (rc) return rc;
-  uint32_t* count = (uint32_t*)ws;
-  uint32_t* items = (uint32_t*)((char*)ws + 256);
-  hipError_t e = mi::launch_build_items(rhs_indices, n_idx, (int)M, 32, items, count, max_items, s);
-  if (e != hipSuccess) return hip_fail(e, "build_items launch");
-  P.items = items;
-  P.item_count = count;
-  P.items_per_pair = 1;
-  P.n_items_fixed = 0;
-  const int64_t expect_items = (total + 31) / 32 + runs_bound;
-  mi::QmvConfig c = qmv_config(P.N, P.K, gs, 32, expect_items, P.x_f32);
-  e = mi::launch_qmv(P, c, s);
-  return e == hipSuccess ? MI_OK : hip_fail(e, "gather qmv launch");
+  QmvPlan plan = qmv_plan(P.N, P.K, gs, use_items ? 32 : rows, n_items, P.x_f32);
+  P.ks = plan.ks;
+  P.gps = plan.gps;
+  P.row_blocks = plan.row_blocks;
+  size_t items_bytes = use_items ? (size_t)max_items * 16 + 256 : 0;
+  size_t part_bytes = P.ks > 1 ? (size_t)P.ks * PT * N * 4 : 0;
+  if (items_bytes || part_bytes) {
+    void* data = nullptr;
+    rc = workspace(s, ((items_bytes + 255) / 256) * 256 + part_bytes, &data);
+    if (rc) return rc;
+    P.part = (float*)((char*)data + ((items_bytes + 255) / 256) * 256);
+    if (use_items) {
+      uint32_t* count = (uint32_t*)data;
+      uint32_t* items = (uint32_t*)((char*)data + 256);
+      hipError_t e = mi::launch_build_items(rhs_indices, n_idx, (int)M, 32, items, count,
+                                            max_items, s);
+      if (e != hipSuccess) return hip_fail(e, "build_items launch");
+      P.items = items;
+      P.item_count = count;
+    }
+  }
+  hipError_t e = mi::launch_qmv(P, plan.cfg, s);
+  return e == hipSuccess ? MI_OK : hip_fail(e, "qmv launch");
 }
 
 int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,

@@ -16,22 +16,25 @@ struct QmvParams {
   const uint32_t* rhs;     // nullable: rhs(i) = i
   const uint32_t* items;   // nullable: sorted work list, 4 u32 per item (expert, pos0, cnt, 0)
   const uint32_t* item_count;  // device count for `items`
+  float* part;             // ks > 1: fp32 partials [ks][n_pairs*M][N] (summed by a 2nd kernel)
   int64_t n_pairs, lhs_div, x_batch, n_experts;
   int M, N, K;
   int bits, group_size, x_f32;
-  int rows_per_item;   // 16*MT rows covered per item
-  int items_per_pair;  // unsorted: ceil(M / rows_per_item)
+  int items_per_pair;  // unsorted: ceil(M / 32)
   int n_items_fixed;   // unsorted: n_pairs * items_per_pair
+  int ks;              // K splits (grid.y)
+  int gps;             // quantization groups per K split
+  int row_blocks;      // grid.x: ceil(N / 32)
 };
 
 struct QmvConfig {
-  int row_groups;  // grid.x: ceil(N / (16*rt))
-  int grid_y;      // grid.y (items, capped; the kernel strides over the rest)
-  int waves;       // waves per block = split-K factor
-  int rt;          // 16-row weight tiles per wave
-  int rows;        // max activation rows per item (selects MT/R4)
+  int grid_z;  // items in the grid (capped; the kernel strides over the rest)
+  int waves;   // waves per block (split the block's K range)
+  int rows;    // max activation rows per item (<= 32; selects the template)
 };
 
+int qmv_mr_for_rows(int rows);
+size_t qmv_lds_bytes(int groups, int gs, int mr, int x_f32, int waves);
 hipError_t launch_qmv(const QmvParams& P, const QmvConfig& C, hipStream_t s);
 
 // Sorted gather: runs of equal rhs -> work items (moe.hip / segments.hip).
