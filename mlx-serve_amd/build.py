@@ -14,7 +14,7 @@ OUT_DIR = os.path.join(HERE, "mi_qmm")
 LIB = os.path.join(OUT_DIR, "libmi_qmm.so")
 BUILD = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["qmv.hip", "qmm.hip", "quant.hip", "moe.hip", "api.cpp"]
+SOURCES = ["qmv.hip", "qmv16.hip", "qmm.hip", "quant.hip", "moe.hip", "api.cpp"]
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I", os.path.join(HERE, "..", "include")]

@@ -1,6 +1,6 @@
 // C ABI (include/mi_qmm.h): argument validation, dispatch to the gfx950 kernels,
 // per-stream workspace, error reporting.
-#include "../../include/mi_qmm.h"
+#include "mi_qmm.h"
 
 #include <hip/hip_runtime.h>
 
@@ -98,35 +98,94 @@ int env_int(const char* name, int dflt) {
 }
 
 // Launch shape for the small-M kernel: one block per (32-row tile, K range, item).
-// K ranges: as few as keep the staged activations within the LDS budget. Waves per
-// block: enough to keep ~16 waves per CU streaming, at least 2 groups per wave.
+// A wave holds at most UG groups of one tile in registers, a block at most 8 waves,
+// and the staged activations must fit the LDS budget; K ranges are the fewest that
+// satisfy both. Waves per block: enough for ~16 resident waves per CU.
 struct QmvPlan {
   mi::QmvConfig cfg;
   int row_blocks, ks, gps;
 };
 
-QmvPlan qmv_plan(int N, int K, int gs, int rows, int64_t n_items, int x_f32) {
+size_t lds_per_block() {
+  static size_t cached = 0;
+  if (!cached) {
+    int v = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+        v <= 0)
+      v = 64 * 1024;
+    cached = (size_t)v;
+  }
+  return cached;
+}
+
+QmvPlan qmv_plan(int N, int K, int gs, int bits, int rows, int64_t n_items, int x_f32) {
   static const int env_w = env_int("MI_QMM_QMV_WAVES", 0);
   static const int env_ks = env_int("MI_QMM_QMV_KS", 0);
-  static const int env_target = env_int("MI_QMM_QMV_TARGET_WAVES", 4096);
-  const size_t lds_max = 64 * 1024;
+  static const int env_units = env_int("MI_QMM_QMV_UNITS", 2048);
+  const size_t lds_max = lds_per_block() - 512;  // static row table headroom
   QmvPlan p;
   p.cfg.rows = rows;
   p.cfg.grid_z = (int)(n_items < 65535 ? n_items : 65535);
-  p.row_blocks = ceil_div(N, 32);
+  const int tiles = ceil_div(N, 32);
   const int G = K / gs;
+  const int ug = mi::qmv_groups_per_wave(bits, gs);
   const int mr = mi::qmv_mr_for_rows(rows);
+  const int nch = ceil_div(G, ug);  // 256-byte chunks per row
+  int w = (env_w >= 1 && env_w <= mi::kQmvMaxWaves) ? env_w : mi::kQmvMaxWaves;
+  if (w > tiles) w = tiles;
+  // K ranges: enough (wave, tile, range) units to fill the GPU, each >= 1 chunk,
+  // and the staged activations of a range within the LDS budget.
+  int ks = (int)((env_units + (int64_t)tiles * p.cfg.grid_z - 1) / ((int64_t)tiles * p.cfg.grid_z));
+  if (ks > nch) ks = nch;
+  if (ks < 1) ks = 1;
+  if (env_ks > 0) ks = env_ks < nch ? env_ks : nch;
+  for (;;) {
+    const int gps = ceil_div(G, ks);
+    if (mi::qmv_lds_bytes(gps, gs, mr, x_f32, w) <= lds_max || ks >= G) break;
+    ++ks;
+  }
+  // Whole chunks per range keep every wave's DMA aligned to 256-byte rows.
+  p.gps = ceil_div(ceil_div(G, ks), ug) * ug;
+  if (p.gps > G) p.gps = G;
+  p.ks = ceil_div(G, p.gps);
+  p.cfg.waves = w;
+  p.row_blocks = ceil_div(tiles, w);
+  return p;
+}
+
+// Launch shape for the 16-row-tile decode kernel: one block per (tile, item) with
+// the waves splitting K; 8 waves per block when the tiles alone give < 512 blocks.
+// K splits across blocks only when the staged activations exceed the LDS budget.
+QmvPlan qmv16_plan(int N, int K, int gs, int bits, int rows, int64_t n_items, int x_f32) {
+  static const int env_w = env_int("MI_QMM_QMV_WAVES", 0);
+  const size_t lds_max = lds_per_block() - 512;
+  QmvPlan p;
+  p.cfg.rows = rows;
+  p.cfg.grid_z = (int)(n_items < 65535 ? n_items : 65535);
+  const int tiles = ceil_div(N, 16);
+  const int G = K / gs;
+  const int ug = mi::qmv16_groups_per_chunk(bits, gs);
+  const int mp = mi::qmv16_mp_for_rows(rows);
+  const int nch = ceil_div(G, ug);
+  int w = (int64_t)tiles * p.cfg.grid_z >= 512 ? 4 : 8;
+  if (env_w >= 1 && env_w <= 8) w = env_w;
+  if (w > nch) w = nch;
   int ks = 1;
-  while (ks < G && mi::qmv_lds_bytes(ceil_div(G, ks), gs, mr, x_f32, 1) > lds_max) ++ks;
-  if (env_ks > 0) ks = env_ks < G ? env_ks : G;
+  for (;;) {
+    const int gps = ceil_div(G, ks);
+    if (mi::qmv16_lds_bytes(gps, gs, mp, x_f32, w) <= lds_max) break;
+    if (w > 1) {
+      w >>= 1;
+      continue;
+    }
+    if (ks >= G) break;
+    ++ks;
+  }
   p.gps = ceil_div(G, ks);
   p.ks = ceil_div(G, p.gps);
-  const int64_t blocks = (int64_t)p.row_blocks * p.cfg.grid_z * p.ks;
-  int w = 4;
-  while (w < 8 && blocks * w < env_target && p.gps / (2 * w) >= 1) w <<= 1;
-  if (env_w >= 1 && env_w <= 8) w = env_w;
-  while (w > 1 && mi::qmv_lds_bytes(p.gps, gs, mr, x_f32, w) > lds_max) w >>= 1;
   p.cfg.waves = w;
+  p.row_blocks = tiles;
   return p;
 }
 
@@ -205,22 +264,27 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
 
   const bool use_items = sorted_indices && rhs_indices != nullptr && n_idx > 1;
   const int64_t PT = n_idx * M;
-  const int rows = M <= 32 ? (int)M : 32;
+  // Decode widths (<= 16 rows per pair, or sorted runs cut into 16-row items) use the
+  // 16-row-tile kernel; 17..32 rows per pair use the 32-row-tile kernel.
+  const bool narrow = use_items ? true : M <= 16;
+  P.rpi = narrow ? 16 : 32;
+  const int rows = (int)(M < P.rpi ? M : P.rpi);
   int64_t n_items, max_items = 0;
   if (!use_items) {
-    P.items_per_pair = ceil_div(M, 32);
+    P.items_per_pair = ceil_div(M, P.rpi);
     n_items = n_idx * P.items_per_pair;
     if (n_items > INT32_MAX) return fail(MI_ERR_INVALID, "too many work items");
     P.n_items_fixed = (int)n_items;
   } else {
-    // Runs of equal rhs, cut into 32-row chunks; bound valid for any input order.
-    max_items = (PT + 31) / 32 + n_idx;
+    // Runs of equal rhs cut into rpi-row chunks; the bound holds for any input order.
+    max_items = (PT + P.rpi - 1) / P.rpi + n_idx;
     const int64_t runs_bound = n_idx < n_experts ? n_idx : n_experts;
-    n_items = (PT + 31) / 32 + runs_bound;
+    n_items = (PT + P.rpi - 1) / P.rpi + runs_bound;
     P.items_per_pair = 1;
     P.n_items_fixed = 0;
   }
-  QmvPlan plan = qmv_plan(P.N, P.K, gs, use_items ? 32 : rows, n_items, P.x_f32);
+  QmvPlan plan = narrow ? qmv16_plan(P.N, P.K, gs, nb, use_items ? P.rpi : rows, n_items, P.x_f32)
+                        : qmv_plan(P.N, P.K, gs, nb, rows, n_items, P.x_f32);
   P.ks = plan.ks;
   P.gps = plan.gps;
   P.row_blocks = plan.row_blocks;
@@ -234,14 +298,14 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
     if (use_items) {
       uint32_t* count = (uint32_t*)data;
       uint32_t* items = (uint32_t*)((char*)data + 256);
-      hipError_t e = mi::launch_build_items(rhs_indices, n_idx, (int)M, 32, items, count,
+      hipError_t e = mi::launch_build_items(rhs_indices, n_idx, (int)M, P.rpi, items, count,
                                             max_items, s);
       if (e != hipSuccess) return hip_fail(e, "build_items launch");
       P.items = items;
       P.item_count = count;
     }
   }
-  hipError_t e = mi::launch_qmv(P, plan.cfg, s);
+  hipError_t e = narrow ? mi::launch_qmv16(P, plan.cfg, s) : mi::launch_qmv(P, plan.cfg, s);
   return e == hipSuccess ? MI_OK : hip_fail(e, "qmv launch");
 }
 

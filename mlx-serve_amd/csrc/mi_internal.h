@@ -20,7 +20,8 @@ struct QmvParams {
   int64_t n_pairs, lhs_div, x_batch, n_experts;
   int M, N, K;
   int bits, group_size, x_f32;
-  int items_per_pair;  // unsorted: ceil(M / 32)
+  int rpi;             // rows per work item (32: qmv, 16: qmv16)
+  int items_per_pair;  // unsorted: ceil(M / rpi)
   int n_items_fixed;   // unsorted: n_pairs * items_per_pair
   int ks;              // K splits (grid.y)
   int gps;             // quantization groups per K split
@@ -33,9 +34,18 @@ struct QmvConfig {
   int rows;    // max activation rows per item (<= 32; selects the template)
 };
 
+constexpr int kQmvMaxWaves = 4;  // waves per qmv block (weight-slice LDS is static)
 int qmv_mr_for_rows(int rows);
+int qmv_groups_per_wave(int bits, int gs);
 size_t qmv_lds_bytes(int groups, int gs, int mr, int x_f32, int waves);
 hipError_t launch_qmv(const QmvParams& P, const QmvConfig& C, hipStream_t s);
+hipError_t launch_reduce_splits(const QmvParams& P, hipStream_t s);
+
+// Decode-width kernel (qmv16.hip): M <= 16 rows per item, 16-row weight tiles.
+int qmv16_mp_for_rows(int rows);
+int qmv16_groups_per_chunk(int bits, int gs);
+size_t qmv16_lds_bytes(int groups, int gs, int mp, int x_f32, int waves);
+hipError_t launch_qmv16(const QmvParams& P, const QmvConfig& C, hipStream_t s);
 
 // Sorted gather: runs of equal rhs -> work items (moe.hip / segments.hip).
 hipError_t launch_build_items(const uint32_t* rhs, int64_t n_pairs, int M, int rows_per_item,

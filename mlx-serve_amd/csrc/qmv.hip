@@ -22,132 +22,39 @@
 // summed through LDS in wave order. K ranges beyond one per block (activations too
 // large for LDS) are summed by a second, elementwise kernel in range order. Every
 // sum has a fixed order, so results are deterministic.
-#include "mi_common.h"
-#include "mi_internal.h"
+#include "qmv_common.h"
 
-// Packed words per lane per load chunk (one chunk is in flight while one computes).
-#ifndef MI_QMV_CW
-#define MI_QMV_CW 32
-#endif
 
 namespace mi {
 
 namespace {
 
-typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+using namespace qmv_detail;
 
-MI_DEV f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v, a),
-                                                  __builtin_bit_cast(bf16x8v, b), c, 0, 0, 0);
-}
-
-template <int N>
-MI_DEV void load_u32(const uint32_t* __restrict__ p, uint32_t (&out)[N]) {
-  if constexpr (N == 2) {
-    u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
-    out[0] = v.x; out[1] = v.y;
-  } else {
-#pragma unroll
-    for (int i = 0; i < N / 4; ++i) {
-      u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p) + i);
-      out[4 * i] = v.x; out[4 * i + 1] = v.y; out[4 * i + 2] = v.z; out[4 * i + 3] = v.w;
-    }
-  }
-}
-
-// 4-bit unpack: lo = w & 0x0F0F0F0F holds nibbles 0,2,4,6 in its bytes, hi the odd
-// ones; v_perm pairs each nibble byte with a 0x43 byte, giving bf16 0x43qq = 128+q.
-// Fragment k order is therefore [0,2,4,6,1,3,5,7]; activations are permuted to match.
-template <int BITS>
-MI_DEV u32x4_t a_perm(u32x4_t X) {
-  if constexpr (BITS == 4) {
-    return u32x4_t{perm_b32(X.y, X.x, 0x05040100u), perm_b32(X.w, X.z, 0x05040100u),
-                   perm_b32(X.y, X.x, 0x07060302u), perm_b32(X.w, X.z, 0x07060302u)};
-  } else {
-    return X;
-  }
-}
-
-// B fragment (8 k values of one weight row) for MFMA step j of a lane's words.
-template <int BITS>
-MI_DEV u32x4_t b_frag(const uint32_t* words, int j, uint32_t c43) {
-  if constexpr (BITS == 4) {
-    const uint32_t w = words[j];
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-    return u32x4_t{perm_b32(c43, lo, 0x04010400u), perm_b32(c43, lo, 0x04030402u),
-                   perm_b32(c43, hi, 0x04010400u), perm_b32(c43, hi, 0x04030402u)};
-  } else {
-    const uint32_t w0 = words[2 * j], w1 = words[2 * j + 1];
-    // Bytes are exact in bf16: the fp32 value's upper half is the bf16 value.
-    const uint32_t f0 = __float_as_uint((float)(w0 & 0xFFu));
-    const uint32_t f1 = __float_as_uint((float)((w0 >> 8) & 0xFFu));
-    const uint32_t f2 = __float_as_uint((float)((w0 >> 16) & 0xFFu));
-    const uint32_t f3 = __float_as_uint((float)(w0 >> 24));
-    const uint32_t f4 = __float_as_uint((float)(w1 & 0xFFu));
-    const uint32_t f5 = __float_as_uint((float)((w1 >> 8) & 0xFFu));
-    const uint32_t f6 = __float_as_uint((float)((w1 >> 16) & 0xFFu));
-    const uint32_t f7 = __float_as_uint((float)(w1 >> 24));
-    return u32x4_t{perm_b32(f1, f0, 0x07060302u), perm_b32(f3, f2, 0x07060302u),
-                   perm_b32(f5, f4, 0x07060302u), perm_b32(f7, f6, 0x07060302u)};
-  }
-}
-
-struct Item {
-  int64_t pos0;  // first flattened (pair, m) position
-  int cnt;       // positions in this item (<= 32)
-  uint32_t expert;
-  bool expert_ok;
-};
-
-MI_DEV Item decode_item(const QmvParams& P, int it) {
-  Item r;
-  if (P.items) {
-    const uint32_t* e = P.items + 4 * (int64_t)it;
-    r.expert = e[0];
-    r.pos0 = (int64_t)e[1];
-    r.cnt = (int)e[2];
-  } else {
-    const int64_t pair = it / P.items_per_pair;
-    const int c = it - (int)(pair * P.items_per_pair);
-    r.pos0 = pair * P.M + (int64_t)c * 32;
-    r.cnt = min(32, P.M - c * 32);
-    r.expert = P.rhs ? P.rhs[pair] : (uint32_t)pair;
-  }
-  r.expert_ok = r.expert < (uint32_t)P.n_experts;
-  return r;
-}
-
-// Element offset of x's row for item row li; -1: not a row of this item; -2: the
-// row exists but its lhs index is out of range (NaN output). Sorted items keep a
-// row only while its pair's rhs is the item's expert.
-MI_DEV int64_t item_x_row(const QmvParams& P, const Item& it, int li) {
-  if (li >= it.cnt) return -1;
-  const int64_t p = it.pos0 + li;
-  const int64_t pair = p / P.M;
-  if (P.items && P.rhs[pair] != it.expert) return -1;
-  const int64_t m = p - pair * P.M;
-  const int64_t l = P.lhs ? (int64_t)P.lhs[pair] : pair / P.lhs_div;
-  if (l >= P.x_batch) return -2;
-  return (l * P.M + m) * (int64_t)P.K;
-}
-
-// One block = W waves on one 32-row weight tile of one item over one K range.
-// The K range's activations are staged into LDS once (fragment order, group sums),
-// the waves split the range's groups between them, stream their weights as 16-byte
-// loads one chunk ahead, and the block sums the waves' partials through LDS in wave
-// order. With a single K range the block writes y; otherwise it writes an fp32
-// partial that reduce_splits_kernel sums in split order.
+// One block = W waves sharing one K range [g0, g1) of one item; wave w owns the
+// 32-row weight tile blockIdx.x*W + w and streams it over the K range in chunks of
+// UG groups (256 bytes of each row). Flow:
+//   1. the block stages the range's activations into LDS (fragment order, group
+//      sums) -- all LDS writes happen here, before any weight DMA is in flight;
+//   2. each wave DMAs chunk c+1 of its tile straight into LDS (global_load_lds
+//      dwordx4: every instruction reads 4 rows x 256 contiguous bytes; 16-byte slot
+//      s of row r lands at slot s ^ (r & 15), so fragment reads hit distinct banks)
+//      while it runs the MFMAs of chunk c from the other buffer;
+//   3. each wave writes its finished rows (y, or an fp32 partial per K range that
+//      reduce_splits_kernel sums in range order).
 template <int BITS, int GS, int MR, bool XF32>
-__global__ void __launch_bounds__(512) qmv_kernel(QmvParams P) {
+__global__ void __launch_bounds__(64 * kQmvMaxWaves) qmv_kernel(QmvParams P) {
   constexpr int PF = 32 / BITS;
   constexpr int WPG = GS / PF;    // packed words per group per row
   constexpr int VPL = WPG / 2;    // words per lane per group (one k-half)
   constexpr int STEPS = GS / 16;  // MFMA steps per group
-  constexpr int UG = VPL >= MI_QMV_CW ? 1 : MI_QMV_CW / VPL;  // groups per chunk
+  constexpr int GSB = WPG * 4;    // bytes per group per row
+  constexpr int UG = 256 / GSB;   // groups per chunk (256 bytes per row)
   constexpr int MPAD = MR == 1 ? 1 : MR == 2 ? 2 : MR == 4 ? 8 : MR == 8 ? 16 : 32;
   constexpr int MXS = MPAD < 8 ? 8 : MPAD;  // group-sum row stride (b128 reads)
   constexpr int PLANES = XF32 ? 2 : 1;
-  constexpr int FB = 4;                     // staging fragments per thread per pass
+  constexpr int FB = 2;                     // staging fragments per thread per pass
+  constexpr int CHUNK = 32 * 256;           // LDS bytes of one chunk of one tile
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ int64_t srow[32];
@@ -159,51 +66,38 @@ __global__ void __launch_bounds__(512) qmv_kernel(QmvParams P) {
   const int l32 = lane & 31, hh = lane >> 5;
   const int K = P.K, N = P.N;
   const int G = K / GS;
-  const int64_t wrow = (int64_t)K / PF;
-  const int rb = blockIdx.x, ks = blockIdx.y;
+  const uint32_t wrow_b = (uint32_t)(K / PF) * 4u;  // bytes per packed weight row
+  const int ks = blockIdx.y;
   const int g0 = ks * P.gps;
   const int g1 = min(G, g0 + P.gps);
-  const int GB = g1 - g0;                        // groups staged by this block
+  const int GB = g1 - g0;                        // groups in this K range
   const int NF = GB * STEPS * 2 * MPAD;          // A fragments staged
-  u32x4_t* sx = (u32x4_t*)smem;                  // [GB][STEPS][2][MPAD] (+ lo plane)
-  float* sxs = (float*)(sx + (size_t)NF * PLANES);  // [GB][MXS]
-  float* sred = (float*)smem;                    // reused after the main loop
+  const int nch = (GB + UG - 1) / UG;            // chunks per tile
+  unsigned char* swt = smem;                     // [W][2][32 rows][256 B]
+  unsigned char* ssb = smem + (size_t)W * 2 * CHUNK;  // [W][2][scales 32x16 B, biases]
+  u32x4_t* sx = (u32x4_t*)(ssb + (size_t)W * 2 * 1024);  // [GB][STEPS][2][MPAD] (+lo)
+  float* sxs = (float*)(sx + (size_t)NF * PLANES);          // [GB][MXS]
   const uint32_t c43 = 0x43434343u;  // byte pool for the 4-bit unpack
-  // This wave's share of the block's groups.
-  const int gw0 = g0 + (int)((int64_t)GB * wave / W);
-  const int gw1 = g0 + (int)((int64_t)GB * (wave + 1) / W);
+  const int arow = l32 & (MPAD - 1);  // A rows >= MPAD: don't-care C rows, no mask
+  const int tile = blockIdx.x * W + wave;
+  const bool active = tile * 32 < N;
+  unsigned char* wbuf = swt + wave * 2 * CHUNK;
+  unsigned char* sbuf = ssb + wave * 2 * 1024;
+  const unsigned char* myrow0 = wbuf + l32 * 256;
+  // Scales/biases come by DMA (16-byte runs of 8 groups per row) when the packing
+  // allows 16-byte aligned runs; otherwise each lane loads its own.
+  constexpr bool kSdmaOk = UG <= 8;
+  const bool sdma = kSdmaOk && (G % 8) == 0;
+  const int sw = l32 & 15;
 
   const int n_items = P.item_count ? (int)*P.item_count : P.n_items_fixed;
   for (int itx = blockIdx.z; itx < n_items; itx += gridDim.z) {
     const Item it = decode_item(P, itx);
     const uint32_t ex = it.expert_ok ? it.expert : 0u;
     if (tid < 32) srow[tid] = item_x_row(P, it, tid);
+    lds_barrier();
 
-    // Uniform (SGPR) expert bases plus 32-bit per-lane byte offsets, so loads use
-    // the saddr form and per-group addresses are scalar adds.
-    const int n = min(rb * 32 + l32, N - 1);
-    const uint32_t* wbase = P.w + (int64_t)ex * N * wrow;
-    const uint16_t* sbase = P.scales + (int64_t)ex * N * G;
-    const uint16_t* bbase = P.biases + (int64_t)ex * N * G;
-    const uint32_t woff = (uint32_t)(((int64_t)n * wrow + hh * VPL) * 4);
-    const uint32_t soff = (uint32_t)((int64_t)n * G * 2);
-
-    uint32_t wcur[UG][VPL], scur[UG], bcur[UG];
-    auto load_chunk = [&](int gc, uint32_t (&wv)[UG][VPL], uint32_t (&sv)[UG],
-                          uint32_t (&bv)[UG]) {
-#pragma unroll
-      for (int u = 0; u < UG; ++u) {
-        const int g = min(gc + u, gw1 - 1);
-        load_u32<VPL>((const uint32_t*)((const char*)(wbase + (int64_t)g * WPG) + woff), wv[u]);
-        sv[u] = *(const uint16_t*)((const char*)(sbase + g) + soff);
-        bv[u] = *(const uint16_t*)((const char*)(bbase + g) + soff);
-      }
-    };
-    // First chunk's weights go out before the staging so both latencies overlap.
-    if (gw0 < gw1) load_chunk(gw0, wcur, scur, bcur);
-    __syncthreads();  // srow visible
-
-    // ---- stage x[rows][g0*GS, g1*GS) into LDS ---------------------------------
+    // ---- 1. stage x[rows][g0*GS, g1*GS) into LDS ---------------------------------
     for (int base = 0; base < NF; base += FB * BD) {
       u32x4_t v[FB][PLANES];
       float sum[FB];
@@ -270,127 +164,223 @@ __global__ void __launch_bounds__(512) qmv_kernel(QmvParams P) {
       for (int t = tid; t < GB * (MXS - MPAD); t += BD)
         sxs[(t / (MXS - MPAD)) * MXS + MPAD + t % (MXS - MPAD)] = 0.f;
     }
-    __syncthreads();
+    lds_barrier();
 
-    // ---- this wave's groups -----------------------------------------------------
-    // A rows >= MPAD read row (l32 % MPAD): those C rows are never written, so the
-    // values are don't-care and the LDS reads need no mask.
-    const int arow = l32 & (MPAD - 1);
-    float acc[MR];
+    if (active) {
+      // ---- 2. stream the tile over the K range ---------------------------------
+      const unsigned char* tbase = (const unsigned char*)P.w + ((int64_t)ex * N) * wrow_b;
+      const int n = min(tile * 32 + l32, N - 1);
+      const uint16_t* srp = P.scales + ((int64_t)ex * N + n) * G;
+      const uint16_t* brp = P.biases + ((int64_t)ex * N + n) * G;
+      // DMA chunk c (groups g0 + c*UG ...) into buffer b; scales/biases to registers.
+      auto issue = [&](int c, int b, uint32_t (&sv)[UG], uint32_t (&bv)[UG]) {
+        const int gc = g0 + c * UG;
+        const int nslots = min(UG, g1 - gc) * GSB / 16;  // valid slots per row
+        const int s = lane & 15;
 #pragma unroll
-    for (int r = 0; r < MR; ++r) acc[r] = 0.f;
-    auto group_mfma = [&](int ul, const uint32_t* words, f32x16_t& accg) {
+        for (int i = 0; i < 8; ++i) {
+          const int r = 4 * i + (lane >> 4);
+          const int sl = s ^ (r & 15);
+          const uint32_t nr = (uint32_t)min(tile * 32 + r, N - 1);
+          const unsigned char* src =
+              tbase + nr * wrow_b + (uint32_t)gc * GSB + (sl < nslots ? sl * 16 : 0);
+          __builtin_amdgcn_global_load_lds(
+              src, (__attribute__((address_space(3))) void*)(wbuf + b * CHUNK + i * 1024),
+              16, 0, 0);
+        }
+        if (sdma) {
+          // One instruction: lanes 0-31 fetch the scale run, 32-63 the bias run, of
+          // row l32 for the 8 groups [gc & ~7, +8) that hold this chunk.
+          const uint32_t nr = (uint32_t)min(tile * 32 + l32, N - 1);
+          const uint16_t* run = (hh ? P.biases : P.scales) + ((int64_t)ex * N + nr) * G + (gc & ~7);
+          __builtin_amdgcn_global_load_lds(
+              run, (__attribute__((address_space(3))) void*)(sbuf + b * 1024), 16, 0, 0);
+        } else {
 #pragma unroll
-      for (int j = 0; j < STEPS; ++j) {
-        const int idx = ((ul * STEPS + j) * 2 + hh) * MPAD + arow;
-        const u32x4_t B = b_frag<BITS>(words, j, c43);
-        accg = mfma32(sx[idx], B, j == 0 ? f32x16_t{} : accg);
-        if constexpr (XF32) accg = mfma32(sx[NF + idx], B, accg);
-      }
-    };
-    auto group_epilogue = [&](int ul, uint32_t sbits, uint32_t bbits, const f32x16_t& accg) {
-      float xs[MR];
-#pragma unroll
-      for (int r4 = 0; r4 < (MR + 3) / 4; ++r4) {
-        const f32x4_t v4 = *(const f32x4_t*)&sxs[ul * MXS + 8 * r4 + 4 * hh];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (4 * r4 + e < MR) xs[4 * r4 + e] = v4[e];
-      }
-      const float sc = bf16_bits_to_f32(sbits);
-      const float bi = bf16_bits_to_f32(bbits);
-      const float bb = (BITS == 4) ? fmaf(-128.f, sc, bi) : bi;
-#pragma unroll
-      for (int r = 0; r < MR; ++r) acc[r] = fmaf(bb, xs[r], fmaf(sc, accg[r], acc[r]));
-    };
-    for (int gc = gw0; gc < gw1; gc += UG) {
-      const bool more = gc + UG < gw1;
-      uint32_t wnx[UG][VPL], snx[UG], bnx[UG];
-      if (more) load_chunk(gc + UG, wnx, snx, bnx);
-      // Two groups at a time: their MFMA chains are independent and interleave.
-#pragma unroll
-      for (int u = 0; u < UG; u += 2) {
-        const int ul = gc + u - g0;
-        if (gc + u + 1 < gw1 && u + 1 < UG) {
-          f32x16_t a0, a1;
-#pragma unroll
-          for (int j = 0; j < STEPS; ++j) {
-            const int i0 = ((ul * STEPS + j) * 2 + hh) * MPAD + arow;
-            const int i1 = (((ul + 1) * STEPS + j) * 2 + hh) * MPAD + arow;
-            const u32x4_t B0 = b_frag<BITS>(wcur[u], j, c43);
-            const u32x4_t B1 = b_frag<BITS>(wcur[u + 1 < UG ? u + 1 : u], j, c43);
-            a0 = mfma32(sx[i0], B0, j == 0 ? f32x16_t{} : a0);
-            a1 = mfma32(sx[i1], B1, j == 0 ? f32x16_t{} : a1);
-            if constexpr (XF32) {
-              a0 = mfma32(sx[NF + i0], B0, a0);
-              a1 = mfma32(sx[NF + i1], B1, a1);
-            }
+          for (int u = 0; u < UG; ++u) {
+            const int g = min(gc + u, g1 - 1);
+            sv[u] = srp[g];
+            bv[u] = brp[g];
           }
-          group_epilogue(ul, scur[u], bcur[u], a0);
-          group_epilogue(ul + 1, scur[u + 1 < UG ? u + 1 : u], bcur[u + 1 < UG ? u + 1 : u], a1);
-        } else if (gc + u < gw1) {
-          f32x16_t a0;
-          group_mfma(ul, wcur[u], a0);
-          group_epilogue(ul, scur[u], bcur[u], a0);
         }
-      }
-      if (more) {
+      };
+      float acc[MR];
 #pragma unroll
-        for (int u = 0; u < UG; ++u) {
+      for (int r = 0; r < MR; ++r) acc[r] = 0.f;
+      // MFMAs of chunk c from buffer b (two groups interleaved).
+      auto compute = [&](int c, int b, const uint32_t (&sv)[UG], const uint32_t (&bv)[UG]) {
+        const unsigned char* myrow = myrow0 + b * CHUNK;
+        const int gc = g0 + c * UG;
+        const int ng = min(UG, g1 - gc);
+        auto load_words = [&](int u, uint32_t (&words)[VPL]) {
+          const int byte0 = u * GSB + hh * (GSB / 2);
+          if constexpr (VPL >= 4) {
 #pragma unroll
-          for (int q = 0; q < VPL; ++q) wcur[u][q] = wnx[u][q];
-          scur[u] = snx[u];
-          bcur[u] = bnx[u];
+            for (int q = 0; q < VPL / 4; ++q) {
+              const int slot = (byte0 >> 4) + q;
+              const u32x4_t t = *(const u32x4_t*)(myrow + ((slot ^ sw) << 4));
+              words[4 * q] = t.x; words[4 * q + 1] = t.y; words[4 * q + 2] = t.z;
+              words[4 * q + 3] = t.w;
+            }
+          } else {
+            const int slot = byte0 >> 4;
+            const u32x2_t t = *(const u32x2_t*)(myrow + ((slot ^ sw) << 4) + (byte0 & 15));
+            words[0] = t.x; words[1] = t.y;
+          }
+        };
+        auto epilogue = [&](int u, int ul, const f32x16_t& accg) {
+          float xs[MR];
+#pragma unroll
+          for (int r4 = 0; r4 < (MR + 3) / 4; ++r4) {
+            const f32x4_t v4 = *(const f32x4_t*)&sxs[ul * MXS + 8 * r4 + 4 * hh];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (4 * r4 + e < MR) xs[4 * r4 + e] = v4[e];
+          }
+          uint32_t sbits, bbits;
+          if (sdma) {
+            const int gi = ((gc & 7) + u) * 2;  // byte of group gc+u inside the run
+            sbits = *(const uint16_t*)(sbuf + b * 1024 + l32 * 16 + gi);
+            bbits = *(const uint16_t*)(sbuf + b * 1024 + 512 + l32 * 16 + gi);
+          } else {
+            sbits = sv[u];
+            bbits = bv[u];
+          }
+          const float sc = bf16_bits_to_f32(sbits);
+          const float bi = bf16_bits_to_f32(bbits);
+          const float bb = (BITS == 4) ? fmaf(-128.f, sc, bi) : bi;
+#pragma unroll
+          for (int r = 0; r < MR; ++r) acc[r] = fmaf(bb, xs[r], fmaf(sc, accg[r], acc[r]));
+        };
+#pragma unroll
+        for (int u = 0; u < UG; u += 2) {
+          const int ul = gc + u - g0;
+          if (u + 1 < ng) {
+            uint32_t w0[VPL], w1[VPL];
+            load_words(u, w0);
+            load_words(u + 1, w1);
+            f32x16_t a0, a1;
+#pragma unroll
+            for (int j = 0; j < STEPS; ++j) {
+              const int i0 = ((ul * STEPS + j) * 2 + hh) * MPAD + arow;
+              const int i1 = i0 + STEPS * 2 * MPAD;
+              const u32x4_t B0 = b_frag<BITS>(w0, j, c43);
+              const u32x4_t B1 = b_frag<BITS>(w1, j, c43);
+              a0 = mfma32(sx[i0], B0, j == 0 ? f32x16_t{} : a0);
+              a1 = mfma32(sx[i1], B1, j == 0 ? f32x16_t{} : a1);
+              if constexpr (XF32) {
+                a0 = mfma32(sx[NF + i0], B0, a0);
+                a1 = mfma32(sx[NF + i1], B1, a1);
+              }
+            }
+            epilogue(u, ul, a0);
+            epilogue(u + 1, ul + 1, a1);
+          } else if (u < ng) {
+            uint32_t w0[VPL];
+            load_words(u, w0);
+            f32x16_t a0;
+#pragma unroll
+            for (int j = 0; j < STEPS; ++j) {
+              const int i0 = ((ul * STEPS + j) * 2 + hh) * MPAD + arow;
+              const u32x4_t B0 = b_frag<BITS>(w0, j, c43);
+              a0 = mfma32(sx[i0], B0, j == 0 ? f32x16_t{} : a0);
+              if constexpr (XF32) a0 = mfma32(sx[NF + i0], B0, a0);
+            }
+            epilogue(u, ul, a0);
+          }
         }
-      }
-    }
+      };
 
-    // ---- reduce the waves' partials (wave order), write --------------------------
-    __syncthreads();  // staging area is reused
-#pragma unroll
-    for (int r = 0; r < MR; ++r) sred[(wave * MR + r) * 64 + lane] = acc[r];
-    __syncthreads();
-    const int64_t PT = P.n_pairs * P.M;
-    for (int t = tid; t < MR * 64; t += BD) {
-      const int r = t >> 6, l2 = t & 63;
-      const int li = 8 * (r / 4) + 4 * (l2 >> 5) + (r % 4);
-      const int nn = rb * 32 + (l2 & 31);
-      const int64_t xr = li < 32 ? srow[li] : -1;
-      if (nn >= N || li >= it.cnt || xr == -1) continue;
-      float v = 0.f;
-      for (int w2 = 0; w2 < W; ++w2) v += sred[(w2 * MR + r) * 64 + l2];
-      const int64_t p = it.pos0 + li;
-      if (P.ks > 1) {
-        P.part[((int64_t)ks * PT + p) * N + nn] = v;
+      uint32_t sA[UG], bA[UG], sB[UG], bB[UG];
+      issue(0, 0, sA, bA);
+      // Steady state, two chunks per trip so the scale registers ping-pong without
+      // copies; every issue is unconditional so vmcnt accounting stays exact.
+      // "chunk c landed" = at most one chunk's loads (issued later) still pending.
+      auto wait_prev = [&]() {
+        if (sdma) __builtin_amdgcn_s_waitcnt(vmcnt_imm(9));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(8 + 2 * UG));
+      };
+      int c = 0;
+      for (; c + 2 < nch; c += 2) {
+        issue(c + 1, 1, sB, bB);
+        wait_prev();                          // chunk c landed
+        compute(c, 0, sA, bA);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // buffer 0 reads done
+        issue(c + 2, 0, sA, bA);
+        wait_prev();                          // chunk c+1 landed
+        compute(c + 1, 1, sB, bB);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // buffer 1 reads done
+      }
+      if (c + 1 < nch) {
+        issue(c + 1, 1, sB, bB);
+        wait_prev();
+        compute(c, 0, sA, bA);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        compute(c + 1, 1, sB, bB);
       } else {
-        if (xr < 0 || !it.expert_ok) v = __builtin_nanf("");
-        if constexpr (XF32) ((float*)P.y)[p * N + nn] = v;
-        else ((uint16_t*)P.y)[p * N + nn] = (uint16_t)f32_to_bf16_bits(v);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        compute(c, 0, sA, bA);
+      }
+
+      // ---- 3. write this wave's rows ---------------------------------------------
+      const int64_t PT = P.n_pairs * P.M;
+      const int nn = tile * 32 + l32;
+#pragma unroll
+      for (int r = 0; r < MR; ++r) {
+        const int li = 8 * (r / 4) + 4 * hh + (r % 4);
+        const int64_t xr = li < 32 ? srow[li] : -1;
+        if (nn < N && li < it.cnt && xr != -1) {
+          float v = acc[r];
+          const int64_t p = it.pos0 + li;
+          if (P.ks > 1) {
+            P.part[((int64_t)ks * PT + p) * N + nn] = v;
+          } else {
+            if (xr < 0 || !it.expert_ok) v = __builtin_nanf("");
+            if constexpr (XF32) ((float*)P.y)[p * N + nn] = v;
+            else ((uint16_t*)P.y)[p * N + nn] = (uint16_t)f32_to_bf16_bits(v);
+          }
+        }
       }
     }
-    __syncthreads();
+    lds_barrier();  // LDS is restaged for the next item
   }
 }
 
 // Sums the K-split partials in split order and applies the NaN rule for rows whose
-// indices were out of range (recomputed from the item list).
+// indices were out of range. One thread per output element, 32-bit index math.
 template <bool XF32>
 __global__ void reduce_splits_kernel(QmvParams P) {
-  const int64_t PT = P.n_pairs * P.M;
-  const int64_t total = PT * P.N;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t p = i / P.N;
-    const int64_t pair = p / P.M;
+  const uint32_t PT = (uint32_t)(P.n_pairs * P.M);
+  const uint32_t N = (uint32_t)P.N;
+  const uint32_t total = PT * N;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += gridDim.x * blockDim.x) {
     float v = 0.f;
-    for (int k2 = 0; k2 < P.ks; ++k2) v += P.part[(int64_t)k2 * total + i];
-    const uint32_t e = P.rhs ? P.rhs[pair] : (uint32_t)pair;
-    const int64_t l = P.lhs ? (int64_t)P.lhs[pair] : pair / P.lhs_div;
-    if (e >= (uint32_t)P.n_experts || l >= P.x_batch) v = __builtin_nanf("");
+    for (int k2 = 0; k2 < P.ks; ++k2) v += P.part[(size_t)k2 * total + i];
+    const uint32_t p = i / N;
+    const uint32_t pair = P.M == 1 ? p : p / (uint32_t)P.M;
+    const uint32_t e = P.rhs ? P.rhs[pair] : pair;
+    const uint32_t l = P.lhs ? P.lhs[pair] : pair / (uint32_t)P.lhs_div;
+    if (e >= (uint32_t)P.n_experts || (int64_t)l >= P.x_batch) v = __builtin_nanf("");
     if constexpr (XF32) ((float*)P.y)[i] = v;
     else ((uint16_t*)P.y)[i] = (uint16_t)f32_to_bf16_bits(v);
   }
 }
+
+}  // namespace
+
+hipError_t launch_reduce_splits(const QmvParams& P, hipStream_t s) {
+  const int64_t total = P.n_pairs * P.M * P.N;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (P.x_f32)
+    hipLaunchKernelGGL(reduce_splits_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, P);
+  else
+    hipLaunchKernelGGL(reduce_splits_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, P);
+  return hipGetLastError();
+}
+
+namespace {
 
 template <int BITS, int GS, int MR, bool XF32>
 hipError_t launch_t(const QmvParams& P, dim3 grid, int waves, size_t lds, hipStream_t s) {
@@ -426,14 +416,17 @@ int qmv_mr_for_rows(int rows) {
   return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 8 ? 4 : rows <= 16 ? 8 : 16;
 }
 
-// LDS bytes of one block: staged fragments + group sums, or the wave reduction.
+// Groups in one wave's weight slice (256 bytes of each row).
+int qmv_groups_per_wave(int bits, int gs) { return 256 / (gs * bits / 8); }
+
+// Dynamic LDS bytes of one block: double-buffered weight chunks of every wave +
+// staged fragments + group sums.
 size_t qmv_lds_bytes(int groups, int gs, int mr, int x_f32, int waves) {
   const int mpad = mr == 1 ? 1 : mr == 2 ? 2 : mr == 4 ? 8 : mr == 8 ? 16 : 32;
   const int mxs = mpad < 8 ? 8 : mpad;
-  const size_t stage = (size_t)groups * (gs / 16) * 2 * mpad * 16 * (x_f32 ? 2 : 1) +
-                       (size_t)groups * mxs * 4;
-  const size_t red = (size_t)waves * mr * 64 * 4;
-  return stage > red ? stage : red;
+  return (size_t)waves * 2 * (32 * 256 + 1024) +
+         (size_t)groups * (gs / 16) * 2 * mpad * 16 * (x_f32 ? 2 : 1) +
+         (size_t)groups * mxs * 4;
 }
 
 hipError_t launch_qmv(const QmvParams& P, const QmvConfig& C, hipStream_t s) {
@@ -446,14 +439,7 @@ hipError_t launch_qmv(const QmvParams& P, const QmvConfig& C, hipStream_t s) {
                      : (P.x_f32 ? launch_gs<8, true>(P, grid, C.waves, lds, mr, s)
                                 : launch_gs<8, false>(P, grid, C.waves, lds, mr, s));
   if (e != hipSuccess || P.ks == 1) return e;
-  const int64_t total = P.n_pairs * P.M * P.N;
-  int64_t blocks = (total + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  if (P.x_f32)
-    hipLaunchKernelGGL(reduce_splits_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, P);
-  else
-    hipLaunchKernelGGL(reduce_splits_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, P);
-  return hipGetLastError();
+  return launch_reduce_splits(P, s);
 }
 
 }  // namespace mi
