@@ -174,7 +174,7 @@ QmvPlan qmv16_plan(int N, int K, int gs, int bits, int rows, int64_t n_items, in
   int ks = 1;
   for (;;) {
     const int gps = ceil_div(G, ks);
-    if (mi::qmv16_lds_bytes(gps, gs, mp, x_f32, w) <= lds_max) break;
+    if (mi::qmv16_lds_bytes(gps, gs, bits, mp, x_f32, w) <= lds_max) break;
     if (w > 1) {
       w >>= 1;
       continue;
@@ -182,7 +182,8 @@ QmvPlan qmv16_plan(int N, int K, int gs, int bits, int rows, int64_t n_items, in
     if (ks >= G) break;
     ++ks;
   }
-  p.gps = ceil_div(G, ks);
+  // K ranges start on 8-group boundaries (aligned scale runs).
+  p.gps = ks == 1 ? G : ceil_div(ceil_div(G, ks), 8) * 8;
   p.ks = ceil_div(G, p.gps);
   p.cfg.waves = w;
   p.row_blocks = tiles;
@@ -266,7 +267,7 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
   const int64_t PT = n_idx * M;
   // Decode widths (<= 16 rows per pair, or sorted runs cut into 16-row items) use the
   // 16-row-tile kernel; 17..32 rows per pair use the 32-row-tile kernel.
-  const bool narrow = use_items ? true : M <= 16;
+  const bool narrow = (use_items || M <= 16) && mi::qmv16_supported(P.K, gs, nb);
   P.rpi = narrow ? 16 : 32;
   const int rows = (int)(M < P.rpi ? M : P.rpi);
   int64_t n_items, max_items = 0;
@@ -284,7 +285,7 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
     P.n_items_fixed = 0;
   }
   QmvPlan plan = narrow ? qmv16_plan(P.N, P.K, gs, nb, use_items ? P.rpi : rows, n_items, P.x_f32)
-                        : qmv_plan(P.N, P.K, gs, nb, rows, n_items, P.x_f32);
+                        : qmv_plan(P.N, P.K, gs, nb, use_items ? P.rpi : rows, n_items, P.x_f32);
   P.ks = plan.ks;
   P.gps = plan.gps;
   P.row_blocks = plan.row_blocks;

@@ -44,7 +44,8 @@ hipError_t launch_reduce_splits(const QmvParams& P, hipStream_t s);
 // Decode-width kernel (qmv16.hip): M <= 16 rows per item, 16-row weight tiles.
 int qmv16_mp_for_rows(int rows);
 int qmv16_groups_per_chunk(int bits, int gs);
-size_t qmv16_lds_bytes(int groups, int gs, int mp, int x_f32, int waves);
+bool qmv16_supported(int K, int gs, int bits);
+size_t qmv16_lds_bytes(int groups, int gs, int bits, int mp, int x_f32, int waves);
 hipError_t launch_qmv16(const QmvParams& P, const QmvConfig& C, hipStream_t s);
 
 // Sorted gather: runs of equal rhs -> work items (moe.hip / segments.hip).

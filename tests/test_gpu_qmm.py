@@ -53,7 +53,8 @@ def test_quantize_bit_exact(dev, bits, gs):
 
 QMM_CASES = [(1, 4096, 512), (1, 100, 1024), (2, 64, 256), (3, 48, 512), (4, 80, 256),
              (5, 32, 384), (8, 64, 512), (16, 64, 256), (17, 40, 256), (32, 96, 512),
-             (33, 64, 256), (64, 48, 256)]
+             (33, 64, 256), (64, 48, 256), (1, 1024, 4096), (3, 512, 8192), (16, 256, 4096),
+             (1, 320, 14336), (5, 48, 2560)]
 
 
 @pytest.mark.parametrize("bits", [4, 8])
@@ -126,11 +127,11 @@ def test_gather_decode_broadcast(dev):
     assert max_err_ratio(to_f64(y).reshape(2 * topk, 1, N), truth) <= BF16_TOL
 
 
-@pytest.mark.parametrize("M", [1, 3])
-def test_gather_sorted_matches_unsorted(dev, M):
-    """Sorted (grouped) path == unsorted path bit-for-bit per pair, and both match truth."""
-    _print_case(t="gather_sorted", M=M)
-    E, N, K, T, topk = 8, 64, 256, 40, 3
+@pytest.mark.parametrize("M,K", [(1, 256), (3, 256), (1, 1024), (2, 2048)])
+def test_gather_sorted_matches_unsorted(dev, M, K):
+    """Sorted (grouped) path and unsorted path both match truth."""
+    _print_case(t="gather_sorted", M=M, K=K)
+    E, N, T, topk = 8, 64, 40, 3
     wq, s, b = weights(E, N, K, 4, 64, 77)
     rng = np.random.default_rng(5)
     flat = rng.integers(0, E, size=T * topk).astype(np.uint32)
