@@ -126,6 +126,19 @@ def cpu_baseline(torch, layers, bits, gs, hidden=4096, inter=14336, budget_s=10.
                       f"{n_l} layers' weights, {t:.1f} s, C oracle mo_qmm_f32 with OpenMP"}
 
 
+def pmc_traffic():
+    """HBM bytes per decode launch, from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (counters scaled by a copy kernel of known size); None if absent."""
+    path = os.path.join(ROOT, "profiles", "qmv16_decode_llama8b_mlp_pmc_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -135,6 +148,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 4 device copies of 256 MiB (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build's path runs on a single MI355X "
@@ -143,8 +159,16 @@ def main():
         sys.exit(2)
 
     import torch
-    import mi_qmm as mi
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        a = torch.empty(1 << 27, dtype=torch.int16, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(4):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_each_way": a.numel() * 2, "copies": 4}))
+        return
+    import mi_qmm as mi
     bits, gs = 4, 64
     layers = build_mlp_layers(torch, mi, args.layers, bits, gs, dev)
     head = decode_mlp(torch, mi, layers, 1, bits, gs, dev, args.steps, args.warmup)
@@ -182,7 +206,7 @@ def main():
                    "tokens_per_s": round(head["tokens_per_s"], 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "qmv_kernel<4,64,1,1,*,false>",
+                     "traffic": pmc_traffic(), "kernel": "mi::qmv16_kernel<4, 64, 1, false>",
                      "bytes_per_launch": head["bytes_per_launch"],
                      "avg_launch_us": round(head["avg_launch_us"], 3)},
         "cpu_baseline": cpu,

@@ -267,7 +267,8 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
   const int64_t PT = n_idx * M;
   // Decode widths (<= 16 rows per pair, or sorted runs cut into 16-row items) use the
   // 16-row-tile kernel; 17..32 rows per pair use the 32-row-tile kernel.
-  const bool narrow = (use_items || M <= 16) && mi::qmv16_supported(P.K, gs, nb);
+  static const int narrow_max = env_int("MI_QMM_NARROW_MAX", 4);
+  const bool narrow = (use_items || M <= narrow_max) && mi::qmv16_supported(P.K, gs, nb);
   P.rpi = narrow ? 16 : 32;
   const int rows = (int)(M < P.rpi ? M : P.rpi);
   int64_t n_items, max_items = 0;
