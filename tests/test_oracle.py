@@ -1,0 +1,278 @@
+"""Pins the CPU oracle (oracle/mi_oracle.c) before it is trusted as the checker.
+
+Each check comes from somewhere other than the oracle's own formula: published
+constants (SplitMix64), torch's bf16 arithmetic, numpy float64 matmuls, hand-worked
+groups, closed forms, brute force on tiny inputs, and the reference's own test
+expectations (tests/golden/geometry_cases.json, from src/transformer.zig:22930).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+# ------------------------------------------------------------------ bf16 --
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(0)
+    f = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 20000),
+        np.array([0.0, -0.0, 1.0, -1.0, np.inf, -np.inf, 3.0e38, 1e-40, -1e-42], np.float32),
+        # exact ties at bf16 precision: round to even
+        (np.arange(1, 2000, dtype=np.uint32) << 16 | 0x8000).view(np.float32),
+    ]).astype(np.float32)
+    ours = O.f32_to_bf16(f)
+    theirs = torch.from_numpy(f).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, theirs)
+    assert np.array_equal(O.bf16_to_f32(ours), torch.from_numpy(ours.view(np.int16))
+                          .view(torch.bfloat16).float().numpy())
+
+
+def test_bf16_nan_stays_nan():
+    f = np.array([np.nan, -np.nan], np.float32)
+    assert np.isnan(O.bf16_to_f32(O.f32_to_bf16(f))).all()
+
+
+# ------------------------------------------------------------- generator --
+def test_splitmix64_known_answers():
+    # SplitMix64 (Steele, Lea, Flood 2014) seeded with 0: its published first outputs.
+    L = O.lib()
+    assert L.mo_splitmix64(0, 0) == 0xE220A8397B1DCDAF
+    assert L.mo_splitmix64(0, 1) == 0x6E789E6AA1B965F4
+    assert L.mo_splitmix64(0, 2) == 0x06C45D188009454F
+
+
+def test_randn_moments_and_determinism():
+    a = O.randn(1 << 20, O.seed_for(1, 1))
+    assert abs(a.mean()) < 5e-3 and abs(a.std() - 1.0) < 5e-3
+    assert np.array_equal(a[:1000], O.randn(1000, O.seed_for(1, 1)))
+    b = O.randn(1 << 16, 7, 0.0, 0.02)
+    assert abs(b.std() - 0.02) < 5e-4
+    u = O.uniform(1 << 16, 3)
+    assert u.min() >= 0.0 and u.max() < 1.0 and abs(u.mean() - 0.5) < 5e-3
+
+
+# --------------------------------------------------------------- packing --
+def test_pack_known_words():
+    # LSB-first: value j of a word sits at bits [j*bits, (j+1)*bits)
+    # (src/transformer.zig:20098-20108 nibbles, :522-525 bytes).
+    q4 = np.array([[0, 1, 2, 3, 4, 5, 6, 7, 15, 14, 13, 12, 11, 10, 9, 8]], np.uint8)
+    assert O.pack(q4, 4).tolist() == [[0x76543210, 0x89ABCDEF]]
+    q8 = np.array([[1, 2, 3, 4, 255, 0, 128, 7]], np.uint8)
+    assert O.pack(q8, 8).tolist() == [[0x04030201, 0x078000FF]]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_pack_round_trip(bits):
+    rng = np.random.default_rng(bits)
+    q = rng.integers(0, 1 << bits, size=(7, 256)).astype(np.uint8)
+    wq = O.pack(q, bits)
+    assert wq.shape == (7, 256 * bits // 32)
+    assert np.array_equal(O.unpack(wq, 256, bits), q)
+    # independent numpy unpack
+    shifts = np.arange(32 // bits, dtype=np.uint32) * bits
+    nq = ((wq[..., None] >> shifts) & ((1 << bits) - 1)).reshape(7, 256)
+    assert np.array_equal(nq, q)
+
+
+# -------------------------------------------------------------- quantize --
+def test_quantize_hand_worked_group():
+    # group min -1, max 0.5: |min| > |max| so scale = 1.5/15 = 0.1 > 0, edge = min = -1,
+    # q0 = rint(-1/0.1) = -10, scale = -1/-10 = 0.1, bias = -1; 0.5 -> q 15, 0 -> q 10.
+    g = np.zeros(64, np.float32)
+    g[0], g[1] = -1.0, 0.5
+    w = O.f32_to_bf16(g[None, :])
+    wq, s, b = O.quantize(w, 64, 4)
+    q = O.unpack(wq, 64, 4)[0]
+    assert q[0] == 0 and q[1] == 15 and (q[2:] == 10).all()
+    assert s[0, 0] == O.f32_to_bf16(np.float32(0.1)) and b[0, 0] == 0xBF80
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_quantize_invariants(bits, gs):
+    w = O.f32_to_bf16(O.randn(32 * 512, 9, 0.0, 0.02).reshape(32, 512))
+    w[0, :gs] = O.f32_to_bf16(np.full(gs, 0.375, np.float32))  # constant group
+    w[1, :gs] = 0                                                # zero group
+    # on a 0.25 grid spanning codes 0 .. 2^bits-1 (every value fits bf16 exactly)
+    codes = np.random.default_rng(bits).integers(0, 1 << bits, gs)
+    codes[0], codes[1] = 0, (1 << bits) - 1
+    w[2, :gs] = O.f32_to_bf16(codes.astype(np.float32) * 0.25 - 1.0)
+    wq, s, b = O.quantize(w, gs, bits)
+    deq = O.dequantize(wq, s, b, gs, bits, O.DQ_F32)
+    wf = O.bf16_to_f32(w)
+    sf = np.repeat(O.bf16_to_f32(s), gs, axis=1)
+    bf = np.repeat(O.bf16_to_f32(b), gs, axis=1)
+    # At most one step: the edge refit scale = edge/rint(edge/scale) can stretch the
+    # far end of the group past the top code, where it clamps (worst case q0 = 2^(bits-1)).
+    # Plus the bf16 rounding of the scale (times q <= 2^bits-1) and of the bias.
+    bound = np.abs(sf) * (1.0 + (1 << bits) * 2.0 ** -8) + np.abs(bf) * 2.0 ** -8 + 1e-12
+    assert (np.abs(deq - wf) <= bound).all()
+    assert np.array_equal(deq[0, :gs], wf[0, :gs])
+    assert np.array_equal(deq[1, :gs], wf[1, :gs])
+    assert np.array_equal(deq[2, :gs], wf[2, :gs])
+    # the edge element of every group (the larger-magnitude end, max on a tie) is
+    # reproduced exactly: it becomes the bias and code 0
+    G = 512 // gs
+    for r in range(32):
+        for g in range(G):
+            seg = wf[r, g * gs:(g + 1) * gs]
+            e = int(np.argmin(seg)) if abs(seg.min()) > abs(seg.max()) else int(np.argmax(seg))
+            assert deq[r, g * gs + e] == seg[e]
+
+
+# ------------------------------------------------------------ dequantize --
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequantize_closed_forms(bits):
+    rng = np.random.default_rng(1)
+    N, K, gs = 16, 256, 64
+    q = rng.integers(0, 1 << bits, size=(N, K)).astype(np.uint8)
+    s = O.f32_to_bf16(rng.standard_normal((N, K // gs)).astype(np.float32) * 0.01)
+    b = O.f32_to_bf16(rng.standard_normal((N, K // gs)).astype(np.float32) * 0.1)
+    wq = O.pack(q, bits)
+    sf = np.repeat(O.bf16_to_f32(s), gs, axis=1).astype(np.float64)
+    bf = np.repeat(O.bf16_to_f32(b), gs, axis=1).astype(np.float64)
+    exact = sf * q + bf   # exact in float64: 8-bit significands times <= 8-bit integers
+    f32 = O.dequantize(wq, s, b, gs, bits, O.DQ_F32)
+    assert np.array_equal(f32, exact.astype(np.float32))
+    fused = O.dequantize(wq, s, b, gs, bits, O.DQ_BF16_FUSED)
+    assert np.array_equal(fused, O.f32_to_bf16(exact.astype(np.float32)))
+    # op-by-op bf16: torch's bf16 multiply, then bf16 add
+    tq = torch.from_numpy(q.astype(np.float32)).to(torch.bfloat16)
+    ts = torch.from_numpy(np.repeat(s, gs, axis=1).view(np.int16)).view(torch.bfloat16)
+    tb = torch.from_numpy(np.repeat(b, gs, axis=1).view(np.int16)).view(torch.bfloat16)
+    opw = (ts * tq + tb).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.dequantize(wq, s, b, gs, bits, O.DQ_BF16_OPWISE), opw)
+
+
+# ------------------------------------------------------------------- qmm --
+def _dense(wq, s, b, gs, bits):
+    return O.dequantize(wq, s, b, gs, bits, O.DQ_F32).astype(np.float64)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmm_f64_matches_numpy(bits):
+    wq, s, b = O.make_weight(48, 512, 5, bits)
+    x = O.make_x_bf16(3, 512, 6)
+    truth = O.bf16_to_f32(x).astype(np.float64) @ _dense(wq, s, b, 64, bits).T
+    assert np.allclose(O.qmm_f64(x, wq, s, b, 64, bits), truth, rtol=1e-12, atol=1e-12)
+    xf = O.randn(2 * 512, 8).reshape(2, 512)
+    assert np.allclose(O.qmm_f64(xf, wq, s, b, 64, bits),
+                       xf.astype(np.float64) @ _dense(wq, s, b, 64, bits).T, rtol=1e-12,
+                       atol=1e-12)
+    y32 = O.qmm_f32(x, wq, s, b, 64, bits, 2)
+    assert np.max(np.abs(y32 - truth)) <= 1e-5 * np.max(np.abs(truth))
+
+
+def test_qmm_special_cases():
+    N, K = 32, 128
+    q = (np.arange(N * K) * 5 % 16).astype(np.uint8).reshape(N, K)
+    wq = O.pack(q, 4)
+    one = O.f32_to_bf16(np.ones((N, 2), np.float32))
+    zero = np.zeros((N, 2), np.uint16)
+    x = np.zeros((3, K), np.float32)
+    x[0, 9] = 1.0
+    x[1] = 1.0
+    x[2] = np.arange(K) % 3
+    y = O.qmm_f64(x, wq, one, zero, 64, 4)
+    assert np.array_equal(y[0], q[:, 9].astype(np.float64))
+    assert np.array_equal(y[1], q.sum(axis=1).astype(np.float64))
+    assert np.array_equal(y[2], (q * (np.arange(K) % 3)).sum(axis=1).astype(np.float64))
+
+
+def test_gather_qmm_per_index_and_broadcast():
+    E, N, K = 5, 24, 256
+    wq, s, b = O.make_weight(E * N, K, 12)
+    wq, s, b = wq.reshape(E, N, -1), s.reshape(E, N, -1), b.reshape(E, N, -1)
+    x = O.make_x_bf16(4 * 2, K, 13).reshape(4, 2, K)
+    lhs = np.array([3, 0, 0, 2, 1, 3], np.uint32)
+    rhs = np.array([4, 4, 0, 1, 2, 3], np.uint32)
+    y = O.gather_qmm_f64(x, wq, s, b, lhs, rhs, 6)
+    for i in range(6):
+        t = O.bf16_to_f32(x[lhs[i]]).astype(np.float64) @ _dense(wq[rhs[i]], s[rhs[i]], b[rhs[i]],
+                                                                 64, 4).T
+        assert np.allclose(y[i], t, rtol=1e-12, atol=1e-12)
+    # lhs absent: lhs(i) = i // lhs_div
+    y2 = O.gather_qmm_f64(x, wq, s, b, None, rhs[:4], 4, lhs_div=2)
+    y3 = O.gather_qmm_f64(x, wq, s, b, np.array([0, 0, 1, 1], np.uint32), rhs[:4], 4)
+    assert np.array_equal(y2, y3)
+    # out-of-range indices are refused (the GPU path writes NaN rows for them)
+    with pytest.raises(ValueError):
+        O.gather_qmm_f64(x, wq, s, b, np.array([9], np.uint32), np.array([0], np.uint32), 1)
+
+
+# --------------------------------------------------------------- routing --
+def test_route_softmax_topk_matches_numpy():
+    rng = np.random.default_rng(2)
+    T, E, k = 17, 128, 8
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    logits[0, 5] = logits[0, 9] = 4.0   # tie: the lower expert id comes first
+    inds, scores = O.route_softmax_topk(logits, k)
+    p = np.exp(logits.astype(np.float64) - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    order = np.lexsort((np.tile(np.arange(E), (T, 1)), -logits), axis=1)[:, :k]
+    assert np.array_equal(inds, order.astype(np.uint32))
+    top = np.take_along_axis(p, order, 1)
+    assert np.allclose(scores, top / top.sum(1, keepdims=True), rtol=1e-5, atol=1e-7)
+    assert inds[0, 0] == 5 and inds[0, 1] == 9
+
+
+def test_sort_dispatch_matches_argsort():
+    rng = np.random.default_rng(3)
+    k = 8
+    flat = rng.integers(0, 128, size=64 * k).astype(np.uint32)
+    order, inv, srt, lhs = O.sort_dispatch(flat, k)
+    ref = np.argsort(flat, kind="stable")
+    assert np.array_equal(order, ref)
+    assert np.array_equal(inv[order], np.arange(flat.size))
+    assert np.array_equal(srt, flat[ref]) and (np.diff(srt.astype(np.int64)) >= 0).all()
+    assert np.array_equal(lhs, ref // k)
+    assert np.array_equal(srt[inv], flat)
+
+
+# ---------------------------------------------------- fused tail contracts --
+def test_sigmoid_table_exhaustive():
+    t = O.sigmoid_table_bf16()
+    v = O.bf16_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16)).astype(np.float64)
+    # fp32 exp(-v) overflows below about -88.7 (the table is 0 there, fp64 gives
+    # subnormals), so compare where the fp32 formula is finite
+    ok = ~np.isnan(v) & (v > -88.0)
+    sig = 1.0 / (1.0 + np.exp(-v[ok]))
+    want = O.f32_to_bf16(sig.astype(np.float32))
+    diff = np.abs(t[ok].astype(np.int32) - want.astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.999
+
+
+def test_swiglu_and_down_reduce_compositions():
+    rng = np.random.default_rng(4)
+    g = O.f32_to_bf16(rng.standard_normal(4096).astype(np.float32))
+    u = O.f32_to_bf16(rng.standard_normal(4096).astype(np.float32))
+    tg = torch.from_numpy(g.view(np.int16)).view(torch.bfloat16)
+    tu = torch.from_numpy(u.view(np.int16)).view(torch.bfloat16)
+    sig = torch.from_numpy(O.sigmoid_table_bf16()[g].view(np.int16)).view(torch.bfloat16)
+    want = ((tg * sig) * tu).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.swiglu_bf16(g, u), want)
+    v = O.f32_to_bf16(rng.standard_normal((8, 300)).astype(np.float32))
+    sc = O.f32_to_bf16(rng.random(8).astype(np.float32))
+    tv = torch.from_numpy(v.view(np.int16)).view(torch.bfloat16)
+    ts = torch.from_numpy(sc.view(np.int16)).view(torch.bfloat16)
+    acc = torch.zeros(300, dtype=torch.bfloat16)
+    for j in range(8):
+        acc = acc + tv[j] * ts[j]
+    assert np.array_equal(O.down_reduce_bf16(v, sc), acc.view(torch.int16).numpy().view(np.uint16))
+
+
+# -------------------------------------------------------- geometry solve --
+def test_geometry_cases_from_reference_tests():
+    cases = json.load(open(os.path.join(GOLDEN, "geometry_cases.json")))["cases"]
+    for c in cases:
+        got = O.affine_params_from_geometry(c["w_cols"], c["s_cols"], c["in_dim"])
+        want = None if c["bits"] is None else (c["bits"], c["group_size"])
+        assert got == want, c["name"]
+    assert O.affine_params_from_geometry(512, 64, 4096) == (4, 64)
+    assert O.affine_params_from_geometry(1024, 64, 4096) == (8, 64)
