@@ -187,3 +187,41 @@ def test_fill_randn_matches_oracle_stream(dev):
     ref = O.randn(4097, 1234)
     got = t.cpu().numpy()
     assert np.max(np.abs(got - ref)) <= 1e-6
+
+
+PREFILL_CASES = [(33, 64, 256), (128, 256, 512), (257, 300, 1024), (512, 520, 2048),
+                 (640, 256, 4096)]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("M,N,K", PREFILL_CASES)
+def test_prefill_qmm(dev, M, N, K, bits, gs):
+    """Large-M path (MFMA GEMM with the dequantized weight tile staged in LDS)."""
+    _print_case(t="prefill", M=M, N=N, K=K, bits=bits, gs=gs)
+    wq, s, b = weights(1, N, K, bits, gs, 5000 + M)
+    x = O.make_x_bf16(M, K, 6000 + N)
+    y = mi_qmm.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(wq[0], dev),
+                                to_dev_bf16(s[0], dev), to_dev_bf16(b[0], dev), True, gs, bits)
+    truth = O.qmm_f64(x, wq[0], s[0], b[0], gs, bits)
+    assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
+def test_prefill_full_size_sampled_rows(dev, N, K):
+    """configs[2] shapes at M=2048: 48 sampled output rows against the oracle, and the
+    whole output against a torch fp32 GEMM on the exactly dequantized weight."""
+    _print_case(t="prefill_full", N=N, K=K)
+    M = 2048
+    wq, s, b = weights(1, N, K, 4, 64, 7000 + N)
+    x = O.make_x_bf16(M, K, 7100 + N)
+    W, S, B = to_dev_u32(wq[0], dev), to_dev_bf16(s[0], dev), to_dev_bf16(b[0], dev)
+    xd = to_dev_bf16(x, dev)
+    y = mi_qmm.quantized_matmul(xd, W, S, B, True, 64, 4)
+    rows = np.random.default_rng(N).choice(M, 48, replace=False)
+    truth = O.qmm_f64(x[rows], wq[0], s[0], b[0], 64, 4)
+    assert max_err_ratio(to_f64(y)[rows], truth) <= BF16_TOL
+    wf = mi_qmm.dequantize(W, S, B, 64, 4, dtype=torch.float32)
+    ref = xd.float() @ wf.t()
+    err = (y.float() - ref).abs().max().item() / ref.abs().max().item()
+    assert err <= BF16_TOL
