@@ -13,6 +13,8 @@
 //   - 8 waves in a 2 (M) x 4 (N) grid; each wave owns BM/2 x 64 outputs as 32x32 tiles of
 //     v_mfma_f32_32x32x16_bf16.
 // Double-buffered LDS (A and B) with one barrier per K step.
+#include <cstdlib>
+
 #include "mi_internal.h"
 #include "qmv_common.h"
 
@@ -20,10 +22,12 @@ namespace mi {
 namespace {
 
 using qmv_detail::mfma32;
+using qmv_detail::vmcnt_imm;
+using qmv_detail::lds_barrier;
 
 constexpr int kBN = 256;       // weight rows (output columns) per block
 constexpr int kBK = 64;        // K per step
-constexpr int kThreads = 512;  // 8 waves
+constexpr int kThreads = 256;  // 4 waves, one per SIMD
 constexpr int kRowBytes = kBK * 2;  // one LDS row: 64 bf16 = 8 slots of 16 bytes
 
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -42,27 +46,28 @@ MI_DEV void dma16(const void* src, unsigned char* lds) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
 }
 
-// LDS byte offset of 16-byte slot `c` (0..7) of row `r` in a [rows][64 bf16] tile.
-MI_DEV int swz(int r, int c) { return r * kRowBytes + ((c ^ (r & 7)) << 4); }
+// LDS byte offset of 16-byte slot `c` (0..7) of row `r` in a [rows][64 bf16] tile. A
+// 16-byte read serves 16 lanes per pass over 64 banks (256 B); with slot c ^ ((r>>1)&7) the
+// 16 consecutive rows a fragment read touches fall in 16 distinct bank quads.
+MI_DEV int swz(int r, int c) { return r * kRowBytes + ((c ^ ((r >> 1) & 7)) << 4); }
 
-template <int BITS>
+template <int BITS, int TN>
 struct WRegs {
-  static constexpr int kWords = 32 * BITS / 32;  // packed words for 32 values
-  uint32_t q[kWords];
-  uint32_t s, b;  // bf16 bits of the scale and bias
+  static constexpr int kWords = BITS;  // packed words for 32 values of one row
+  uint32_t q[TN][kWords];
+  uint32_t s[TN], b[TN];  // bf16 bits of the group's scale and bias
 };
 
 template <int BITS, int GS, int BM>
-__global__ void __launch_bounds__(kThreads) qmm_kernel(QmmParams P) {
-  constexpr int WM = BM / 2;       // wave tile rows (M)
-  constexpr int TM = WM / 32;      // 32-row MFMA tiles per wave
-  constexpr int TN = 2;            // 32-col MFMA tiles per wave (wave tile 64 wide)
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+qmm_kernel(QmmParams P) {
+  constexpr int TM = BM / 32;  // 32-row MFMA tiles per wave (the wave covers all BM rows)
+  constexpr int TN = 2;        // 32-column MFMA tiles per wave (64 weight rows)
   constexpr int PF = 32 / BITS;
   constexpr int ABYTES = BM * kRowBytes;
-  constexpr int BBYTES = kBN * kRowBytes;
-  extern __shared__ __align__(16) unsigned char smem[];
-  unsigned char* abuf = smem;                 // [2][BM][128 B]
-  unsigned char* bbuf = smem + 2 * ABYTES;    // [2][256][128 B]
+  constexpr int A_INSTR = ABYTES / (kThreads * 16);  // DMA instructions per thread per step
+  constexpr int W_OPS = TN * (BITS / 4) + 2 * TN;     // vector-memory ops of one W prefetch
+  extern __shared__ __align__(16) unsigned char smem[];  // [3][BM][128 B] x tiles
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -75,79 +80,68 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(QmmParams P) {
   const int m0 = mt * BM, n0 = nt * kBN;
   const int nsteps = K / kBK;
 
-  // ---- A (x) DMA plan: a wave instruction moves 8 rows x 128 B.
-  constexpr int A_INSTR = BM * kRowBytes / (kThreads * 16);  // per thread per step
-  const uint16_t* xa[A_INSTR];
-  int a_lds[A_INSTR];
+  // ---- x: a wave DMA instruction moves 8 rows x 128 B; slot s of row r holds chunk s^(r&7).
+  // 32-bit element offsets from the uniform base (x is below 2^31 bytes, checked on host).
+  uint32_t xo[A_INSTR];
 #pragma unroll
   for (int i = 0; i < A_INSTR; ++i) {
     const int r = (wave * A_INSTR + i) * 8 + (lane >> 3);
-    const int slot = lane & 7;
-    const int c = slot ^ (r & 7);  // logical chunk that lands in this slot
-    const int gm = min(m0 + r, M - 1);
-    xa[i] = P.x + (int64_t)gm * K + c * 8;
-    a_lds[i] = (wave * A_INSTR + i) * 8 * kRowBytes;  // wave-uniform base of the 1 KiB run
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    xo[i] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K + c * 8;
   }
-  auto issue_a = [&](int step, int buf) {
+  auto issue_a = [&](int step, int slot) {
+    unsigned char* dst = smem + slot * ABYTES + wave * A_INSTR * 8 * kRowBytes;
 #pragma unroll
-    for (int i = 0; i < A_INSTR; ++i)
-      dma16(xa[i] + step * kBK, abuf + buf * ABYTES + a_lds[i]);
+    for (int i = 0; i < A_INSTR; ++i) dma16(P.x + (xo[i] + step * kBK), dst + i * 8 * kRowBytes);
   };
 
-  // ---- B (w) plan: thread -> (row, half of the 64-wide step).
-  const int wr = tid >> 1, half = tid & 1;
-  const int gn = min(n0 + wr, N - 1);
-  const uint32_t* wrow = P.w + (int64_t)gn * (K / PF) + half * (32 / PF);
-  const uint16_t* srow = P.scales + (int64_t)gn * G;
-  const uint16_t* brow = P.biases + (int64_t)gn * G;
-  auto load_w = [&](int step, WRegs<BITS>& R) {
-    const uint32_t* p = wrow + step * (kBK / PF);
+  // ---- w: the MFMA k-slots of lane l at k-step ks (0..3) are mapped to the step's
+  // columns 32*(l/32) + 8*ks .. +8 for both operands, so a lane's B operands for a whole
+  // 64-wide step are the 32 consecutive values [32*(l/32), +32) of one weight row.
+  const int fr = lane & 31, fk = lane >> 5;
+  // 32-bit word / group offsets from the uniform bases (sizes checked on host).
+  uint32_t wo[TN], so[TN];
 #pragma unroll
-    for (int i = 0; i < R.kWords / 4; ++i) {
-      u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p) + i);
-      R.q[4 * i] = v.x; R.q[4 * i + 1] = v.y; R.q[4 * i + 2] = v.z; R.q[4 * i + 3] = v.w;
+  for (int j = 0; j < TN; ++j) {
+    const uint32_t n = (uint32_t)min(n0 + wave * 64 + j * 32 + fr, N - 1);
+    wo[j] = n * (uint32_t)(K / PF) + fk * (32 / PF);
+    so[j] = n * (uint32_t)G;
+  }
+  auto load_w = [&](int step, WRegs<BITS, TN>& R) {
+    const uint32_t g = (uint32_t)(step * kBK + fk * 32) / GS;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(P.w + (wo[j] + step * (kBK / PF)));
+#pragma unroll
+      for (int i = 0; i < BITS / 4; ++i) {
+        u32x4_t v = p[i];
+        R.q[j][4 * i] = v.x; R.q[j][4 * i + 1] = v.y;
+        R.q[j][4 * i + 2] = v.z; R.q[j][4 * i + 3] = v.w;
+      }
+      R.s[j] = P.scales[so[j] + g];
+      R.b[j] = P.biases[so[j] + g];
     }
-    const int g = (step * kBK + half * 32) / GS;
-    R.s = srow[g];
-    R.b = brow[g];
   };
-  auto store_w = [&](const WRegs<BITS>& R, int buf) {
-    const float s = bf16_bits_to_f32(R.s), b = bf16_bits_to_f32(R.b);
-    uint32_t o[16];
+  // Dequantize values [8*ks, 8*ks+8) of a lane's 32 into one MFMA B operand (k order).
+  auto dequant = [&](const WRegs<BITS, TN>& R, int j, int ks) -> u32x4_t {
+    const float sc = bf16_bits_to_f32(R.s[j]), bi = bf16_bits_to_f32(R.b[j]);
+    u32x4_t o;
     if constexpr (BITS == 4) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = R.q[i] & 0x0F0F0F0Fu, hi = (R.q[i] >> 4) & 0x0F0F0F0Fu;
-        // values 8i..8i+7 are lo.b0, hi.b0, lo.b1, hi.b1, ...
-        o[4 * i + 0] = pack_bf16x2(fmaf(s, ubyte<0>(lo), b),
-                                   fmaf(s, ubyte<0>(hi), b));
-        o[4 * i + 1] = pack_bf16x2(fmaf(s, ubyte<1>(lo), b),
-                                   fmaf(s, ubyte<1>(hi), b));
-        o[4 * i + 2] = pack_bf16x2(fmaf(s, ubyte<2>(lo), b),
-                                   fmaf(s, ubyte<2>(hi), b));
-        o[4 * i + 3] = pack_bf16x2(fmaf(s, ubyte<3>(lo), b),
-                                   fmaf(s, ubyte<3>(hi), b));
-      }
+      const uint32_t lo = R.q[j][ks] & 0x0F0F0F0Fu, hi = (R.q[j][ks] >> 4) & 0x0F0F0F0Fu;
+      o.x = pack_bf16x2(fmaf(sc, ubyte<0>(lo), bi), fmaf(sc, ubyte<0>(hi), bi));
+      o.y = pack_bf16x2(fmaf(sc, ubyte<1>(lo), bi), fmaf(sc, ubyte<1>(hi), bi));
+      o.z = pack_bf16x2(fmaf(sc, ubyte<2>(lo), bi), fmaf(sc, ubyte<2>(hi), bi));
+      o.w = pack_bf16x2(fmaf(sc, ubyte<3>(lo), bi), fmaf(sc, ubyte<3>(hi), bi));
     } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t w = R.q[i];
-        o[2 * i + 0] = pack_bf16x2(fmaf(s, ubyte<0>(w), b),
-                                   fmaf(s, ubyte<1>(w), b));
-        o[2 * i + 1] = pack_bf16x2(fmaf(s, ubyte<2>(w), b),
-                                   fmaf(s, ubyte<3>(w), b));
-      }
+      const uint32_t w0 = R.q[j][2 * ks], w1 = R.q[j][2 * ks + 1];
+      o.x = pack_bf16x2(fmaf(sc, ubyte<0>(w0), bi), fmaf(sc, ubyte<1>(w0), bi));
+      o.y = pack_bf16x2(fmaf(sc, ubyte<2>(w0), bi), fmaf(sc, ubyte<3>(w0), bi));
+      o.z = pack_bf16x2(fmaf(sc, ubyte<0>(w1), bi), fmaf(sc, ubyte<1>(w1), bi));
+      o.w = pack_bf16x2(fmaf(sc, ubyte<2>(w1), bi), fmaf(sc, ubyte<3>(w1), bi));
     }
-    unsigned char* dst = bbuf + buf * BBYTES;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      u32x4_t v = {o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
-      *reinterpret_cast<u32x4_t*>(dst + swz(wr, half * 4 + j)) = v;
-    }
+    return o;
   };
 
-  // ---- MFMA plan: wave (wm, wn) owns rows [wm*WM, +WM) x cols [wn*64, +64) of the tile.
-  const int wm = wave >> 2, wn = wave & 3;
   f32x16_t acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -156,69 +150,91 @@ __global__ void __launch_bounds__(kThreads) qmm_kernel(QmmParams P) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int fr = lane & 31, fk = lane >> 5;  // fragment row, k half (8 values)
-  auto compute = [&](int buf) {
-    const unsigned char* A = abuf + buf * ABYTES;
-    const unsigned char* B = bbuf + buf * BBYTES;
+  // One 64-wide step: k-step ks runs its TM*TN MFMAs while the A fragments and the
+  // dequantized B operands of k-step ks+1 are produced; scheduling groups interleave
+  // them (1 MFMA : 4 VALU : 1 LDS read) so LDS latency and dequant hide under the MFMAs.
+  auto compute = [&](int step, const WRegs<BITS, TN>& R) {
+    const unsigned char* A = smem + (step % 3) * ABYTES;
+    u32x4_t a[2][TM], bop[2][TN];
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int c = 2 * ks + fk;
-      u32x4_t a[TM], b[TN];
+    for (int i = 0; i < TM; ++i)
+      a[0][i] = *reinterpret_cast<const u32x4_t*>(A + swz(i * 32 + fr, 4 * fk));
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int r = wm * WM + i * 32 + fr;
-        a[i] = *reinterpret_cast<const u32x4_t*>(A + swz(r, c));
-      }
+    for (int j = 0; j < TN; ++j) bop[0][j] = dequant(R, j, 0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int r = wn * 64 + j * 32 + fr;
-        b[j] = *reinterpret_cast<const u32x4_t*>(B + swz(r, c));
+    for (int ks = 0; ks < 4; ++ks) {
+      const int cur = ks & 1, nxt = cur ^ 1;
+      if (ks + 1 < 4) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          a[nxt][i] = *reinterpret_cast<const u32x4_t*>(A + swz(i * 32 + fr, 4 * fk + ks + 1));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bop[nxt][j] = dequant(R, j, ks + 1);
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(a[cur][i], bop[cur][j], acc[i][j]);
+      if (ks + 1 < 4) {
+#pragma unroll
+        for (int m = 0; m < TM * TN; ++m) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+          if (m % TN == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // ---- pipeline
-  WRegs<BITS> R;
-  load_w(0, R);
+  // ---- pipeline: x two steps ahead in a 3-deep LDS ring, w two steps ahead in registers.
+  // Prefetches are unconditional (clamped to the last step) so the number of memory
+  // operations in flight is the same on every iteration and the waits stay exact.
+  WRegs<BITS, TN> R0, R1;
+  load_w(0, R0);
   issue_a(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) & lgkmcnt(0)
-  store_w(R, 0);
-  __syncthreads();
-  for (int step = 0; step < nsteps; ++step) {
-    const int buf = step & 1;
-    const bool more = step + 1 < nsteps;
-    if (more) {
-      load_w(step + 1, R);
-      issue_a(step + 1, buf ^ 1);
-    }
-    compute(buf);
-    if (more) store_w(R, buf ^ 1);  // waits for the loads (and the DMA) of step + 1
-    __syncthreads();
+  load_w(min(1, nsteps - 1), R1);
+  issue_a(min(1, nsteps - 1), 1);
+  auto body = [&](int step, WRegs<BITS, TN>& Rc) {
+    // x of `step` landed (only the next step's prefetch may still be in flight), and
+    // every wave is done with the ring slot the step + 2 prefetch overwrites.
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(W_OPS + A_INSTR));
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    compute(step, Rc);
+    const int pf = min(step + 2, nsteps - 1);
+    load_w(pf, Rc);
+    issue_a(pf, (step + 2) % 3);
+  };
+  int step = 0;
+  for (; step + 1 < nsteps; step += 2) {
+    body(step, R0);
+    body(step + 1, R1);
   }
+  if (step < nsteps) body(step, R0);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no DMA may outlive the block
 
   // ---- epilogue: C reg r of a 32x32 tile is row 8(r/4) + 4(lane/32) + r%4, col lane%32.
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + wave * 64 + j * 32 + fr;
+    if (n >= N) continue;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + wn * 64 + j * 32 + fr;
-      if (n >= N) continue;
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+        const int m = m0 + i * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
         if (m < M) P.y[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[i][j][r]);
       }
-    }
+  }
 }
 
 template <int BITS, int GS, int BM>
 hipError_t launch_bm(const QmmParams& P, hipStream_t s) {
   const int mtiles = (P.M + BM - 1) / BM, ntiles = (P.N + kBN - 1) / kBN;
-  const size_t lds = 2 * (size_t)BM * kRowBytes + 2 * (size_t)kBN * kRowBytes;
+  const size_t lds = 3 * (size_t)BM * kRowBytes;
   auto k = qmm_kernel<BITS, GS, BM>;
   static bool attr = false;
   if (!attr) {
@@ -235,7 +251,12 @@ template <int BITS, int GS>
 hipError_t launch_gs(const QmmParams& P, hipStream_t s) {
   // 128-row tiles when 256-row tiles would leave CUs idle.
   const int64_t big = (int64_t)((P.M + 255) / 256) * ((P.N + kBN - 1) / kBN);
-  return big >= 240 ? launch_bm<BITS, GS, 256>(P, s) : launch_bm<BITS, GS, 128>(P, s);
+  static const int forced = [] {
+    const char* v = std::getenv("MI_QMM_BM");
+    return v ? std::atoi(v) : 0;
+  }();
+  const bool use256 = forced ? forced == 256 : big >= 240;
+  return use256 ? launch_bm<BITS, GS, 256>(P, s) : launch_bm<BITS, GS, 128>(P, s);
 }
 
 }  // namespace
@@ -244,6 +265,9 @@ bool qmm_supported(int M, int N, int K, int bits, int gs) {
   (void)N;
   if (bits != 4 && bits != 8) return false;
   if (gs != 32 && gs != 64 && gs != 128) return false;
+  // 32-bit in-kernel offsets: x, packed w and scales must each stay below 2^31 bytes.
+  if ((int64_t)M * K * 2 >= ((int64_t)1 << 31) || (int64_t)N * K * bits / 8 >= ((int64_t)1 << 31))
+    return false;
   return M >= 1 && K % kBK == 0 && K % gs == 0;
 }
 
