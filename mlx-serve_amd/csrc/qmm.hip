@@ -51,11 +51,18 @@ MI_DEV void dma16(const void* src, unsigned char* lds) {
 // 16 consecutive rows a fragment read touches fall in 16 distinct bank quads.
 MI_DEV int swz(int r, int c) { return r * kRowBytes + ((c ^ ((r >> 1) & 7)) << 4); }
 
-template <int BITS, int TN>
+// Sub-steps (64-wide K steps) per super-step: a lane's packed weights for one super-step
+// are 64 contiguous bytes of one row.
+template <int BITS>
+constexpr int kSubSteps = BITS == 4 ? 4 : 2;
+
+template <int BITS, int GS, int TN>
 struct WRegs {
-  static constexpr int kWords = BITS;  // packed words for 32 values of one row
+  static constexpr int SS = kSubSteps<BITS>;
+  static constexpr int kWords = 16;                          // 64 bytes per row
+  static constexpr int kGroups = (SS * 32) / GS > 0 ? (SS * 32) / GS : 1;
   uint32_t q[TN][kWords];
-  uint32_t s[TN], b[TN];  // bf16 bits of the group's scale and bias
+  uint32_t s[TN][kGroups], b[TN][kGroups];  // bf16 bits of scales / biases
 };
 
 template <int BITS, int GS, int BM>
@@ -64,9 +71,14 @@ qmm_kernel(QmmParams P) {
   constexpr int TM = BM / 32;  // 32-row MFMA tiles per wave (the wave covers all BM rows)
   constexpr int TN = 2;        // 32-column MFMA tiles per wave (64 weight rows)
   constexpr int PF = 32 / BITS;
+  constexpr int SS = kSubSteps<BITS>;
+  constexpr int SSK = SS * kBK;       // K per super-step
+  constexpr int LV = SS * 32;         // values of one row a lane owns per super-step
+  using R_t = WRegs<BITS, GS, TN>;
+  constexpr int NG = R_t::kGroups;
   constexpr int ABYTES = BM * kRowBytes;
   constexpr int A_INSTR = ABYTES / (kThreads * 16);  // DMA instructions per thread per step
-  constexpr int W_OPS = TN * (BITS / 4) + 2 * TN;     // vector-memory ops of one W prefetch
+  constexpr int W_OPS = TN * 4 + 2 * TN * NG;         // vector-memory ops of one W prefetch
   extern __shared__ __align__(16) unsigned char smem[];  // [3][BM][128 B] x tiles
 
   const int tid = threadIdx.x;
@@ -79,61 +91,71 @@ qmm_kernel(QmmParams P) {
   const int mt = blockIdx.x % mtiles, nt = blockIdx.x / mtiles;
   const int m0 = mt * BM, n0 = nt * kBN;
   const int nsteps = K / kBK;
+  const int nsup = K / SSK;
 
-  // ---- x: a wave DMA instruction moves 8 rows x 128 B; slot s of row r holds chunk s^(r&7).
-  // 32-bit element offsets from the uniform base (x is below 2^31 bytes, checked on host).
+  // K order. The MFMA k-slots [8*(l/32), +8) of lane l at k-step ks (0..3) of sub-step t of
+  // super-step T stand for columns SSK*T + LV*(l/32) + 32*t + 8*ks .. +8, for both operands.
+  // So a lane's B operands for a whole super-step are LV consecutive values of one weight
+  // row (64 bytes), and x tile chunk c (h = c/4, ks = c%4) of sub-step t holds columns
+  // SSK*T + LV*h + 32*t + 8*ks.
+  // ---- x: a wave DMA instruction moves 8 rows x 128 B; slot s of row r holds chunk
+  // s ^ ((r>>1)&7). 32-bit element offsets (x below 2^31 bytes, checked on host).
   uint32_t xo[A_INSTR];
 #pragma unroll
   for (int i = 0; i < A_INSTR; ++i) {
     const int r = (wave * A_INSTR + i) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
-    xo[i] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K + c * 8;
+    xo[i] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K + LV * (c >> 2) + 8 * (c & 3);
   }
   auto issue_a = [&](int step, int slot) {
     unsigned char* dst = smem + slot * ABYTES + wave * A_INSTR * 8 * kRowBytes;
+    const uint32_t ko = (uint32_t)((step / SS) * SSK + (step % SS) * 32);
 #pragma unroll
-    for (int i = 0; i < A_INSTR; ++i) dma16(P.x + (xo[i] + step * kBK), dst + i * 8 * kRowBytes);
+    for (int i = 0; i < A_INSTR; ++i) dma16(P.x + (xo[i] + ko), dst + i * 8 * kRowBytes);
   };
 
-  // ---- w: the MFMA k-slots of lane l at k-step ks (0..3) are mapped to the step's
-  // columns 32*(l/32) + 8*ks .. +8 for both operands, so a lane's B operands for a whole
-  // 64-wide step are the 32 consecutive values [32*(l/32), +32) of one weight row.
+  // ---- w: 32-bit word / group offsets from the uniform bases (sizes checked on host).
   const int fr = lane & 31, fk = lane >> 5;
-  // 32-bit word / group offsets from the uniform bases (sizes checked on host).
   uint32_t wo[TN], so[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const uint32_t n = (uint32_t)min(n0 + wave * 64 + j * 32 + fr, N - 1);
-    wo[j] = n * (uint32_t)(K / PF) + fk * (32 / PF);
+    wo[j] = n * (uint32_t)(K / PF) + fk * (LV / PF);
     so[j] = n * (uint32_t)G;
   }
-  auto load_w = [&](int step, WRegs<BITS, TN>& R) {
-    const uint32_t g = (uint32_t)(step * kBK + fk * 32) / GS;
+  auto load_w = [&](int sup, R_t& R) {
+    const uint32_t g0 = (uint32_t)(sup * SSK + fk * LV) / GS;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(P.w + (wo[j] + step * (kBK / PF)));
+      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(P.w + (wo[j] + sup * (SSK / PF)));
 #pragma unroll
-      for (int i = 0; i < BITS / 4; ++i) {
+      for (int i = 0; i < 4; ++i) {
         u32x4_t v = p[i];
         R.q[j][4 * i] = v.x; R.q[j][4 * i + 1] = v.y;
         R.q[j][4 * i + 2] = v.z; R.q[j][4 * i + 3] = v.w;
       }
-      R.s[j] = P.scales[so[j] + g];
-      R.b[j] = P.biases[so[j] + g];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        R.s[j][g] = P.scales[so[j] + g0 + g];
+        R.b[j][g] = P.biases[so[j] + g0 + g];
+      }
     }
   };
-  // Dequantize values [8*ks, 8*ks+8) of a lane's 32 into one MFMA B operand (k order).
-  auto dequant = [&](const WRegs<BITS, TN>& R, int j, int ks) -> u32x4_t {
-    const float sc = bf16_bits_to_f32(R.s[j]), bi = bf16_bits_to_f32(R.b[j]);
+  // Dequantize the 8 values of sub-step t, k-step ks of tile j into one MFMA B operand.
+  auto dequant = [&](const R_t& R, int j, int t, int ks) -> u32x4_t {
+    constexpr int kPerGroup = GS / 32 > 0 ? GS / 32 : 1;  // sub-steps per group
+    const int g = NG == 1 ? 0 : t / kPerGroup;
+    const float sc = bf16_bits_to_f32(R.s[j][g]), bi = bf16_bits_to_f32(R.b[j][g]);
     u32x4_t o;
     if constexpr (BITS == 4) {
-      const uint32_t lo = R.q[j][ks] & 0x0F0F0F0Fu, hi = (R.q[j][ks] >> 4) & 0x0F0F0F0Fu;
+      const uint32_t w = R.q[j][4 * t + ks];
+      const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
       o.x = pack_bf16x2(fmaf(sc, ubyte<0>(lo), bi), fmaf(sc, ubyte<0>(hi), bi));
       o.y = pack_bf16x2(fmaf(sc, ubyte<1>(lo), bi), fmaf(sc, ubyte<1>(hi), bi));
       o.z = pack_bf16x2(fmaf(sc, ubyte<2>(lo), bi), fmaf(sc, ubyte<2>(hi), bi));
       o.w = pack_bf16x2(fmaf(sc, ubyte<3>(lo), bi), fmaf(sc, ubyte<3>(hi), bi));
     } else {
-      const uint32_t w0 = R.q[j][2 * ks], w1 = R.q[j][2 * ks + 1];
+      const uint32_t w0 = R.q[j][8 * t + 2 * ks], w1 = R.q[j][8 * t + 2 * ks + 1];
       o.x = pack_bf16x2(fmaf(sc, ubyte<0>(w0), bi), fmaf(sc, ubyte<1>(w0), bi));
       o.y = pack_bf16x2(fmaf(sc, ubyte<2>(w0), bi), fmaf(sc, ubyte<3>(w0), bi));
       o.z = pack_bf16x2(fmaf(sc, ubyte<0>(w1), bi), fmaf(sc, ubyte<1>(w1), bi));
@@ -150,17 +172,17 @@ qmm_kernel(QmmParams P) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // One 64-wide step: k-step ks runs its TM*TN MFMAs while the A fragments and the
-  // dequantized B operands of k-step ks+1 are produced; scheduling groups interleave
-  // them (1 MFMA : 4 VALU : 1 LDS read) so LDS latency and dequant hide under the MFMAs.
-  auto compute = [&](int step, const WRegs<BITS, TN>& R) {
+  // One sub-step: k-step ks runs its TM*TN MFMAs while the A fragments and the dequantized
+  // B operands of k-step ks+1 are produced; scheduling groups interleave them
+  // (1 MFMA : 4 VALU : 1 LDS read) so LDS latency and dequant hide under the MFMAs.
+  auto compute = [&](int step, int t, const R_t& R) {
     const unsigned char* A = smem + (step % 3) * ABYTES;
     u32x4_t a[2][TM], bop[2][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
       a[0][i] = *reinterpret_cast<const u32x4_t*>(A + swz(i * 32 + fr, 4 * fk));
 #pragma unroll
-    for (int j = 0; j < TN; ++j) bop[0][j] = dequant(R, j, 0);
+    for (int j = 0; j < TN; ++j) bop[0][j] = dequant(R, j, t, 0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -170,7 +192,7 @@ qmm_kernel(QmmParams P) {
         for (int i = 0; i < TM; ++i)
           a[nxt][i] = *reinterpret_cast<const u32x4_t*>(A + swz(i * 32 + fr, 4 * fk + ks + 1));
 #pragma unroll
-        for (int j = 0; j < TN; ++j) bop[nxt][j] = dequant(R, j, ks + 1);
+        for (int j = 0; j < TN; ++j) bop[nxt][j] = dequant(R, j, t, ks + 1);
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
@@ -188,32 +210,36 @@ qmm_kernel(QmmParams P) {
     }
   };
 
-  // ---- pipeline: x two steps ahead in a 3-deep LDS ring, w two steps ahead in registers.
-  // Prefetches are unconditional (clamped to the last step) so the number of memory
-  // operations in flight is the same on every iteration and the waits stay exact.
-  WRegs<BITS, TN> R0, R1;
+  // ---- pipeline: x two sub-steps ahead in a 3-deep LDS ring (DMA), w one super-step
+  // ahead in registers. Prefetches are unconditional (clamped to the last step) so the
+  // number of memory operations in flight follows the same pattern every super-step and
+  // the waits stay exact.
+  R_t R0, R1;
   load_w(0, R0);
   issue_a(0, 0);
-  load_w(min(1, nsteps - 1), R1);
   issue_a(min(1, nsteps - 1), 1);
-  auto body = [&](int step, WRegs<BITS, TN>& Rc) {
-    // x of `step` landed (only the next step's prefetch may still be in flight), and
-    // every wave is done with the ring slot the step + 2 prefetch overwrites.
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(W_OPS + A_INSTR));
-    lds_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    compute(step, Rc);
-    const int pf = min(step + 2, nsteps - 1);
-    load_w(pf, Rc);
-    issue_a(pf, (step + 2) % 3);
+  auto super_step = [&](int sup, R_t& Rc, R_t& Rn) {
+#pragma unroll
+    for (int t = 0; t < SS; ++t) {
+      const int step = sup * SS + t;
+      // x of `step` landed: after its DMA only the next step's DMA (and, one step after a
+      // super-step boundary, the w prefetch issued just before it) may still be in flight.
+      __builtin_amdgcn_sched_barrier(0);
+      if (t == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(A_INSTR + W_OPS));
+      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(A_INSTR));
+      lds_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      if (t == 0) load_w(min(sup + 1, nsup - 1), Rn);
+      compute(step, t, Rc);
+      issue_a(min(step + 2, nsteps - 1), (step + 2) % 3);
+    }
   };
-  int step = 0;
-  for (; step + 1 < nsteps; step += 2) {
-    body(step, R0);
-    body(step + 1, R1);
+  int sup = 0;
+  for (; sup + 1 < nsup; sup += 2) {
+    super_step(sup, R0, R1);
+    super_step(sup + 1, R1, R0);
   }
-  if (step < nsteps) body(step, R0);
+  if (sup < nsup) super_step(sup, R0, R1);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no DMA may outlive the block
 
   // ---- epilogue: C reg r of a 32x32 tile is row 8(r/4) + 4(lane/32) + r%4, col lane%32.
@@ -268,7 +294,7 @@ bool qmm_supported(int M, int N, int K, int bits, int gs) {
   // 32-bit in-kernel offsets: x, packed w and scales must each stay below 2^31 bytes.
   if ((int64_t)M * K * 2 >= ((int64_t)1 << 31) || (int64_t)N * K * bits / 8 >= ((int64_t)1 << 31))
     return false;
-  return M >= 1 && K % kBK == 0 && K % gs == 0;
+  return M >= 1 && K % (kSubSteps<4> * kBK) == 0 && K % gs == 0;
 }
 
 hipError_t launch_qmm(const QmmParams& P, hipStream_t s) {

@@ -189,7 +189,7 @@ def test_fill_randn_matches_oracle_stream(dev):
     assert np.max(np.abs(got - ref)) <= 1e-6
 
 
-PREFILL_CASES = [(33, 64, 256), (128, 256, 512), (257, 300, 1024), (512, 520, 2048),
+PREFILL_CASES = [(33, 64, 256), (128, 256, 512), (257, 300, 1024), (512, 520, 2048), (300, 200, 768),
                  (640, 256, 4096)]
 
 
