@@ -29,6 +29,7 @@ constexpr int kBN = 256;       // weight rows (output columns) per block
 constexpr int kBK = 64;        // K per step
 constexpr int kThreads = 256;  // 4 waves, one per SIMD
 constexpr int kRowBytes = kBK * 2;  // one LDS row: 64 bf16 = 8 slots of 16 bytes
+constexpr int kRing = 4;           // x tiles in the LDS ring (prefetch distance kRing - 1)
 
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -79,7 +80,7 @@ qmm_kernel(QmmParams P) {
   constexpr int ABYTES = BM * kRowBytes;
   constexpr int A_INSTR = ABYTES / (kThreads * 16);  // DMA instructions per thread per step
   constexpr int W_OPS = TN * 4 + 2 * TN * NG;         // vector-memory ops of one W prefetch
-  extern __shared__ __align__(16) unsigned char smem[];  // [3][BM][128 B] x tiles
+  extern __shared__ __align__(16) unsigned char smem[];  // [kRing][BM][128 B] x tiles
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -172,67 +173,99 @@ qmm_kernel(QmmParams P) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // One sub-step: k-step ks runs its TM*TN MFMAs while the A fragments and the dequantized
-  // B operands of k-step ks+1 are produced; scheduling groups interleave them
-  // (1 MFMA : 4 VALU : 1 LDS read) so LDS latency and dequant hide under the MFMAs.
-  auto compute = [&](int step, int t, const R_t& R) {
-    const unsigned char* A = smem + (step % 3) * ABYTES;
-    u32x4_t a[2][TM], bop[2][TN];
+  // Software pipeline over sub-steps. Barrier point B(u) makes x tile u visible and frees
+  // the ring slot of tile u-1; it sits inside sub-step u-1, after the LDS reads of that
+  // sub-step's last k-step were issued and before its last MFMAs, so the first A fragments
+  // and B operands of sub-step u are produced under those MFMAs. Within a sub-step, k-step
+  // ks runs its TM*TN MFMAs while k-step ks+1's fragments are read (front-loaded) and its
+  // B operands dequantized (1 MFMA : 1 LDS read : 3-4 VALU).
+  u32x4_t a[2][TM], bop[2][TN];
+  auto read_a = [&](int step, int ks, u32x4_t (&dst)[TM]) {
+    const unsigned char* A = smem + (step % kRing) * ABYTES;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
-      a[0][i] = *reinterpret_cast<const u32x4_t*>(A + swz(i * 32 + fr, 4 * fk));
+      dst[i] = *reinterpret_cast<const u32x4_t*>(A + swz(i * 32 + fr, 4 * fk + ks));
+  };
+  auto mfmas = [&](const u32x4_t (&av)[TM], const u32x4_t (&bv)[TN]) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) bop[0][j] = dequant(R, j, t, 0);
-    __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int cur = ks & 1, nxt = cur ^ 1;
-      if (ks + 1 < 4) {
+      for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(av[i], bv[j], acc[i][j]);
+  };
+  auto interleave = [&]() {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          a[nxt][i] = *reinterpret_cast<const u32x4_t*>(A + swz(i * 32 + fr, 4 * fk + ks + 1));
-#pragma unroll
-        for (int j = 0; j < TN; ++j) bop[nxt][j] = dequant(R, j, t, ks + 1);
+    for (int m = 0; m < TM * TN; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // MFMA
+      if (m < TM) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
       }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(a[cur][i], bop[cur][j], acc[i][j]);
-      if (ks + 1 < 4) {
-#pragma unroll
-        for (int m = 0; m < TM * TN; ++m) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
-          if (m % TN == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // B(u): wait for x tile u, barrier, then issue x tile u+kRing-1 into the slot tile u-1
+  // used and (when u starts a super-step) the next super-step's weights into the free set.
+  // After tile u's DMA (issued at B(u-kRing+1)) tiles u+1 .. u+kRing-2 and the w prefetches
+  // issued at B(u-kRing+1) .. B(u-1) may still be in flight.
+  auto barrier_point = [&](int u, int tu, R_t& Rfree) {
+    int wv = 0;
+#pragma unroll
+    for (int d = 1; d < kRing; ++d) wv += ((tu - d) % SS + SS) % SS == 0 ? 1 : 0;
+    __builtin_amdgcn_sched_barrier(0);
+    if (wv == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kRing - 2) * A_INSTR));
+    else if (wv == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kRing - 2) * A_INSTR + W_OPS));
+    else if (wv == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm((kRing - 2) * A_INSTR + 2 * W_OPS));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm((kRing - 2) * A_INSTR + 3 * W_OPS));
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue_a(min(u + kRing - 1, nsteps - 1), (u + kRing - 1) % kRing);
+    if (tu == 0) load_w(min(u / SS + 1, nsup - 1), Rfree);
+  };
+  // Sub-step `step` (t = step % SS) with weights Rc; Rn is the other weights set.
+  auto sub_step = [&](int step, int t, R_t& Rc, R_t& Rn) {
+#pragma unroll
+    for (int ks = 0; ks < 3; ++ks) {
+      const int cur = ks & 1, nxt = cur ^ 1;
+      read_a(step, ks + 1, a[nxt]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bop[nxt][j] = dequant(Rc, j, t, ks + 1);
+      mfmas(a[cur], bop[cur]);
+      interleave();
+    }
+    const int u = step + 1;
+    // At a super-step end Rc's last values were dequantized above, so it takes the prefetch.
+    if (t + 1 == SS) {
+      barrier_point(u, 0, Rc);
+      read_a(min(u, nsteps - 1), 0, a[0]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bop[0][j] = dequant(Rn, j, 0, 0);
+    } else {
+      barrier_point(u, t + 1, Rn);
+      read_a(u, 0, a[0]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bop[0][j] = dequant(Rc, j, t + 1, 0);
+    }
+    mfmas(a[1], bop[1]);
+    interleave();
   };
 
-  // ---- pipeline: x two sub-steps ahead in a 3-deep LDS ring (DMA), w one super-step
-  // ahead in registers. Prefetches are unconditional (clamped to the last step) so the
-  // number of memory operations in flight follows the same pattern every super-step and
-  // the waits stay exact.
+  // ---- prologue: w of super-step 0, x tiles 0 .. kRing-2, B(0) (issues the next x tile
+  // and the w of super-step 1), first fragments.
   R_t R0, R1;
   load_w(0, R0);
-  issue_a(0, 0);
-  issue_a(min(1, nsteps - 1), 1);
+#pragma unroll
+  for (int u = 0; u < kRing - 1; ++u) issue_a(min(u, nsteps - 1), u);
+  barrier_point(0, 0, R1);
+  read_a(0, 0, a[0]);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) bop[0][j] = dequant(R0, j, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+
   auto super_step = [&](int sup, R_t& Rc, R_t& Rn) {
 #pragma unroll
-    for (int t = 0; t < SS; ++t) {
-      const int step = sup * SS + t;
-      // x of `step` landed: after its DMA only the next step's DMA (and, one step after a
-      // super-step boundary, the w prefetch issued just before it) may still be in flight.
-      __builtin_amdgcn_sched_barrier(0);
-      if (t == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(A_INSTR + W_OPS));
-      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(A_INSTR));
-      lds_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-      if (t == 0) load_w(min(sup + 1, nsup - 1), Rn);
-      compute(step, t, Rc);
-      issue_a(min(step + 2, nsteps - 1), (step + 2) % 3);
-    }
+    for (int t = 0; t < SS; ++t) sub_step(sup * SS + t, t, Rc, Rn);
   };
   int sup = 0;
   for (; sup + 1 < nsup; sup += 2) {
@@ -241,6 +274,7 @@ qmm_kernel(QmmParams P) {
   }
   if (sup < nsup) super_step(sup, R0, R1);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no DMA may outlive the block
+
 
   // ---- epilogue: C reg r of a 32x32 tile is row 8(r/4) + 4(lane/32) + r%4, col lane%32.
 #pragma unroll
@@ -260,7 +294,7 @@ qmm_kernel(QmmParams P) {
 template <int BITS, int GS, int BM>
 hipError_t launch_bm(const QmmParams& P, hipStream_t s) {
   const int mtiles = (P.M + BM - 1) / BM, ntiles = (P.N + kBN - 1) / kBN;
-  const size_t lds = 3 * (size_t)BM * kRowBytes;
+  const size_t lds = kRing * (size_t)BM * kRowBytes;
   auto k = qmm_kernel<BITS, GS, BM>;
   static bool attr = false;
   if (!attr) {
