@@ -115,6 +115,66 @@ int mi_affine_params_from_geometry(int64_t w_cols, int64_t s_cols, int64_t in_di
 int mi_fill_randn(void* out, int64_t n, uint64_t seed, float mean, float stddev, int dtype,
                   void* stream);
 
+/* ---------------------------------------------------------------- MoE glue ---
+ * The steps on either side of gather_qmm in the reference's MoE layer (moeMLP2,
+ * src/transformer.zig:14822-15192), on the GPU so the grouped launch needs no host sync. */
+
+/* Replaces moeRoutingChain (src/transformer.zig:17022-17072): softmax over E fp32 logits
+ * per token, top-k, weights renormalized over the k selected. inds/scores [T, k]; scores
+ * in scores_dtype (float32, or bfloat16 rounded once). Slots are ordered by descending
+ * logit, ties to the lower expert id (MLX's argpartition leaves the order unspecified).
+ * E <= 1024, k <= min(64, E). */
+int mi_moe_route_topk(uint32_t* inds, void* scores, const float* logits, int64_t T, int64_t E,
+                      int k, int scores_dtype, void* stream);
+
+/* Replaces the sort steps of the sorted MoE path (src/transformer.zig:14965-14993):
+ * order = stable argsort(flat), inv = argsort(order), sorted = flat[order],
+ * lhs = order / k. seg_offsets (may be NULL) receives n_experts+1 entries: the first
+ * sorted position of each expert, then the number of in-range ids. Ids >= n_experts
+ * sort last in index order. One block; n_experts <= 8192. */
+int mi_moe_sort_dispatch(uint32_t* order, uint32_t* inv, uint32_t* sorted, uint32_t* lhs,
+                         uint32_t* seg_offsets, const uint32_t* flat, int64_t n, int k,
+                         int64_t n_experts, void* stream);
+
+/* Replaces mlx_take_axis(axis 0) on row-major rows, as used to undo the expert sort
+ * (src/transformer.zig:15037): out[r] = in[indices[r]]; rows of row_bytes bytes; indices
+ * >= n_src give zero rows. n <= 65535 rows per call. */
+int mi_take_rows(void* out, const void* in, const uint32_t* indices, int64_t n, int64_t n_src,
+                 int64_t row_bytes, void* stream);
+
+/* Replaces fusedSwiGLU (src/transformer.zig:19846-19884): y = bf16(bf16(g*sig(g)) * u),
+ * sig(g) the sigmoid of the bf16 value g rounded to fp32 then bf16 (a table over every
+ * bf16 pattern in the reference). dtype bfloat16 only. */
+int mi_swiglu(void* y, const void* gate, const void* up, int64_t n, int dtype, void* stream);
+
+/* The score-weighted sum over the k slots of each token (src/transformer.zig:15127-15140,
+ * the composed pair gatherQmvDownReduce replicates at :20612-20621):
+ * y[t, n] = sum_{s ascending} bf16(v[t*k+s, n] * score[t*k+s]), each add rounded to
+ * bf16, from bf16 zero. v [T*k, N], scores [T*k], y [T, N]; bfloat16 only. */
+int mi_moe_down_reduce(void* y, const void* v, const void* scores, int64_t T, int k, int64_t N,
+                       int dtype, void* stream);
+
+/* Replaces gatherQmvGateUp (src/transformer.zig:20303-20396): for each token t and slot s,
+ * g = x[t] @ dequant(w_gate[inds[t*k+s]])^T and u likewise, each rounded to bf16, then
+ * y[t*k+s] = swiglu(g, u) exactly as mi_swiglu. x [T, K] bf16, y [T*k, N] bf16. Bit-equal
+ * to two mi_gather_qmm calls followed by mi_swiglu. */
+int mi_gather_qmv_gate_up_swiglu(void* y, const void* x, const uint32_t* w_gate,
+                                 const void* s_gate, const void* b_gate, const uint32_t* w_up,
+                                 const void* s_up, const void* b_up, const uint32_t* inds,
+                                 int64_t T, int k, int64_t N, int64_t K, int64_t n_experts,
+                                 mi_optional_int group_size, mi_optional_int bits,
+                                 const char* mode, void* stream);
+
+/* Replaces gatherQmvDownReduce (src/transformer.zig:20675-20761): v[t*k+s] =
+ * act[t*k+s] @ dequant(w_down[inds[t*k+s]])^T rounded to bf16, then y[t] as
+ * mi_moe_down_reduce. act [T*k, K] bf16, scores [T*k] bf16, y [T, N] bf16. Bit-equal to
+ * mi_gather_qmm followed by mi_moe_down_reduce. */
+int mi_gather_qmv_down_reduce(void* y, const void* act, const uint32_t* w_down,
+                              const void* s_down, const void* b_down, const uint32_t* inds,
+                              const void* scores, int64_t T, int k, int64_t N, int64_t K,
+                              int64_t n_experts, mi_optional_int group_size, mi_optional_int bits,
+                              const char* mode, void* stream);
+
 /* Grow the per-device workspace (sorted work lists, K-split partials) to at least
  * `bytes` ahead of HIP graph capture; calls that fit never allocate. No mlx-c
  * counterpart (MLX owns its allocator). Synchronizes the device when it grows. */

@@ -2,6 +2,8 @@
 // per-stream workspace, error reporting.
 #include "mi_qmm.h"
 
+#include <algorithm>
+
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -192,6 +194,113 @@ QmvPlan qmv16_plan(int N, int K, int gs, int bits, int rows, int64_t n_items, in
 
 bool valid_x_dtype(int d) { return d == MI_DTYPE_BFLOAT16 || d == MI_DTYPE_FLOAT32; }
 
+// One gather_qmm call: validated arguments, kernel parameters and launch plan, and the
+// workspace it needs (work items for sorted runs, then K-split partials).
+struct GatherJob {
+  mi::QmvParams P{};
+  QmvPlan plan{};
+  bool empty = false, narrow = false, use_items = false;
+  int64_t max_items = 0;
+  size_t items_bytes = 0, part_bytes = 0;
+  size_t items_region() const { return ((items_bytes + 255) / 256) * 256; }
+  size_t ws_bytes() const { return items_bytes || part_bytes ? items_region() + part_bytes : 0; }
+};
+
+int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, const void* scales,
+                   const void* biases, const uint32_t* lhs_indices,
+                   const uint32_t* rhs_indices, int64_t n_idx, int64_t lhs_div, int64_t x_batch,
+                   int64_t M, int64_t N, int64_t K, int64_t n_experts, bool transpose,
+                   mi_optional_int group_size, mi_optional_int bits, const char* mode,
+                   bool sorted_indices, int x_dtype, int sb_dtype) {
+  int gs = 0, nb = 0;
+  int rc = resolve_common(group_size, bits, mode, transpose, K, &gs, &nb);
+  if (rc) return rc;
+  if (!valid_x_dtype(x_dtype)) return fail(MI_ERR_UNSUPPORTED, "x dtype %d not supported", x_dtype);
+  if (sb_dtype != MI_DTYPE_BFLOAT16)
+    return fail(MI_ERR_UNSUPPORTED, "scales/biases dtype %d not supported", sb_dtype);
+  if (n_idx < 0 || M < 0 || N < 0 || x_batch < 0 || n_experts < 0 || lhs_div <= 0)
+    return fail(MI_ERR_INVALID, "negative size or lhs_div <= 0");
+  if (n_idx == 0 || M == 0 || N == 0) {
+    J.empty = true;
+    return MI_OK;
+  }
+  if (!y || !x || !w || !scales || !biases) return fail(MI_ERR_INVALID, "null tensor pointer");
+  if (x_batch == 0 || n_experts == 0) return fail(MI_ERR_INVALID, "empty x or weight bank");
+  if (N > (int64_t)1 << 30 || M > (int64_t)1 << 30) return fail(MI_ERR_INVALID, "N or M too large");
+  if (n_idx * M >= ((int64_t)1 << 32)) return fail(MI_ERR_INVALID, "n_idx*M exceeds 2^32");
+
+  mi::QmvParams& P = J.P;
+  P.w = w;
+  P.scales = (const uint16_t*)scales;
+  P.biases = (const uint16_t*)biases;
+  P.x = x;
+  P.y = y;
+  P.lhs = lhs_indices;
+  P.rhs = rhs_indices;
+  P.n_pairs = n_idx;
+  P.lhs_div = lhs_div;
+  P.x_batch = x_batch;
+  P.n_experts = n_experts;
+  P.M = (int)M;
+  P.N = (int)N;
+  P.K = (int)K;
+  P.bits = nb;
+  P.group_size = gs;
+  P.x_f32 = x_dtype == MI_DTYPE_FLOAT32;
+
+  J.use_items = sorted_indices && rhs_indices != nullptr && n_idx > 1;
+  const int64_t PT = n_idx * M;
+  // Decode widths (<= 4 rows per pair, or sorted runs cut into 16-row items) use the
+  // 16-row-tile kernel; wider pairs use the 32-row-tile kernel.
+  static const int narrow_max = env_int("MI_QMM_NARROW_MAX", 4);
+  J.narrow = (J.use_items || M <= narrow_max) && mi::qmv16_supported(P.K, gs, nb);
+  P.rpi = J.narrow ? 16 : 32;
+  const int rows = (int)(M < P.rpi ? M : P.rpi);
+  int64_t n_items;
+  if (!J.use_items) {
+    P.items_per_pair = ceil_div(M, P.rpi);
+    n_items = n_idx * P.items_per_pair;
+    if (n_items > INT32_MAX) return fail(MI_ERR_INVALID, "too many work items");
+    P.n_items_fixed = (int)n_items;
+  } else {
+    // Runs of equal rhs cut into rpi-row chunks; the bound holds for any input order.
+    J.max_items = (PT + P.rpi - 1) / P.rpi + n_idx;
+    const int64_t runs_bound = n_idx < n_experts ? n_idx : n_experts;
+    n_items = (PT + P.rpi - 1) / P.rpi + runs_bound;
+    P.items_per_pair = 1;
+    P.n_items_fixed = 0;
+  }
+  J.plan = J.narrow ? qmv16_plan(P.N, P.K, gs, nb, J.use_items ? P.rpi : rows, n_items, P.x_f32)
+                    : qmv_plan(P.N, P.K, gs, nb, J.use_items ? P.rpi : rows, n_items, P.x_f32);
+  P.ks = J.plan.ks;
+  P.gps = J.plan.gps;
+  P.row_blocks = J.plan.row_blocks;
+  J.items_bytes = J.use_items ? (size_t)J.max_items * 16 + 256 : 0;
+  J.part_bytes = P.ks > 1 ? (size_t)P.ks * PT * N * 4 : 0;
+  return MI_OK;
+}
+
+// Launch a prepared gather on `s`; `ws` holds at least J.ws_bytes() bytes.
+int gather_launch(GatherJob& J, void* ws, hipStream_t s) {
+  mi::QmvParams& P = J.P;
+  if (J.ws_bytes()) {
+    P.part = (float*)((char*)ws + J.items_region());
+    if (J.use_items) {
+      uint32_t* count = (uint32_t*)ws;
+      uint32_t* items = (uint32_t*)((char*)ws + 256);
+      hipError_t e = mi::launch_build_items(P.rhs, P.n_pairs, P.M, P.rpi, items, count,
+                                            J.max_items, s);
+      if (e != hipSuccess) return hip_fail(e, "build_items launch");
+      P.items = items;
+      P.item_count = count;
+    }
+  }
+  hipError_t e = J.narrow ? mi::launch_qmv16(P, J.plan.cfg, s) : mi::launch_qmv(P, J.plan.cfg, s);
+  return e == hipSuccess ? MI_OK : hip_fail(e, "qmv launch");
+}
+
+size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
 }  // namespace
 
 extern "C" {
@@ -229,86 +338,18 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
                   int64_t n_experts, bool transpose, mi_optional_int group_size,
                   mi_optional_int bits, const char* mode, bool sorted_indices, int x_dtype,
                   int sb_dtype, void* stream) {
-  int gs = 0, nb = 0;
-  int rc = resolve_common(group_size, bits, mode, transpose, K, &gs, &nb);
-  if (rc) return rc;
-  if (!valid_x_dtype(x_dtype)) return fail(MI_ERR_UNSUPPORTED, "x dtype %d not supported", x_dtype);
-  if (sb_dtype != MI_DTYPE_BFLOAT16)
-    return fail(MI_ERR_UNSUPPORTED, "scales/biases dtype %d not supported", sb_dtype);
-  if (n_idx < 0 || M < 0 || N < 0 || x_batch < 0 || n_experts < 0 || lhs_div <= 0)
-    return fail(MI_ERR_INVALID, "negative size or lhs_div <= 0");
-  if (n_idx == 0 || M == 0 || N == 0) return MI_OK;
-  if (!y || !x || !w || !scales || !biases) return fail(MI_ERR_INVALID, "null tensor pointer");
-  if (x_batch == 0 || n_experts == 0) return fail(MI_ERR_INVALID, "empty x or weight bank");
-  if (N > (int64_t)1 << 30 || M > (int64_t)1 << 30) return fail(MI_ERR_INVALID, "N or M too large");
-  if (n_idx * M >= ((int64_t)1 << 32)) return fail(MI_ERR_INVALID, "n_idx*M exceeds 2^32");
+  GatherJob J;
+  int rc = gather_prepare(J, y, x, w, scales, biases, lhs_indices, rhs_indices, n_idx, lhs_div,
+                          x_batch, M, N, K, n_experts, transpose, group_size, bits, mode,
+                          sorted_indices, x_dtype, sb_dtype);
+  if (rc || J.empty) return rc;
   hipStream_t s = (hipStream_t)stream;
-
-  mi::QmvParams P{};
-  P.w = w;
-  P.scales = (const uint16_t*)scales;
-  P.biases = (const uint16_t*)biases;
-  P.x = x;
-  P.y = y;
-  P.lhs = lhs_indices;
-  P.rhs = rhs_indices;
-  P.n_pairs = n_idx;
-  P.lhs_div = lhs_div;
-  P.x_batch = x_batch;
-  P.n_experts = n_experts;
-  P.M = (int)M;
-  P.N = (int)N;
-  P.K = (int)K;
-  P.bits = nb;
-  P.group_size = gs;
-  P.x_f32 = x_dtype == MI_DTYPE_FLOAT32;
-
-  const bool use_items = sorted_indices && rhs_indices != nullptr && n_idx > 1;
-  const int64_t PT = n_idx * M;
-  // Decode widths (<= 16 rows per pair, or sorted runs cut into 16-row items) use the
-  // 16-row-tile kernel; 17..32 rows per pair use the 32-row-tile kernel.
-  static const int narrow_max = env_int("MI_QMM_NARROW_MAX", 4);
-  const bool narrow = (use_items || M <= narrow_max) && mi::qmv16_supported(P.K, gs, nb);
-  P.rpi = narrow ? 16 : 32;
-  const int rows = (int)(M < P.rpi ? M : P.rpi);
-  int64_t n_items, max_items = 0;
-  if (!use_items) {
-    P.items_per_pair = ceil_div(M, P.rpi);
-    n_items = n_idx * P.items_per_pair;
-    if (n_items > INT32_MAX) return fail(MI_ERR_INVALID, "too many work items");
-    P.n_items_fixed = (int)n_items;
-  } else {
-    // Runs of equal rhs cut into rpi-row chunks; the bound holds for any input order.
-    max_items = (PT + P.rpi - 1) / P.rpi + n_idx;
-    const int64_t runs_bound = n_idx < n_experts ? n_idx : n_experts;
-    n_items = (PT + P.rpi - 1) / P.rpi + runs_bound;
-    P.items_per_pair = 1;
-    P.n_items_fixed = 0;
-  }
-  QmvPlan plan = narrow ? qmv16_plan(P.N, P.K, gs, nb, use_items ? P.rpi : rows, n_items, P.x_f32)
-                        : qmv_plan(P.N, P.K, gs, nb, use_items ? P.rpi : rows, n_items, P.x_f32);
-  P.ks = plan.ks;
-  P.gps = plan.gps;
-  P.row_blocks = plan.row_blocks;
-  size_t items_bytes = use_items ? (size_t)max_items * 16 + 256 : 0;
-  size_t part_bytes = P.ks > 1 ? (size_t)P.ks * PT * N * 4 : 0;
-  if (items_bytes || part_bytes) {
-    void* data = nullptr;
-    rc = workspace(s, ((items_bytes + 255) / 256) * 256 + part_bytes, &data);
+  void* data = nullptr;
+  if (J.ws_bytes()) {
+    rc = workspace(s, J.ws_bytes(), &data);
     if (rc) return rc;
-    P.part = (float*)((char*)data + ((items_bytes + 255) / 256) * 256);
-    if (use_items) {
-      uint32_t* count = (uint32_t*)data;
-      uint32_t* items = (uint32_t*)((char*)data + 256);
-      hipError_t e = mi::launch_build_items(rhs_indices, n_idx, (int)M, P.rpi, items, count,
-                                            max_items, s);
-      if (e != hipSuccess) return hip_fail(e, "build_items launch");
-      P.items = items;
-      P.item_count = count;
-    }
   }
-  hipError_t e = narrow ? mi::launch_qmv16(P, plan.cfg, s) : mi::launch_qmv(P, plan.cfg, s);
-  return e == hipSuccess ? MI_OK : hip_fail(e, "qmv launch");
+  return gather_launch(J, data, s);
 }
 
 int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
@@ -392,6 +433,130 @@ int mi_fill_randn(void* out, int64_t n, uint64_t seed, float mean, float stddev,
   hipError_t e = mi::launch_randn(out, n, seed, mean, stddev, dtype == MI_DTYPE_FLOAT32,
                                   (hipStream_t)stream);
   return e == hipSuccess ? MI_OK : hip_fail(e, "randn launch");
+}
+
+// ---------------------------------------------------------------- MoE glue --
+
+int mi_moe_route_topk(uint32_t* inds, void* scores, const float* logits, int64_t T, int64_t E,
+                      int k, int scores_dtype, void* stream) {
+  if (scores_dtype != MI_DTYPE_FLOAT32 && scores_dtype != MI_DTYPE_BFLOAT16)
+    return fail(MI_ERR_UNSUPPORTED, "scores dtype %d not supported", scores_dtype);
+  if (T < 0 || E <= 0 || k <= 0) return fail(MI_ERR_INVALID, "bad T/E/k");
+  if (E > 1024 || k > 64 || k > E)
+    return fail(MI_ERR_UNSUPPORTED, "E=%lld k=%d outside E<=1024, k<=min(64,E)", (long long)E, k);
+  if (T == 0) return MI_OK;
+  if (!inds || !scores || !logits) return fail(MI_ERR_INVALID, "null tensor pointer");
+  hipError_t e = mi::launch_route_topk(logits, T, (int)E, k, inds, scores,
+                                       scores_dtype == MI_DTYPE_BFLOAT16, (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : hip_fail(e, "route launch");
+}
+
+int mi_moe_sort_dispatch(uint32_t* order, uint32_t* inv, uint32_t* sorted, uint32_t* lhs,
+                         uint32_t* seg_offsets, const uint32_t* flat, int64_t n, int k,
+                         int64_t n_experts, void* stream) {
+  if (n < 0 || k <= 0 || n_experts <= 0) return fail(MI_ERR_INVALID, "bad n/k/n_experts");
+  if (n_experts > 8192) return fail(MI_ERR_UNSUPPORTED, "n_experts > 8192");
+  if (n >= ((int64_t)1 << 31)) return fail(MI_ERR_INVALID, "n too large");
+  if (n == 0 && !seg_offsets) return MI_OK;
+  if (n > 0 && (!order || !inv || !sorted || !lhs || !flat))
+    return fail(MI_ERR_INVALID, "null tensor pointer");
+  hipError_t e = mi::launch_sort_dispatch(flat, n, k, (int)n_experts, order, inv, sorted, lhs,
+                                          seg_offsets, (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : hip_fail(e, "sort_dispatch launch");
+}
+
+int mi_take_rows(void* out, const void* in, const uint32_t* indices, int64_t n, int64_t n_src,
+                 int64_t row_bytes, void* stream) {
+  if (n < 0 || n_src < 0 || row_bytes < 0) return fail(MI_ERR_INVALID, "negative size");
+  if (n == 0 || row_bytes == 0) return MI_OK;
+  if (!out || !in || !indices) return fail(MI_ERR_INVALID, "null tensor pointer");
+  if (n > 65535) return fail(MI_ERR_UNSUPPORTED, "more than 65535 rows per call");
+  hipError_t e = mi::launch_take_rows(out, in, indices, n, n_src, row_bytes, (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : hip_fail(e, "take_rows launch");
+}
+
+int mi_swiglu(void* y, const void* gate, const void* up, int64_t n, int dtype, void* stream) {
+  if (dtype != MI_DTYPE_BFLOAT16) return fail(MI_ERR_UNSUPPORTED, "dtype %d not supported", dtype);
+  if (n < 0) return fail(MI_ERR_INVALID, "negative n");
+  if (n == 0) return MI_OK;
+  if (!y || !gate || !up) return fail(MI_ERR_INVALID, "null tensor pointer");
+  hipError_t e = mi::launch_swiglu((uint16_t*)y, (const uint16_t*)gate, (const uint16_t*)up, n,
+                                   (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : hip_fail(e, "swiglu launch");
+}
+
+int mi_moe_down_reduce(void* y, const void* v, const void* scores, int64_t T, int k, int64_t N,
+                       int dtype, void* stream) {
+  if (dtype != MI_DTYPE_BFLOAT16) return fail(MI_ERR_UNSUPPORTED, "dtype %d not supported", dtype);
+  if (T < 0 || k <= 0 || N < 0) return fail(MI_ERR_INVALID, "bad T/k/N");
+  if (T == 0 || N == 0) return MI_OK;
+  if (T > 65535) return fail(MI_ERR_UNSUPPORTED, "more than 65535 tokens per call");
+  if (!y || !v || !scores) return fail(MI_ERR_INVALID, "null tensor pointer");
+  hipError_t e = mi::launch_down_reduce((uint16_t*)y, (const uint16_t*)v, (const uint16_t*)scores,
+                                        T, k, N, (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : hip_fail(e, "down_reduce launch");
+}
+
+int mi_gather_qmv_gate_up_swiglu(void* y, const void* x, const uint32_t* w_gate,
+                                 const void* s_gate, const void* b_gate, const uint32_t* w_up,
+                                 const void* s_up, const void* b_up, const uint32_t* inds,
+                                 int64_t T, int k, int64_t N, int64_t K, int64_t n_experts,
+                                 mi_optional_int group_size, mi_optional_int bits,
+                                 const char* mode, void* stream) {
+  if (T < 0 || k <= 0) return fail(MI_ERR_INVALID, "bad T/k");
+  if (!inds && T > 0) return fail(MI_ERR_INVALID, "null indices");
+  const int64_t n_idx = T * k;
+  GatherJob G, U;
+  // Every (token, slot) pair reads its token's row: lhs(i) = i / k.
+  int rc = gather_prepare(G, y, x, w_gate, s_gate, b_gate, nullptr, inds, n_idx, k, T, 1, N, K,
+                          n_experts, true, group_size, bits, mode, false, MI_DTYPE_BFLOAT16,
+                          MI_DTYPE_BFLOAT16);
+  if (rc || G.empty) return rc;
+  rc = gather_prepare(U, y, x, w_up, s_up, b_up, nullptr, inds, n_idx, k, T, 1, N, K, n_experts,
+                      true, group_size, bits, mode, false, MI_DTYPE_BFLOAT16, MI_DTYPE_BFLOAT16);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t half = round256((size_t)n_idx * N * 2);
+  const size_t need = 2 * half + std::max(G.ws_bytes(), U.ws_bytes());
+  void* data = nullptr;
+  rc = workspace(s, need, &data);
+  if (rc) return rc;
+  uint16_t* g = (uint16_t*)data;
+  uint16_t* u = (uint16_t*)((char*)data + half);
+  void* rest = (char*)data + 2 * half;
+  G.P.y = g;
+  U.P.y = u;
+  if ((rc = gather_launch(G, rest, s)) != MI_OK) return rc;
+  if ((rc = gather_launch(U, rest, s)) != MI_OK) return rc;
+  hipError_t e = mi::launch_swiglu((uint16_t*)y, g, u, n_idx * N, s);
+  return e == hipSuccess ? MI_OK : hip_fail(e, "swiglu launch");
+}
+
+int mi_gather_qmv_down_reduce(void* y, const void* act, const uint32_t* w_down,
+                              const void* s_down, const void* b_down, const uint32_t* inds,
+                              const void* scores, int64_t T, int k, int64_t N, int64_t K,
+                              int64_t n_experts, mi_optional_int group_size, mi_optional_int bits,
+                              const char* mode, void* stream) {
+  if (T < 0 || k <= 0) return fail(MI_ERR_INVALID, "bad T/k");
+  if (T > 65535) return fail(MI_ERR_UNSUPPORTED, "more than 65535 tokens per call");
+  if ((!inds || !scores) && T > 0) return fail(MI_ERR_INVALID, "null indices or scores");
+  const int64_t n_idx = T * k;
+  GatherJob D;
+  // act holds one row per (token, slot) pair: lhs(i) = i.
+  int rc = gather_prepare(D, y, act, w_down, s_down, b_down, nullptr, inds, n_idx, 1, n_idx, 1, N,
+                          K, n_experts, true, group_size, bits, mode, false, MI_DTYPE_BFLOAT16,
+                          MI_DTYPE_BFLOAT16);
+  if (rc || D.empty) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t vb = round256((size_t)n_idx * N * 2);
+  void* data = nullptr;
+  rc = workspace(s, vb + D.ws_bytes(), &data);
+  if (rc) return rc;
+  uint16_t* v = (uint16_t*)data;
+  D.P.y = v;
+  if ((rc = gather_launch(D, (char*)data + vb, s)) != MI_OK) return rc;
+  hipError_t e = mi::launch_down_reduce((uint16_t*)y, v, (const uint16_t*)scores, T, k, N, s);
+  return e == hipSuccess ? MI_OK : hip_fail(e, "down_reduce launch");
 }
 
 }  // extern "C"

@@ -53,6 +53,20 @@ hipError_t launch_build_items(const uint32_t* rhs, int64_t n_pairs, int M, int r
                               uint32_t* items, uint32_t* item_count, int64_t max_items,
                               hipStream_t s);
 
+// MoE glue (moe.hip).
+hipError_t launch_route_topk(const float* logits, int64_t T, int E, int k, uint32_t* inds,
+                             void* scores, int scores_bf16, hipStream_t s);
+size_t sort_dispatch_lds_bytes(int E);
+hipError_t launch_sort_dispatch(const uint32_t* flat, int64_t n, int k, int E, uint32_t* order,
+                                uint32_t* inv, uint32_t* sorted, uint32_t* lhs, uint32_t* seg,
+                                hipStream_t s);
+hipError_t launch_take_rows(void* out, const void* in, const uint32_t* idx, int64_t n,
+                            int64_t n_src, int64_t row_bytes, hipStream_t s);
+hipError_t launch_swiglu(uint16_t* y, const uint16_t* g, const uint16_t* u, int64_t n,
+                         hipStream_t s);
+hipError_t launch_down_reduce(uint16_t* y, const uint16_t* v, const uint16_t* scores, int64_t T,
+                              int k, int64_t N, hipStream_t s);
+
 // Prefill GEMM (qmm.hip). Returns hipErrorNotSupported if the shape is not handled.
 struct QmmParams {
   const uint32_t* w;

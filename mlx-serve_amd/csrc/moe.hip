@@ -1,1 +1,294 @@
+// MoE glue around gather_qmm, on the GPU so the grouped launch needs no host sync:
+//   route_topk      softmax top-k routing           (src/transformer.zig:17022-17072)
+//   sort_dispatch   argsort / inverse / lhs = order//k (src/transformer.zig:14965-14993)
+//   take_rows       row gather (mlx_take_axis 0)    (src/transformer.zig:15037)
+//   swiglu          table SwiGLU, bf16 rounding     (src/transformer.zig:19846-19884)
+//   down_reduce     bf16 score product + ascending bf16 sum over slots
+//                                                   (src/transformer.zig:20577-20623)
+#include "mi_common.h"
 #include "mi_internal.h"
+
+namespace mi {
+namespace {
+
+MI_DEV uint16_t bf16_mul(uint16_t a, uint16_t b) {
+  // bf16 x bf16 is exact in fp32; one rounding to bf16.
+  return (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(a) * bf16_bits_to_f32(b));
+}
+
+MI_DEV uint16_t bf16_add(uint16_t a, uint16_t b) {
+  return (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(a) + bf16_bits_to_f32(b));
+}
+
+// Sigmoid of a bf16 value, rounded once to fp32 from a double evaluation and then to
+// bf16: the correctly rounded table value for all but astronomically rare inputs.
+MI_DEV uint16_t sigmoid_bf16(uint16_t g) {
+  const double v = (double)bf16_bits_to_f32(g);
+  const float s = (float)(1.0 / (1.0 + exp(-v)));
+  return (uint16_t)f32_to_bf16_bits(s);
+}
+
+// (value, index) ordering of the top-k selection: larger value first, lower index on
+// ties; NaN logits never win.
+MI_DEV bool better(float va, int ia, float vb, int ib) {
+  if (va != va) return false;
+  if (vb != vb) return true;
+  return va > vb || (va == vb && ia < ib);
+}
+
+template <int NV>
+__global__ void __launch_bounds__(256) route_topk_kernel(const float* __restrict__ logits,
+                                                         int64_t T, int E, int k,
+                                                         uint32_t* __restrict__ inds,
+                                                         void* __restrict__ scores,
+                                                         int scores_bf16) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float* row = logits + t * E;
+  float v[NV];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? row[e] : -INFINITY;
+    mx = fmaxf(mx, v[j]);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  float den = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    if (lane + 64 * j < E) den += expf(v[j] - mx);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o, 64);
+
+  uint32_t taken = 0;
+  uint32_t sel_i = 0;
+  float sel_v = 0.f;
+  for (int r = 0; r < k; ++r) {
+    float bv = NAN;
+    int bi = 0x7FFFFFFF;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E && !(taken >> j & 1u) && better(v[j], e, bv, bi)) {
+        bv = v[j];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (bi == 0x7FFFFFFF) bi = r;  // all-NaN row: fill with distinct ids
+    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+    if (lane == r) {
+      sel_i = (uint32_t)bi;
+      sel_v = bv;
+    }
+  }
+  // Renormalized softmax weights of the selected experts; slot r lives in lane r.
+  float w = lane < k ? expf(sel_v - mx) / den : 0.f;
+  float sum = 0.f;
+  for (int r = 0; r < k; ++r) sum += __shfl(w, r, 64);  // ascending slot order
+  if (lane < k) {
+    inds[t * k + lane] = sel_i;
+    const float sc = w / sum;
+    if (scores_bf16) ((uint16_t*)scores)[t * k + lane] = (uint16_t)f32_to_bf16_bits(sc);
+    else ((float*)scores)[t * k + lane] = sc;
+  }
+}
+
+// Stable counting sort of expert ids by one 1024-thread block. Ids >= E share the
+// last bucket (kept in index order). seg may be null; otherwise seg[e] is the first
+// sorted position of expert e and seg[E] the number of in-range ids.
+constexpr int kSortThreads = 1024;
+
+__global__ void __launch_bounds__(kSortThreads) sort_dispatch_kernel(
+    const uint32_t* __restrict__ flat, int64_t n, int k, int E, uint32_t* __restrict__ order,
+    uint32_t* __restrict__ inv, uint32_t* __restrict__ sorted, uint32_t* __restrict__ lhs,
+    uint32_t* __restrict__ seg) {
+  extern __shared__ uint32_t sh[];  // cnt[E+1] then part[kSortThreads]
+  uint32_t* cnt = sh;
+  uint32_t* part = sh + (E + 1);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int NB = E + 1;
+  for (int b = tid; b < NB; b += kSortThreads) cnt[b] = 0;
+  __syncthreads();
+  for (int64_t i = tid; i < n; i += kSortThreads) {
+    const uint32_t v = flat[i];
+    atomicAdd(&cnt[v < (uint32_t)E ? v : (uint32_t)E], 1u);
+  }
+  __syncthreads();
+  // Exclusive scan of cnt: each thread owns a contiguous run of buckets.
+  const int per = (NB + kSortThreads - 1) / kSortThreads;
+  const int b0 = min(tid * per, NB), b1 = min(b0 + per, NB);
+  uint32_t local = 0;
+  for (int b = b0; b < b1; ++b) local += cnt[b];
+  part[tid] = local;
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t run = 0;
+    for (int i = 0; i < kSortThreads; ++i) {
+      const uint32_t c = part[i];
+      part[i] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  uint32_t run = part[tid];
+  for (int b = b0; b < b1; ++b) {
+    const uint32_t c = cnt[b];
+    cnt[b] = run;  // cnt now holds the next free position of each bucket
+    if (seg) seg[b] = run;
+    run += c;
+  }
+  __syncthreads();
+  // Stable scatter, 1024 ids at a time; waves of a chunk take their turn in order.
+  for (int64_t base = 0; base < n; base += kSortThreads) {
+    const int64_t i = base + tid;
+    const bool valid = i < n;
+    const uint32_t raw = valid ? flat[i] : 0u;
+    const uint32_t b = valid ? (raw < (uint32_t)E ? raw : (uint32_t)E) : 0xFFFFFFFFu;
+    // Lanes of this wave holding the same bucket.
+    uint64_t remaining = __ballot(1);
+    uint64_t peers = 0;
+    while (remaining) {
+      const int leader = __ffsll((unsigned long long)remaining) - 1;
+      const uint32_t lb = __shfl(b, leader, 64);
+      const uint64_t m = __ballot(b == lb);
+      if (b == lb) peers = m;
+      remaining &= ~m;
+    }
+    const int rank = __popcll(peers & ((1ull << lane) - 1ull));
+    const bool lead = rank == 0;
+    for (int w = 0; w < kSortThreads / 64; ++w) {
+      if (wave == w && valid) {
+        const uint32_t start = cnt[b];
+        const uint32_t pos = start + (uint32_t)rank;
+        order[pos] = (uint32_t)i;
+        sorted[pos] = raw;
+        lhs[pos] = (uint32_t)(i / k);
+        inv[i] = pos;
+        if (lead) cnt[b] = start + (uint32_t)__popcll(peers);
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__global__ void take_rows_kernel(void* __restrict__ out, const void* __restrict__ in,
+                                 const uint32_t* __restrict__ idx, int64_t n_src,
+                                 int64_t row_bytes) {
+  const int64_t r = blockIdx.y;
+  const uint32_t src = idx[r];
+  const bool ok = (int64_t)src < n_src;
+  if ((row_bytes & 15) == 0) {
+    const int64_t nv = row_bytes >> 4;
+    u32x4_t* o = (u32x4_t*)((char*)out + r * row_bytes);
+    const u32x4_t* s = (const u32x4_t*)((const char*)in + (int64_t)src * row_bytes);
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < nv;
+         j += (int64_t)gridDim.x * blockDim.x) {
+      u32x4_t z = {0u, 0u, 0u, 0u};
+      o[j] = ok ? s[j] : z;
+    }
+  } else {
+    unsigned char* o = (unsigned char*)out + r * row_bytes;
+    const unsigned char* s = (const unsigned char*)in + (int64_t)src * row_bytes;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < row_bytes;
+         j += (int64_t)gridDim.x * blockDim.x)
+      o[j] = ok ? s[j] : 0;
+  }
+}
+
+__global__ void swiglu_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ g,
+                              const uint16_t* __restrict__ u, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const uint16_t gv = g[i];
+    y[i] = bf16_mul(bf16_mul(gv, sigmoid_bf16(gv)), u[i]);
+  }
+}
+
+// y[t, n] = sum over slots s ascending of bf16(v[t*k+s, n] * score[t*k+s]), each add
+// rounded to bf16, starting from bf16 zero.
+__global__ void down_reduce_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ v,
+                                   const uint16_t* __restrict__ scores, int64_t T, int k,
+                                   int64_t N) {
+  const int64_t t = blockIdx.y;
+  for (int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; n < N;
+       n += (int64_t)gridDim.x * blockDim.x) {
+    uint16_t total = 0;
+    for (int s = 0; s < k; ++s) {
+      const int64_t p = t * k + s;
+      total = bf16_add(total, bf16_mul(v[p * N + n], scores[p]));
+    }
+    y[t * N + n] = total;
+  }
+}
+
+unsigned grid_for(int64_t n, int threads) {
+  int64_t b = (n + threads - 1) / threads;
+  return (unsigned)(b < 1 ? 1 : b > 65535 ? 65535 : b);
+}
+
+}  // namespace
+
+hipError_t launch_route_topk(const float* logits, int64_t T, int E, int k, uint32_t* inds,
+                             void* scores, int scores_bf16, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  const unsigned grid = (unsigned)((T + 3) / 4);
+  const int nv = (E + 63) / 64;
+#define MI_ROUTE(NVV)                                                                      \
+  hipLaunchKernelGGL(route_topk_kernel<NVV>, dim3(grid), dim3(256), 0, s, logits, T, E, k, \
+                     inds, scores, scores_bf16)
+  if (nv <= 1) MI_ROUTE(1);
+  else if (nv <= 2) MI_ROUTE(2);
+  else if (nv <= 4) MI_ROUTE(4);
+  else if (nv <= 8) MI_ROUTE(8);
+  else MI_ROUTE(16);
+#undef MI_ROUTE
+  return hipGetLastError();
+}
+
+size_t sort_dispatch_lds_bytes(int E) { return ((size_t)E + 1 + kSortThreads) * 4; }
+
+hipError_t launch_sort_dispatch(const uint32_t* flat, int64_t n, int k, int E, uint32_t* order,
+                                uint32_t* inv, uint32_t* sorted, uint32_t* lhs, uint32_t* seg,
+                                hipStream_t s) {
+  hipLaunchKernelGGL(sort_dispatch_kernel, dim3(1), dim3(kSortThreads),
+                     sort_dispatch_lds_bytes(E), s, flat, n, k, E, order, inv, sorted, lhs, seg);
+  return hipGetLastError();
+}
+
+hipError_t launch_take_rows(void* out, const void* in, const uint32_t* idx, int64_t n,
+                            int64_t n_src, int64_t row_bytes, hipStream_t s) {
+  if (n == 0 || row_bytes == 0) return hipSuccess;
+  const int64_t units = (row_bytes & 15) == 0 ? row_bytes / 16 : row_bytes;
+  hipLaunchKernelGGL(take_rows_kernel, dim3(grid_for(units, 256), (unsigned)n), dim3(256), 0, s,
+                     out, in, idx, n_src, row_bytes);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu(uint16_t* y, const uint16_t* g, const uint16_t* u, int64_t n,
+                         hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, y, g, u, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_down_reduce(uint16_t* y, const uint16_t* v, const uint16_t* scores, int64_t T,
+                              int k, int64_t N, hipStream_t s) {
+  if (T == 0 || N == 0) return hipSuccess;
+  hipLaunchKernelGGL(down_reduce_kernel, dim3(grid_for(N, 256), (unsigned)T), dim3(256), 0, s, y,
+                     v, scores, T, k, N);
+  return hipGetLastError();
+}
+
+}  // namespace mi

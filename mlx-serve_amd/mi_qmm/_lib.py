@@ -51,6 +51,16 @@ def lib():
     L.mi_affine_params_from_geometry.argtypes = [i64, i64, i64, ctypes.POINTER(i32),
                                                  ctypes.POINTER(i32)]
     L.mi_fill_randn.argtypes = [P, i64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, i32, P]
+    L.mi_moe_route_topk.argtypes = [P, P, P, i64, i64, i32, i32, P]
+    L.mi_moe_sort_dispatch.argtypes = [P, P, P, P, P, P, i64, i32, i64, P]
+    L.mi_take_rows.argtypes = [P, P, P, i64, i64, i64, P]
+    L.mi_swiglu.argtypes = [P, P, P, i64, i32, P]
+    L.mi_moe_down_reduce.argtypes = [P, P, P, i64, i32, i64, i32, P]
+    L.mi_gather_qmv_gate_up_swiglu.argtypes = [P, P, P, P, P, P, P, P, P, i64, i32, i64, i64,
+                                               i64, OptInt, OptInt, s, P]
+    L.mi_gather_qmv_down_reduce.argtypes = [P, P, P, P, P, P, P, i64, i32, i64, i64, i64, OptInt,
+                                            OptInt, s, P]
+    L.mi_workspace_reserve.argtypes = [i64, P]
     L.mi_last_error.restype = ctypes.c_char_p
     L.mi_version.restype = ctypes.c_char_p
     for name in EXTRA_SIGNATURES:

@@ -189,3 +189,102 @@ def affine_params_from_geometry(w_cols, s_cols, in_dim):
     rc = lib().mi_affine_params_from_geometry(int(w_cols), int(s_cols), int(in_dim),
                                               ctypes.byref(b), ctypes.byref(g))
     return None if rc != 0 else (b.value, g.value)
+
+
+# ---------------------------------------------------------------- MoE glue --
+def moe_route_topk(logits, k, scores_dtype=torch.float32):
+    """Softmax top-k routing (moeRoutingChain, src/transformer.zig:17022-17072).
+    logits fp32 [..., E] -> (inds uint32-as-int32 [..., k], scores [..., k])."""
+    _contig(logits)
+    _require(logits.dtype == torch.float32, "logits must be float32")
+    E = logits.shape[-1]
+    T = logits.numel() // E if E else 0
+    inds = torch.empty(logits.shape[:-1] + (k,), dtype=torch.int32, device=logits.device)
+    scores = torch.empty(logits.shape[:-1] + (k,), dtype=scores_dtype, device=logits.device)
+    check(lib().mi_moe_route_topk(_ptr(inds), _ptr(scores), _ptr(logits), T, E, int(k),
+                                  _dtype_code(scores, "scores"), _stream(logits)))
+    return inds, scores
+
+
+def moe_sort_dispatch(flat, k, n_experts):
+    """Sorted MoE dispatch (src/transformer.zig:14965-14993): returns (order, inv, sorted,
+    lhs, seg_offsets) with order = stable argsort(flat), inv = argsort(order),
+    sorted = flat[order], lhs = order // k, seg_offsets [n_experts + 1]."""
+    _contig(flat)
+    flat = flat.reshape(-1)
+    n = flat.numel()
+    mk = lambda m: torch.empty(m, dtype=torch.int32, device=flat.device)  # noqa: E731
+    order, inv, srt, lhs, seg = mk(n), mk(n), mk(n), mk(n), mk(n_experts + 1)
+    check(lib().mi_moe_sort_dispatch(_ptr(order), _ptr(inv), _ptr(srt), _ptr(lhs), _ptr(seg),
+                                     _ptr(flat), n, int(k), int(n_experts), _stream(flat)))
+    return order, inv, srt, lhs, seg
+
+
+def take_rows(x, indices):
+    """x[indices] along axis 0 (mlx_take_axis 0 on row-major rows)."""
+    _contig(x, indices)
+    idx = indices.reshape(-1)
+    out = torch.empty((idx.numel(),) + tuple(x.shape[1:]), dtype=x.dtype, device=x.device)
+    row_bytes = x[0].numel() * x.element_size() if x.shape[0] else 0
+    check(lib().mi_take_rows(_ptr(out), _ptr(x), _ptr(idx), idx.numel(), x.shape[0], row_bytes,
+                             _stream(x)))
+    return out
+
+
+def swiglu(gate, up):
+    """bf16(bf16(g * sigmoid(g)) * u) (fusedSwiGLU, src/transformer.zig:19846-19884)."""
+    _contig(gate, up)
+    _require(gate.shape == up.shape, "gate/up shapes differ")
+    y = torch.empty_like(gate)
+    check(lib().mi_swiglu(_ptr(y), _ptr(gate), _ptr(up), gate.numel(), _dtype_code(gate, "gate"),
+                          _stream(gate)))
+    return y
+
+
+def moe_down_reduce(v, scores):
+    """Score-weighted slot sum in bf16: v [T, k, N], scores [T, k] -> [T, N]."""
+    _contig(v, scores)
+    T, k, N = v.shape
+    y = torch.empty((T, N), dtype=v.dtype, device=v.device)
+    check(lib().mi_moe_down_reduce(_ptr(y), _ptr(v), _ptr(scores), T, k, N,
+                                   _dtype_code(v, "v"), _stream(v)))
+    return y
+
+
+def gather_qmv_gate_up_swiglu(x, wg, sg, bg, wu, su, bu, inds, group_size=None, bits=None,
+                              mode="affine"):
+    """gatherQmvGateUp (src/transformer.zig:20303-20396): x [T, K], inds [T, k] ->
+    [T, k, N] = swiglu(x @ Wg[e]^T, x @ Wu[e]^T), each product rounded to bf16 first."""
+    _contig(x, wg, sg, bg, wu, su, bu, inds)
+    T, K = x.shape
+    k = inds.shape[-1]
+    gs, nb = _resolve(_packed(wg), sg, group_size, bits, K)
+    E, N = wg.shape[0], wg.shape[1]
+    y = torch.empty((T, k, N), dtype=x.dtype, device=x.device)
+    check(lib().mi_gather_qmv_gate_up_swiglu(_ptr(y), _ptr(x), _ptr(wg), _ptr(sg), _ptr(bg),
+                                             _ptr(wu), _ptr(su), _ptr(bu), _ptr(inds), T, k, N,
+                                             K, E, opt(gs), opt(nb),
+                                             mode.encode() if mode else None, _stream(x)))
+    return y
+
+
+def gather_qmv_down_reduce(act, wd, sd, bd, inds, scores, group_size=None, bits=None,
+                           mode="affine"):
+    """gatherQmvDownReduce (src/transformer.zig:20675-20761): act [T, k, K], inds/scores
+    [T, k] -> [T, N]."""
+    _contig(act, wd, sd, bd, inds, scores)
+    T, k, K = act.shape
+    gs, nb = _resolve(_packed(wd), sd, group_size, bits, K)
+    E, N = wd.shape[0], wd.shape[1]
+    y = torch.empty((T, N), dtype=act.dtype, device=act.device)
+    check(lib().mi_gather_qmv_down_reduce(_ptr(y), _ptr(act), _ptr(wd), _ptr(sd), _ptr(bd),
+                                          _ptr(inds), _ptr(scores), T, k, N, K, E, opt(gs),
+                                          opt(nb), mode.encode() if mode else None, _stream(act)))
+    return y
+
+
+def workspace_reserve(nbytes, device=None):
+    """Grow the library's per-device workspace ahead of HIP graph capture."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    check(lib().mi_workspace_reserve(int(nbytes),
+                                     ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))

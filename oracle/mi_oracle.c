@@ -406,11 +406,13 @@ int mo_sort_dispatch(const uint32_t* flat, int64_t n, int k, uint32_t* order,
 
 /* ---------------------------------------------------- fused contracts --- */
 /* Table SwiGLU (src/transformer.zig:19855-19884 builds sigmoid over every bf16
- * pattern; :19846-19849 applies g*sig then *up, each a bf16 multiply). */
+ * pattern; :19846-19849 applies g*sig then *up, each a bf16 multiply). The table value
+ * is the sigmoid evaluated in double, rounded to fp32 and then to bf16 (MLX's own
+ * sigmoid rounding is not available here; this is the correctly rounded value). */
 void mo_sigmoid_table_bf16(uint16_t* table) {
   for (uint32_t i = 0; i < 65536u; ++i) {
-    float v = mo_bf16_to_f32((uint16_t)i);
-    float s = 1.0f / (1.0f + expf(-v));
+    double v = (double)mo_bf16_to_f32((uint16_t)i);
+    float s = (float)(1.0 / (1.0 + exp(-v)));
     table[i] = mo_f32_to_bf16(s);
   }
 }

@@ -1,0 +1,170 @@
+"""GPU parity of the MoE glue around gather_qmm: routing, sorted dispatch, row take,
+SwiGLU, the score-weighted slot reduction and the fused decode entry points. Index work is
+bit-exact against the oracle; the bf16 rounding contracts (SwiGLU, down-reduce) are
+bit-exact; fused entry points are bit-equal to the split calls they replace."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import BF16_TOL, bf16_bits, max_err_ratio, to_dev_bf16, to_dev_u32, to_f64, weights
+import mi_qmm
+
+pytestmark = pytest.mark.gpu
+
+
+def _print_case(**kw):
+    print("CASE", kw, flush=True)
+
+
+def _u32(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("T,E,k", [(37, 128, 8), (5, 256, 8), (9, 60, 4), (3, 16, 1),
+                                   (64, 1000, 16)])
+def test_route_topk(dev, T, E, k):
+    _print_case(t="route", T=T, E=E, k=k)
+    logits = O.randn(T * E, O.seed_for(4, 2)).reshape(T, E)
+    logits[0, 3] = logits[0, 7] = logits[0].max() + 1.0   # tie at the top: lower id first
+    if T > 1:
+        logits[1, :] = 0.5                                  # all equal: ids 0..k-1
+    inds, scores = mi_qmm.moe_route_topk(torch.from_numpy(logits).to(dev), k)
+    ri, rs = O.route_softmax_topk(logits, k)
+    assert np.array_equal(_u32(inds), ri)
+    np.testing.assert_allclose(scores.cpu().numpy(), rs, rtol=2e-6, atol=1e-7)
+    _, sb = mi_qmm.moe_route_topk(torch.from_numpy(logits).to(dev), k, torch.bfloat16)
+    # one bf16 rounding of an fp32 score that matches the oracle's to 2e-6
+    d = np.abs(bf16_bits(sb).astype(np.int32) - O.f32_to_bf16(rs).astype(np.int32))
+    assert d.max() <= 1
+
+
+@pytest.mark.parametrize("n,E,k,skew", [(1, 128, 1, False), (8, 128, 8, False),
+                                        (1000, 128, 8, False), (4096, 128, 8, True),
+                                        (5000, 256, 8, True), (512, 8192, 4, False)])
+def test_sort_dispatch(dev, n, E, k, skew):
+    _print_case(t="sort", n=n, E=E, k=k, skew=skew)
+    rng = np.random.default_rng(n + E)
+    flat = rng.integers(0, E, size=n).astype(np.uint32)
+    if skew:
+        hot = rng.choice(E, 8, replace=False)
+        m = rng.random(n) < 0.5
+        flat[m] = rng.choice(hot, m.sum())
+    order, inv, srt, lhs, seg = mi_qmm.moe_sort_dispatch(to_dev_u32(flat, dev), k, E)
+    ro, ri, rsrt, rl = O.sort_dispatch(flat, k)
+    assert np.array_equal(_u32(order), ro)
+    assert np.array_equal(_u32(inv), ri)
+    assert np.array_equal(_u32(srt), rsrt)
+    assert np.array_equal(_u32(lhs), rl)
+    counts = np.bincount(flat, minlength=E)
+    want = np.concatenate([[0], np.cumsum(counts)]).astype(np.uint32)
+    assert np.array_equal(_u32(seg), want)
+
+
+def test_sort_dispatch_out_of_range_ids_sort_last(dev):
+    _print_case(t="sort_oob")
+    flat = np.array([3, 99, 1, 3, 99, 0], np.uint32)
+    order, inv, srt, lhs, seg = mi_qmm.moe_sort_dispatch(to_dev_u32(flat, dev), 2, 4)
+    assert _u32(order).tolist() == [5, 2, 0, 3, 1, 4]
+    assert _u32(srt).tolist() == [0, 1, 3, 3, 99, 99]
+    assert _u32(seg).tolist() == [0, 1, 2, 2, 4]
+
+
+def test_take_rows(dev):
+    _print_case(t="take")
+    rng = np.random.default_rng(1)
+    x = torch.from_numpy(rng.standard_normal((50, 768)).astype(np.float32)).to(dev).bfloat16()
+    idx = rng.integers(0, 50, size=77).astype(np.uint32)
+    idx[5] = 1000  # out of range -> zero row
+    got = mi_qmm.take_rows(x, to_dev_u32(idx, dev)).cpu()
+    ref = x.cpu()[torch.from_numpy(np.minimum(idx, 49).astype(np.int64))]
+    ref[5] = 0
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    b = torch.from_numpy(rng.integers(0, 255, size=(9, 3)).astype(np.uint8)).to(dev)
+    got = mi_qmm.take_rows(b, to_dev_u32(np.array([8, 0, 4], np.uint32), dev)).cpu()
+    assert torch.equal(got, b.cpu()[[8, 0, 4]])
+
+
+def test_swiglu_exhaustive(dev):
+    _print_case(t="swiglu")
+    g = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    g = g[~np.isnan(O.bf16_to_f32(g))]
+    u = O.f32_to_bf16(np.random.default_rng(2).standard_normal(g.size).astype(np.float32))
+    y = mi_qmm.swiglu(to_dev_bf16(g, dev), to_dev_bf16(u, dev))
+    assert np.array_equal(bf16_bits(y), O.swiglu_bf16(g, u))
+
+
+def test_down_reduce_bit_exact(dev):
+    _print_case(t="down_reduce")
+    T, k, N = 6, 8, 2048
+    rng = np.random.default_rng(3)
+    v = O.f32_to_bf16(rng.standard_normal((T, k, N)).astype(np.float32))
+    sc = O.f32_to_bf16(rng.random((T, k)).astype(np.float32))
+    y = bf16_bits(mi_qmm.moe_down_reduce(to_dev_bf16(v, dev), to_dev_bf16(sc, dev)))
+    for t in range(T):
+        assert np.array_equal(y[t], O.down_reduce_bf16(v[t], sc[t]))
+
+
+def _bank(E, N, K, seed, bits=4):
+    wq, s, b = weights(E, N, K, bits, 64, seed)
+    return wq, s, b
+
+
+@pytest.mark.parametrize("T,E,k,N,K", [(1, 16, 8, 192, 512), (3, 12, 4, 128, 256)])
+def test_fused_decode_mlp_matches_split(dev, T, E, k, N, K):
+    """gate+up+SwiGLU and down+reduce entry points == split gather_qmm + glue, bit for bit;
+    and the split path matches the oracle composition within tolerance."""
+    _print_case(t="fused", T=T, E=E, k=k, N=N, K=K)
+    rng = np.random.default_rng(T * 100 + E)
+    gq, gs_, gb = _bank(E, N, K, 11)
+    uq, us, ub = _bank(E, N, K, 12)
+    dq, ds, db = _bank(E, K, N, 13)
+    x = O.make_x_bf16(T, K, 14)
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.uint32)
+    sc = O.f32_to_bf16(rng.random((T, k)).astype(np.float32))
+    D = lambda *a: [to_dev_u32(a[0], dev), to_dev_bf16(a[1], dev), to_dev_bf16(a[2], dev)]  # noqa
+    G, U, Dn = D(gq, gs_, gb), D(uq, us, ub), D(dq, ds, db)
+    xd, idd, scd = to_dev_bf16(x, dev), to_dev_u32(inds, dev), to_dev_bf16(sc, dev)
+
+    act = mi_qmm.gather_qmv_gate_up_swiglu(xd, *G, *U, idd, group_size=64, bits=4)
+    xg = xd.reshape(T, 1, 1, K)
+    g_split = mi_qmm.gather_qmm(xg, *G, rhs_indices=idd, group_size=64, bits=4)
+    u_split = mi_qmm.gather_qmm(xg, *U, rhs_indices=idd, group_size=64, bits=4)
+    act_split = mi_qmm.swiglu(g_split, u_split).reshape(T, k, N)
+    assert torch.equal(act.view(torch.int16), act_split.view(torch.int16))
+
+    y = mi_qmm.gather_qmv_down_reduce(act, *Dn, idd, scd, group_size=64, bits=4)
+    v_split = mi_qmm.gather_qmm(act.reshape(T * k, 1, N), *Dn, rhs_indices=idd.reshape(-1),
+                                group_size=64, bits=4)
+    y_split = mi_qmm.moe_down_reduce(v_split.reshape(T, k, K), scd)
+    assert torch.equal(y.view(torch.int16), y_split.view(torch.int16))
+
+    # split path against the oracle: gate/up products, then the bf16 glue on GPU values
+    tg = O.gather_qmm_f64(x.reshape(T, 1, K), gq, gs_, gb, None, inds.reshape(-1), T * k,
+                          lhs_div=k)
+    assert max_err_ratio(to_f64(g_split).reshape(T * k, 1, N), tg) <= BF16_TOL
+    a_np = bf16_bits(act).reshape(T * k, N)
+    assert np.array_equal(a_np, O.swiglu_bf16(bf16_bits(g_split).reshape(T * k, N),
+                                              bf16_bits(u_split).reshape(T * k, N)))
+    tv = O.gather_qmm_f64(a_np.reshape(T * k, 1, N), dq, ds, db, None, inds.reshape(-1), T * k)
+    assert max_err_ratio(to_f64(v_split).reshape(T * k, 1, K), tv) <= BF16_TOL
+
+
+def test_sorted_moe_pipeline_end_to_end(dev):
+    """Router -> sort -> gather_qmm(sorted, lhs = order//k) -> take_rows(inv) equals the
+    unsorted per-(token, slot) products (the reference's sorted prefill path, :14961-15043)."""
+    _print_case(t="pipeline")
+    T, E, k, N, K = 48, 16, 4, 96, 512
+    logits = O.randn(T * E, O.seed_for(4, 2)).reshape(T, E)
+    inds, _ = mi_qmm.moe_route_topk(torch.from_numpy(logits).to(dev), k)
+    order, inv, srt, lhs, seg = mi_qmm.moe_sort_dispatch(inds.reshape(-1), k, E)
+    wq, s, b = _bank(E, N, K, 21)
+    x = O.make_x_bf16(T, K, 22)
+    xd = to_dev_bf16(x, dev).reshape(T, 1, K)
+    W = [to_dev_u32(wq, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev)]
+    ys = mi_qmm.gather_qmm(xd, *W, lhs_indices=lhs, rhs_indices=srt, group_size=64, bits=4,
+                           sorted_indices=True)
+    y = mi_qmm.take_rows(ys.reshape(T * k, N), inv)
+    ri, _ = O.route_softmax_topk(logits, k)
+    truth = O.gather_qmm_f64(x.reshape(T, 1, K), wq, s, b, None, ri.reshape(-1), T * k, lhs_div=k)
+    assert max_err_ratio(to_f64(y).reshape(T * k, 1, N), truth) <= BF16_TOL
