@@ -126,6 +126,138 @@ def cpu_baseline(torch, layers, bits, gs, hidden=4096, inter=14336, budget_s=10.
                       f"{n_l} layers' weights, {t:.1f} s, C oracle mo_qmm_f32 with OpenMP"}
 
 
+def graph_time(torch, fn, replays, warmup=2):
+    """Capture fn() once in a HIP graph (after an eager warm-up that sizes the library
+    workspace) and return seconds per replay."""
+    fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    return time_region(torch, graph.replay, replays, warmup) / replays
+
+
+def prefill(torch, mi, dev, Ms, steps=10, warmup=2, bits=4, gs=64):
+    """prefill qmm TFLOP/s for x [M, K] against 4-bit g64 W [N, K]."""
+    out = {}
+    for (N, K, name) in ((14336, 4096, "gate"), (4096, 14336, "down")):
+        tmp = torch.empty(N * K, dtype=torch.bfloat16, device=dev).view(N, K)
+        mi.fill_randn(tmp, seed(3, 1), 0.0, 0.02)
+        W = mi.quantize(tmp, gs, bits)
+        del tmp
+        for M in Ms:
+            x = torch.empty(M, K, dtype=torch.bfloat16, device=dev)
+            mi.fill_randn(x, seed(3, 0, M), 0.0, 1.0)
+            t = time_region(torch, lambda: mi.quantized_matmul(x, *W, True, gs, bits), steps,
+                            warmup)
+            tf = 2.0 * M * N * K * steps / t / 1e12
+            out[f"prefill_{name}_M{M}_TFLOPs"] = round(tf, 1)
+            out[f"prefill_{name}_M{M}_pct_bf16_peak"] = round(100 * tf / BF16_PEAK_TFLOPS, 2)
+            out[f"prefill_{name}_M{M}_tok_s"] = round(M * steps / t, 1)
+        del W
+    return out
+
+
+def moe_bank(torch, mi, dev, E, N, K, bits, gs, sd):
+    tmp = torch.empty(E * N * K, dtype=torch.bfloat16, device=dev).view(E * N, K)
+    mi.fill_randn(tmp, sd, 0.0, 0.02)
+    wq, s, b = mi.quantize(tmp, gs, bits)
+    return wq.view(E, N, -1), s.view(E, N, -1), b.view(E, N, -1)
+
+
+def moe_layer(torch, mi, dev, cfg, E, hidden, inter, k, Ts, n_routes=16, steps=10, warmup=2,
+              skew=False):
+    """configs[3]/[4]: one routed-expert MoE layer (route -> gate/up -> SwiGLU -> down ->
+    score-weighted sum), 4-bit g64, decode (T=1, fused entry points) and sorted prefill.
+    Routings differ per iteration so the touched experts are not cache-resident.
+    GB/s counts each distinct expert's packed + scale/bias bytes once, plus activations."""
+    bits, gs = 4, 64
+    G = moe_bank(torch, mi, dev, E, inter, hidden, bits, gs, seed(cfg, 1, 1))
+    U = moe_bank(torch, mi, dev, E, inter, hidden, bits, gs, seed(cfg, 1, 2))
+    D = moe_bank(torch, mi, dev, E, hidden, inter, bits, gs, seed(cfg, 1, 3))
+    per_expert = 3 * (inter * hidden * bits // 8 + 2 * (inter * hidden // gs) * 2)
+    out = {}
+    for T in Ts:
+        logits = torch.empty(n_routes, T, E, dtype=torch.float32, device=dev)
+        mi.fill_randn(logits, seed(cfg, 2, T), 0.0, 1.0)
+        if skew:
+            # 10% of tokens pushed onto 8 fixed hot experts (+8.0 on their logits)
+            g = torch.Generator().manual_seed(seed(cfg, 3) & 0x7FFFFFFF)
+            hot = torch.randperm(E, generator=g)[:8]
+            pick = torch.rand(n_routes, T, generator=g) < 0.1
+            bump = torch.zeros(n_routes, T, E)
+            bump[:, :, hot] = 8.0
+            logits += (bump * pick[..., None]).to(dev)
+        x = torch.empty(T, hidden, dtype=torch.bfloat16, device=dev)
+        mi.fill_randn(x, seed(cfg, 0, T), 0.0, 1.0)
+        routes = [mi.moe_route_topk(logits[r], k, torch.bfloat16) for r in range(n_routes)]
+        distinct = [torch.unique(r[0]).numel() for r in routes]
+
+        def layer(r):
+            inds, sc = mi.moe_route_topk(logits[r], k, torch.bfloat16)
+            if T == 1:
+                act = mi.gather_qmv_gate_up_swiglu(x, *G, *U, inds, gs, bits)
+                return mi.gather_qmv_down_reduce(act, *D, inds, sc, gs, bits)
+            order, inv, srt, lhs, seg = mi.moe_sort_dispatch(inds.reshape(-1), k, E)
+            xs = x.view(T, 1, hidden)
+            g = mi.gather_qmm(xs, *G, lhs_indices=lhs, rhs_indices=srt, group_size=gs,
+                              bits=bits, sorted_indices=True)
+            u = mi.gather_qmm(xs, *U, lhs_indices=lhs, rhs_indices=srt, group_size=gs,
+                              bits=bits, sorted_indices=True)
+            a = mi.swiglu(g, u)
+            v = mi.gather_qmm(a, *D, rhs_indices=srt, group_size=gs, bits=bits,
+                              sorted_indices=True)
+            v = mi.take_rows(v.view(T * k, hidden), inv)
+            return mi.moe_down_reduce(v.view(T, k, hidden), sc)
+
+        def all_routes():
+            for r in range(n_routes):
+                layer(r)
+
+        # one graph = n_routes layer steps, each with its own routing
+        t = graph_time(torch, all_routes, steps, warmup) / n_routes
+        avg_distinct = sum(distinct) / len(distinct)
+        byts = avg_distinct * per_expert + T * hidden * 2 * 2 + T * k * inter * 2 * 3
+        out[f"moe{cfg + 1}_T{T}_us"] = round(t * 1e6, 1)
+        out[f"moe{cfg + 1}_T{T}_GBs"] = round(byts / t / 1e9, 1)
+        out[f"moe{cfg + 1}_T{T}_tok_s"] = round(T / t, 1)
+        out[f"moe{cfg + 1}_T{T}_distinct_experts"] = round(avg_distinct, 1)
+    return out
+
+
+def shared_expert_8bit(torch, mi, dev, Ts, steps=10, warmup=2):
+    """configs[4] shared expert: 8-bit g64 dense MLP (2048,7168)x2 + (7168,2048)."""
+    bits, gs = 8, 64
+    mats = []
+    for (N, K, st) in ((2048, 7168, 4), (2048, 7168, 5), (7168, 2048, 6)):
+        tmp = torch.empty(N * K, dtype=torch.bfloat16, device=dev).view(N, K)
+        mi.fill_randn(tmp, seed(4, 1, st), 0.0, 0.02)
+        mats.append(mi.quantize(tmp, gs, bits))
+    out = {}
+    for T in Ts:
+        x = torch.empty(T, 7168, dtype=torch.bfloat16, device=dev)
+        h = torch.empty(T, 2048, dtype=torch.bfloat16, device=dev)
+        mi.fill_randn(x, seed(4, 0, T), 0.0, 1.0)
+        mi.fill_randn(h, seed(4, 0, T + 1), 0.0, 1.0)
+
+        def step():
+            mi.quantized_matmul(x, *mats[0], True, gs, bits)
+            mi.quantized_matmul(x, *mats[1], True, gs, bits)
+            mi.quantized_matmul(h, *mats[2], True, gs, bits)
+
+        t = graph_time(torch, step, steps * 5, warmup)
+        byts = sum(qbytes(N, K, bits, gs, T) for (N, K) in ((2048, 7168), (2048, 7168),
+                                                           (7168, 2048)))
+        out[f"shared8_T{T}_GBs"] = round(byts / t / 1e9, 1)
+        out[f"shared8_T{T}_us"] = round(t * 1e6, 1)
+    return out
+
+
 def pmc_traffic():
     """HBM bytes per decode launch, from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     summary (counters scaled by a copy kernel of known size); None if absent."""
@@ -179,9 +311,25 @@ def main():
             r = decode_mlp(torch, mi, layers, M, bits, gs, dev, max(5, args.steps // 5), 2)
             extra[f"q4_M{M}_GBs"] = round(r["GBs"], 1)
             extra[f"q4_M{M}_tok_s"] = round(r["tokens_per_s"], 1)
+        del layers
+        torch.cuda.empty_cache()
+        layers8 = build_mlp_layers(torch, mi, args.layers, 8, gs, dev)
+        for M in (1, 8, 32):
+            r = decode_mlp(torch, mi, layers8, M, 8, gs, dev, max(5, args.steps // 5), 2)
+            extra[f"q8_M{M}_GBs"] = round(r["GBs"], 1)
+            extra[f"q8_M{M}_tok_s"] = round(r["tokens_per_s"], 1)
+        del layers8
+        torch.cuda.empty_cache()
+        extra.update(prefill(torch, mi, dev, (512, 2048, 8192)))
+        extra.update(moe_layer(torch, mi, dev, 3, 128, 2048, 768, 8, (1, 512)))
+        extra.update(moe_layer(torch, mi, dev, 4, 256, 7168, 2048, 8, (1, 8, 64), skew=True))
+        extra.update(shared_expert_8bit(torch, mi, dev, (1, 8, 64)))
+        layers = None
 
     cpu = None
     if not args.no_cpu:
+        if layers is None:
+            layers = build_mlp_layers(torch, mi, 2, bits, gs, dev)
         cpu = cpu_baseline(torch, layers, bits, gs, budget_s=args.cpu_seconds)
 
     ms_per_step = head["seconds"] / args.steps * 1e3

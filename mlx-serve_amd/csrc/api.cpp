@@ -250,11 +250,25 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
 
   J.use_items = sorted_indices && rhs_indices != nullptr && n_idx > 1;
   const int64_t PT = n_idx * M;
-  // Decode widths (<= 4 rows per pair, or sorted runs cut into 16-row items) use the
-  // 16-row-tile kernel; wider pairs use the 32-row-tile kernel.
+  // Rows per work item. Dense pairs: up to 4 rows per pair ride the 16-row-tile kernel
+  // (qmv16), wider pairs the 32-row-tile kernel. Sorted runs are cut into items sized
+  // from the average run length (rows / distinct-run bound, known without reading the
+  // indices): short runs take qmv16 with 1, 2 or 4 staged rows, longer runs 8..32-row
+  // items on the 32-row-tile kernel. A run longer than one item re-reads its expert.
   static const int narrow_max = env_int("MI_QMM_NARROW_MAX", 4);
-  J.narrow = (J.use_items || M <= narrow_max) && mi::qmv16_supported(P.K, gs, nb);
-  P.rpi = J.narrow ? 16 : 32;
+  static const int item_rows = env_int("MI_QMM_ITEM_ROWS", 0);
+  const bool q16 = mi::qmv16_supported(P.K, gs, nb);
+  if (J.use_items) {
+    const int64_t runs = n_idx < n_experts ? n_idx : n_experts;
+    int64_t avg = (PT + runs - 1) / runs;
+    if (item_rows > 0) avg = item_rows;
+    J.narrow = q16 && avg <= 4;
+    P.rpi = avg <= 1 ? 1 : avg <= 2 ? 2 : avg <= 4 ? 4 : avg <= 8 ? 8 : avg <= 16 ? 16 : 32;
+    if (!J.narrow && P.rpi < 8) P.rpi = 8;
+  } else {
+    J.narrow = M <= narrow_max && q16;
+    P.rpi = J.narrow ? 16 : 32;
+  }
   const int rows = (int)(M < P.rpi ? M : P.rpi);
   int64_t n_items;
   if (!J.use_items) {
@@ -369,7 +383,14 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   hipStream_t s = (hipStream_t)stream;
   if (x_dtype == MI_DTYPE_BFLOAT16 && M > 32 && mi::qmm_supported((int)M, (int)N, (int)K, nb, gs)) {
     mi::QmmParams Q{w, (const uint16_t*)scales, (const uint16_t*)biases, (const uint16_t*)x,
-                    (uint16_t*)y, (int)M, (int)N, (int)K, nb, gs};
+                    (uint16_t*)y, (int)M, (int)N, (int)K, nb, gs, nullptr, 1, 0, 0};
+    const size_t ws = mi::qmm_plan(Q);
+    if (ws) {
+      void* data = nullptr;
+      rc = workspace(s, ws, &data);
+      if (rc) return rc;
+      Q.part = (float*)data;
+    }
     hipError_t e = mi::launch_qmm(Q, s);
     return e == hipSuccess ? MI_OK : hip_fail(e, "qmm launch");
   }

@@ -76,7 +76,13 @@ struct QmmParams {
   uint16_t* y;        // bf16 [M, N]
   int M, N, K;
   int bits, group_size;
+  // K split: grid.y = ks ranges of sup_per_split super-steps; ks > 1 writes fp32
+  // partials [ks][M][N] to `part` and a fixed-order reduce produces y.
+  float* part;
+  int ks, sup_per_split, bm;
 };
+// Fills bm / ks / sup_per_split; returns the workspace bytes the call needs.
+size_t qmm_plan(QmmParams& P);
 hipError_t launch_qmm(const QmmParams& P, hipStream_t s);
 bool qmm_supported(int M, int N, int K, int bits, int gs);
 

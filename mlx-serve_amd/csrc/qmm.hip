@@ -91,8 +91,11 @@ qmm_kernel(QmmParams P) {
   // same x row block while the weight tiles stream past.
   const int mt = blockIdx.x % mtiles, nt = blockIdx.x / mtiles;
   const int m0 = mt * BM, n0 = nt * kBN;
-  const int nsteps = K / kBK;
-  const int nsup = K / SSK;
+  // This block's K range: super-steps [sup_base, sup_base + nsup).
+  const int split = blockIdx.y;
+  const int sup_base = split * P.sup_per_split;
+  const int nsup = min(P.sup_per_split, K / SSK - sup_base);
+  const int nsteps = nsup * SS;
 
   // K order. The MFMA k-slots [8*(l/32), +8) of lane l at k-step ks (0..3) of sub-step t of
   // super-step T stand for columns SSK*T + LV*(l/32) + 32*t + 8*ks .. +8, for both operands.
@@ -110,7 +113,7 @@ qmm_kernel(QmmParams P) {
   }
   auto issue_a = [&](int step, int slot) {
     unsigned char* dst = smem + slot * ABYTES + wave * A_INSTR * 8 * kRowBytes;
-    const uint32_t ko = (uint32_t)((step / SS) * SSK + (step % SS) * 32);
+    const uint32_t ko = (uint32_t)((sup_base + step / SS) * SSK + (step % SS) * 32);
 #pragma unroll
     for (int i = 0; i < A_INSTR; ++i) dma16(P.x + (xo[i] + ko), dst + i * 8 * kRowBytes);
   };
@@ -125,10 +128,11 @@ qmm_kernel(QmmParams P) {
     so[j] = n * (uint32_t)G;
   }
   auto load_w = [&](int sup, R_t& R) {
-    const uint32_t g0 = (uint32_t)(sup * SSK + fk * LV) / GS;
+    const uint32_t g0 = (uint32_t)((sup_base + sup) * SSK + fk * LV) / GS;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const u32x4_t* p = reinterpret_cast<const u32x4_t*>(P.w + (wo[j] + sup * (SSK / PF)));
+      const u32x4_t* p =
+          reinterpret_cast<const u32x4_t*>(P.w + (wo[j] + (sup_base + sup) * (SSK / PF)));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         u32x4_t v = p[i];
@@ -286,7 +290,9 @@ qmm_kernel(QmmParams P) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + i * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
-        if (m < M) P.y[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[i][j][r]);
+        if (m >= M) continue;
+        if (P.part) P.part[((int64_t)split * M + m) * N + n] = acc[i][j][r];
+        else P.y[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[i][j][r]);
       }
   }
 }
@@ -303,20 +309,25 @@ hipError_t launch_bm(const QmmParams& P, hipStream_t s) {
     if (e != hipSuccess) return e;
     attr = true;
   }
-  hipLaunchKernelGGL(k, dim3((unsigned)(mtiles * ntiles)), dim3(kThreads), lds, s, P);
+  hipLaunchKernelGGL(k, dim3((unsigned)(mtiles * ntiles), (unsigned)P.ks), dim3(kThreads), lds, s,
+                     P);
   return hipGetLastError();
 }
 
 template <int BITS, int GS>
 hipError_t launch_gs(const QmmParams& P, hipStream_t s) {
-  // 128-row tiles when 256-row tiles would leave CUs idle.
-  const int64_t big = (int64_t)((P.M + 255) / 256) * ((P.N + kBN - 1) / kBN);
-  static const int forced = [] {
-    const char* v = std::getenv("MI_QMM_BM");
-    return v ? std::atoi(v) : 0;
-  }();
-  const bool use256 = forced ? forced == 256 : big >= 240;
-  return use256 ? launch_bm<BITS, GS, 256>(P, s) : launch_bm<BITS, GS, 128>(P, s);
+  return P.bm == 256 ? launch_bm<BITS, GS, 256>(P, s) : launch_bm<BITS, GS, 128>(P, s);
+}
+
+// y[m, n] = bf16(sum over splits in order of part[split, m, n]).
+__global__ void qmm_reduce_kernel(const float* __restrict__ part, uint16_t* __restrict__ y,
+                                  int64_t mn, int ks) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float acc = part[i];
+    for (int s = 1; s < ks; ++s) acc += part[(int64_t)s * mn + i];
+    y[i] = (uint16_t)f32_to_bf16_bits(acc);
+  }
 }
 
 }  // namespace
@@ -331,20 +342,55 @@ bool qmm_supported(int M, int N, int K, int bits, int gs) {
   return M >= 1 && K % (kSubSteps<4> * kBK) == 0 && K % gs == 0;
 }
 
+size_t qmm_plan(QmmParams& P) {
+  static const int forced_bm = [] {
+    const char* v = std::getenv("MI_QMM_BM");
+    return v ? std::atoi(v) : 0;
+  }();
+  static const int forced_ks = [] {
+    const char* v = std::getenv("MI_QMM_KS");
+    return v ? std::atoi(v) : 0;
+  }();
+  const int ss = P.bits == 4 ? kSubSteps<4> : kSubSteps<8>;
+  const int nsup = P.K / (ss * kBK);
+  const int ntiles = (P.N + kBN - 1) / kBN;
+  // 256-row tiles when they fill the GPU; otherwise 128-row tiles.
+  const int64_t big = (int64_t)((P.M + 255) / 256) * ntiles;
+  P.bm = forced_bm ? (forced_bm == 256 ? 256 : 128) : (big >= 240 ? 256 : 128);
+  const int64_t blocks = (int64_t)((P.M + P.bm - 1) / P.bm) * ntiles;
+  // Split K when the tiles cannot fill the GPU, keeping >= 2 super-steps per split.
+  int ks = 1;
+  if (forced_ks > 0) ks = forced_ks;
+  else if (blocks < 200) ks = (int)std::min<int64_t>((320 + blocks - 1) / blocks, nsup / 2);
+  ks = std::max(1, std::min(ks, nsup));
+  P.sup_per_split = (nsup + ks - 1) / ks;
+  P.ks = (nsup + P.sup_per_split - 1) / P.sup_per_split;
+  return P.ks > 1 ? (size_t)P.ks * P.M * P.N * sizeof(float) : 0;
+}
+
 hipError_t launch_qmm(const QmmParams& P, hipStream_t s) {
   if (!qmm_supported(P.M, P.N, P.K, P.bits, P.group_size)) return hipErrorNotSupported;
+  if (P.ks > 1 && !P.part) return hipErrorInvalidValue;
+  hipError_t e;
   if (P.bits == 4) {
     switch (P.group_size) {
-      case 32: return launch_gs<4, 32>(P, s);
-      case 64: return launch_gs<4, 64>(P, s);
-      default: return launch_gs<4, 128>(P, s);
+      case 32: e = launch_gs<4, 32>(P, s); break;
+      case 64: e = launch_gs<4, 64>(P, s); break;
+      default: e = launch_gs<4, 128>(P, s); break;
+    }
+  } else {
+    switch (P.group_size) {
+      case 32: e = launch_gs<8, 32>(P, s); break;
+      case 64: e = launch_gs<8, 64>(P, s); break;
+      default: e = launch_gs<8, 128>(P, s); break;
     }
   }
-  switch (P.group_size) {
-    case 32: return launch_gs<8, 32>(P, s);
-    case 64: return launch_gs<8, 64>(P, s);
-    default: return launch_gs<8, 128>(P, s);
-  }
+  if (e != hipSuccess || P.ks == 1) return e;
+  const int64_t mn = (int64_t)P.M * P.N;
+  int64_t g = (mn + 255) / 256;
+  if (g > 65535) g = 65535;
+  hipLaunchKernelGGL(qmm_reduce_kernel, dim3((unsigned)g), dim3(256), 0, s, P.part, P.y, mn, P.ks);
+  return hipGetLastError();
 }
 
 }  // namespace mi

@@ -127,11 +127,16 @@ def test_gather_decode_broadcast(dev):
     assert max_err_ratio(to_f64(y).reshape(2 * topk, 1, N), truth) <= BF16_TOL
 
 
-@pytest.mark.parametrize("M,K", [(1, 256), (3, 256), (1, 1024), (2, 2048)])
-def test_gather_sorted_matches_unsorted(dev, M, K):
-    """Sorted (grouped) path and unsorted path both match truth."""
-    _print_case(t="gather_sorted", M=M, K=K)
-    E, N, T, topk = 8, 64, 40, 3
+@pytest.mark.parametrize("M,K,E,T,topk", [(1, 256, 8, 40, 3), (3, 256, 8, 40, 3),
+                                          (1, 1024, 8, 40, 3), (2, 2048, 8, 40, 3),
+                                          (1, 512, 64, 20, 2), (1, 512, 40, 30, 2),
+                                          (1, 1024, 32, 40, 3), (2, 512, 16, 24, 2),
+                                          (1, 512, 4, 64, 4)])
+def test_gather_sorted_matches_unsorted(dev, M, K, E, T, topk):
+    """Sorted (grouped) path and unsorted path both match truth; the shapes cover work
+    items of 1, 2, 4 rows (16-row-tile kernel) and 8..32 rows (32-row-tile kernel)."""
+    _print_case(t="gather_sorted", M=M, K=K, E=E, T=T, topk=topk)
+    N = 64
     wq, s, b = weights(E, N, K, 4, 64, 77)
     rng = np.random.default_rng(5)
     flat = rng.integers(0, E, size=T * topk).astype(np.uint32)
