@@ -9,20 +9,24 @@ import subprocess
 import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "mi_qmm")
 LIB = os.path.join(OUT_DIR, "libmi_qmm.so")
 BUILD = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["qmv.hip", "qmv16.hip", "qmm.hip", "quant.hip", "moe.hip", "api.cpp"]
+HOST = os.path.join(HERE, "host")
+ROOT = os.path.dirname(HERE)
+SOURCES = ["csrc/qmv.hip", "csrc/qmv16.hip", "csrc/qmm.hip", "csrc/quant.hip", "csrc/moe.hip",
+           "csrc/api.cpp", "host/mi_host.cpp"]
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-         "-I", os.path.join(HERE, "..", "include")]
+         "-I", os.path.join(ROOT, "include"), "-I", HOST]
+TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_host.cpp")
+TEST_BIN = os.path.join(ROOT, "tests", "cpp", "_build", "test_host")
 
 
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC] + FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC] + FLAGS + ["-c", os.path.join(HERE, src), "-o", obj]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -35,7 +39,7 @@ def _compile(src):
 
 def build(verbose=True):
     os.makedirs(BUILD, exist_ok=True)
-    srcs = [s for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    srcs = [s for s in SOURCES if os.path.exists(os.path.join(HERE, s))]
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
@@ -47,6 +51,23 @@ def build(verbose=True):
     if verbose:
         print("built", LIB)
     return LIB
+
+
+def build_host_tests(verbose=True):
+    """The C++ host-mirror test binary (tests/cpp/test_host.cpp), linked against
+    libmi_qmm.so and the oracle (oracle/liboracle.so, its checker)."""
+    os.makedirs(os.path.dirname(TEST_BIN), exist_ok=True)
+    cmd = [HIPCC, "-O2", "-std=c++17", "-x", "hip", "--offload-arch=gfx950", TEST_SRC,
+           "-I", HOST, "-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROOT, "oracle"),
+           "-L", OUT_DIR, "-lmi_qmm", "-L", os.path.join(ROOT, "oracle"), "-loracle",
+           "-Wl,-rpath,$ORIGIN/../../../mlx-serve_amd/mi_qmm",
+           "-Wl,-rpath,$ORIGIN/../../../oracle", "-o", TEST_BIN]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("test_host build failed:\n" + r.stderr)
+    if verbose:
+        print("built", TEST_BIN)
+    return TEST_BIN
 
 
 if __name__ == "__main__":
