@@ -199,7 +199,8 @@ bool valid_x_dtype(int d) { return d == MI_DTYPE_BFLOAT16 || d == MI_DTYPE_FLOAT
 struct GatherJob {
   mi::QmvParams P{};
   QmvPlan plan{};
-  bool empty = false, narrow = false, use_items = false;
+  mi::Qmv1Plan plan1{};
+  bool empty = false, narrow = false, use_items = false, one_row = false;
   int64_t max_items = 0;
   size_t items_bytes = 0, part_bytes = 0;
   size_t items_region() const { return ((items_bytes + 255) / 256) * 256; }
@@ -284,11 +285,30 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
     P.items_per_pair = 1;
     P.n_items_fixed = 0;
   }
-  J.plan = J.narrow ? qmv16_plan(P.N, P.K, gs, nb, J.use_items ? P.rpi : rows, n_items, P.x_f32)
-                    : qmv_plan(P.N, P.K, gs, nb, J.use_items ? P.rpi : rows, n_items, P.x_f32);
-  P.ks = J.plan.ks;
-  P.gps = J.plan.gps;
-  P.row_blocks = J.plan.row_blocks;
+  // Items of exactly one activation row (dense M == 1, MoE decode pairs, sorted runs cut
+  // into single rows) stream through the one-row kernel when it supports the layout.
+  static const int use_qmv1 = env_int("MI_QMM_QMV1", 1);
+  J.one_row = use_qmv1 && ((J.use_items && P.rpi == 1) || (!J.use_items && M == 1));
+  J.one_row = J.one_row && mi::qmv1_supported(P.K, gs, nb, P.x_f32);
+  if (J.one_row) {
+    P.rpi = 1;
+    if (!J.use_items) {
+      P.items_per_pair = 1;
+      P.n_items_fixed = (int)n_idx;
+      n_items = n_idx;
+    }
+    J.plan1 = mi::qmv1_plan(P.N, P.K, gs, n_items);
+    P.ks = J.plan1.ks;
+    P.gps = J.plan1.gps;
+    P.row_blocks = J.plan1.tiles;
+    J.plan.cfg.grid_z = (int)(n_items < 65535 ? n_items : 65535);
+  } else {
+    J.plan = J.narrow ? qmv16_plan(P.N, P.K, gs, nb, J.use_items ? P.rpi : rows, n_items, P.x_f32)
+                      : qmv_plan(P.N, P.K, gs, nb, J.use_items ? P.rpi : rows, n_items, P.x_f32);
+    P.ks = J.plan.ks;
+    P.gps = J.plan.gps;
+    P.row_blocks = J.plan.row_blocks;
+  }
   J.items_bytes = J.use_items ? (size_t)J.max_items * 16 + 256 : 0;
   J.part_bytes = P.ks > 1 ? (size_t)P.ks * PT * N * 4 : 0;
   return MI_OK;
@@ -309,7 +329,9 @@ int gather_launch(GatherJob& J, void* ws, hipStream_t s) {
       P.item_count = count;
     }
   }
-  hipError_t e = J.narrow ? mi::launch_qmv16(P, J.plan.cfg, s) : mi::launch_qmv(P, J.plan.cfg, s);
+  hipError_t e = J.one_row ? mi::launch_qmv1(P, J.plan1, J.plan.cfg.grid_z, s)
+                 : J.narrow  ? mi::launch_qmv16(P, J.plan.cfg, s)
+                             : mi::launch_qmv(P, J.plan.cfg, s);
   return e == hipSuccess ? MI_OK : hip_fail(e, "qmv launch");
 }
 

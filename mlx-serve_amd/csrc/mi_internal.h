@@ -1,6 +1,8 @@
 // Internal (host + device) declarations shared by the kernels and the C ABI layer.
 #pragma once
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <stdint.h>
 
 namespace mi {
@@ -40,6 +42,15 @@ int qmv_groups_per_wave(int bits, int gs);
 size_t qmv_lds_bytes(int groups, int gs, int mr, int x_f32, int waves);
 hipError_t launch_qmv(const QmvParams& P, const QmvConfig& C, hipStream_t s);
 hipError_t launch_reduce_splits(const QmvParams& P, hipStream_t s);
+
+// One-row decode kernel (qmv1.hip): 4-bit, bf16 x, items of exactly one row.
+struct Qmv1Plan {
+  int ks, gps, waves, nc, xu, tiles;
+  size_t lds;
+};
+bool qmv1_supported(int K, int gs, int bits, int x_f32);
+Qmv1Plan qmv1_plan(int N, int K, int gs, int64_t n_items);
+hipError_t launch_qmv1(const QmvParams& P, const Qmv1Plan& plan, int grid_z, hipStream_t s);
 
 // Decode-width kernel (qmv16.hip): M <= 16 rows per item, 16-row weight tiles.
 int qmv16_mp_for_rows(int rows);

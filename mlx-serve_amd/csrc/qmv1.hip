@@ -1,0 +1,319 @@
+// Decode GEMV for work items of one activation row (dense M == 1, MoE decode pairs,
+// sorted items of one row), 4-bit affine, bf16 activations: the HBM-streaming kernel.
+//
+// A block owns a 16-row weight tile and W waves split its K range. Lane l of a wave
+// owns row l/4 and the 32-value slice l%4 of every 128-value chunk, so the 4 lanes of a
+// row read its 64 contiguous bytes per chunk. A wave issues ALL of its weight loads (16 B
+// per chunk per lane) and the matching scale/bias loads before anything waits on them;
+// the activation row is staged into LDS while they are in flight.
+//
+// Per 8 packed values: two masks split even/odd nibbles, v_perm builds bf16 pairs
+// 0x43qq (= 128 + q exactly) and v_dot2_f32_bf16 multiplies them with the activations,
+// which are staged in the same pair order ([x0,x2,x4,x6,x1,x3,x5,x7] per 8). The affine
+// terms are applied per 32-value slice in fp32: s*sum(x*(128+q)) + (b - 128 s)*sum(x),
+// with sum(x) per slice staged next to x. Rows reduce over their 4 lanes by shuffles and
+// over the W waves through LDS in wave order (deterministic).
+#include "mi_common.h"
+#include "mi_internal.h"
+#include "qmv_common.h"
+
+#include <cstdlib>
+
+namespace mi {
+namespace {
+
+using qmv_detail::decode_item;
+using qmv_detail::item_x_row;
+using qmv_detail::Item;
+using qmv_detail::lds_barrier;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kChunkVals = 128;
+
+MI_DEV float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// sum over 8 packed nibbles of x*(128+q); x4 holds the 8 activations in pair order.
+MI_DEV float dot8(uint32_t w, u32x4_t x4, float acc) {
+  constexpr uint32_t c43 = 0x43434343u;
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  acc = dot2(perm_b32(c43, lo, 0x04010400u), x4.x, acc);  // (q0, q2)
+  acc = dot2(perm_b32(c43, lo, 0x04030402u), x4.y, acc);  // (q4, q6)
+  acc = dot2(perm_b32(c43, hi, 0x04010400u), x4.z, acc);  // (q1, q3)
+  acc = dot2(perm_b32(c43, hi, 0x04030402u), x4.w, acc);  // (q5, q7)
+  return acc;
+}
+
+template <int GS>
+constexpr int groups_per_chunk() {
+  return kChunkVals / GS;
+}
+
+// Scale/bias of one chunk for one row: the GPC bf16 values of the chunk's groups.
+template <int GPC>
+struct SB {
+  uint32_t v[(GPC + 1) / 2];
+};
+
+template <int GPC>
+MI_DEV SB<GPC> load_sb(const uint16_t* p) {
+  SB<GPC> r;
+  if constexpr (GPC == 1) {
+    r.v[0] = *p;
+  } else if constexpr (GPC == 2) {
+    r.v[0] = *reinterpret_cast<const uint32_t*>(p);
+  } else {
+    const u32x2_t t = *reinterpret_cast<const u32x2_t*>(p);
+    r.v[0] = t.x;
+    r.v[1] = t.y;
+  }
+  return r;
+}
+
+// bf16 value of group (slice g's group) within the chunk.
+template <int GPC>
+MI_DEV float pick(const SB<GPC>& s, int g) {
+  if constexpr (GPC == 1) {
+    return bf16_bits_to_f32(s.v[0] & 0xFFFFu);
+  } else if constexpr (GPC == 2) {
+    return bf16_bits_to_f32(g >= 2 ? s.v[0] >> 16 : s.v[0] & 0xFFFFu);
+  } else {
+    const uint32_t w = g >= 2 ? s.v[1] : s.v[0];
+    return bf16_bits_to_f32((g & 1) ? w >> 16 : w & 0xFFFFu);
+  }
+}
+
+template <int GS, int NC, int XU>
+__global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
+  constexpr int GPC = groups_per_chunk<GS>();
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x, BD = blockDim.x, W = BD >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane >> 2, g = lane & 3;
+  const int K = P.K, N = P.N, G = K / GS;
+  const int tile = blockIdx.x, ks = blockIdx.y;
+  // Block K range (whole chunks) and this wave's chunks.
+  const int kb0 = ks * P.gps * GS;
+  const int kb1 = min(K, kb0 + P.gps * GS);
+  const int nchb = (kb1 - kb0) / kChunkVals;
+  const int per = (nchb + W - 1) / W;
+  const int c0 = min(wave * per, nchb - 1), nmine = max(1, min(per, nchb - c0));
+  const int nvals = kb1 - kb0, nunits = nvals / 8;
+  uint32_t* xs = reinterpret_cast<uint32_t*>(smem);               // nvals bf16, pair order
+  float* xsum = reinterpret_cast<float*>(smem + nvals * 2);        // nvals/32 slice sums
+  float* red = xsum + nvals / 32;                                  // [W][16]
+  const int n = tile * 16 + r;
+  const uint32_t nn = (uint32_t)min(n, N - 1);
+  const int64_t PT = P.n_pairs * P.M;
+  const int n_items = P.items ? (int)*P.item_count : P.n_items_fixed;
+
+  for (int it_i = blockIdx.z; it_i < n_items; it_i += gridDim.z) {
+    const Item it = decode_item(P, it_i);
+    if (it.cnt <= 0) continue;
+    const int64_t xr = item_x_row(P, it, 0);
+    if (xr == -1) continue;  // block-uniform
+    const uint32_t e = it.expert_ok ? it.expert : 0u;
+    const bool ok = it.expert_ok && xr >= 0;
+
+    // 1. every global load of this item, before anything waits: the activation units
+    //    this thread stages (first, so their LDS writes wait on nothing else), then the
+    //    weight words and scale/bias values of this wave's chunks. Indices are clamped so
+    //    no load sits behind a branch (loads beyond the range repeat valid addresses).
+    const uint16_t* xrow = reinterpret_cast<const uint16_t*>(P.x) + (xr < 0 ? 0 : xr) + kb0;
+    u32x4_t xv[XU];
+#pragma unroll
+    for (int i = 0; i < XU; ++i)
+      xv[i] = *reinterpret_cast<const u32x4_t*>(xrow + 8 * min(tid + i * BD, nunits - 1));
+    const uint32_t* wrow = P.w + ((uint64_t)e * (uint32_t)N + nn) * (uint32_t)(K / 8);
+    const uint16_t* srow = P.scales + ((uint64_t)e * (uint32_t)N + nn) * (uint32_t)G;
+    const uint16_t* brow = P.biases + ((uint64_t)e * (uint32_t)N + nn) * (uint32_t)G;
+    u32x4_t wv[NC];
+    SB<GPC> sv[NC], bv[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int k = kb0 + (c0 + min(j, nmine - 1)) * kChunkVals;
+      wv[j] = *reinterpret_cast<const u32x4_t*>(wrow + k / 8 + 4 * g);
+      sv[j] = load_sb<GPC>(srow + k / GS);
+      bv[j] = load_sb<GPC>(brow + k / GS);
+    }
+    // 2. stage the activations in pair order, with per-32-value sums.
+#pragma unroll
+    for (int i = 0; i < XU; ++i) {
+      const int u = tid + i * BD;
+      const u32x4_t X = xv[i];
+      float s8 = ((bf16_bits_to_f32(X.x & 0xFFFFu) + bf16_bits_to_f32(X.x >> 16)) +
+                  (bf16_bits_to_f32(X.y & 0xFFFFu) + bf16_bits_to_f32(X.y >> 16))) +
+                 ((bf16_bits_to_f32(X.z & 0xFFFFu) + bf16_bits_to_f32(X.z >> 16)) +
+                  (bf16_bits_to_f32(X.w & 0xFFFFu) + bf16_bits_to_f32(X.w >> 16)));
+      s8 += __shfl_xor(s8, 1, 64);
+      s8 += __shfl_xor(s8, 2, 64);
+      if (u < nunits) {
+        u32x4_t o;
+        o.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
+        o.y = perm_b32(X.w, X.z, 0x05040100u);  // (x4, x6)
+        o.z = perm_b32(X.y, X.x, 0x07060302u);  // (x1, x3)
+        o.w = perm_b32(X.w, X.z, 0x07060302u);  // (x5, x7)
+        *reinterpret_cast<u32x4_t*>(xs + u * 4) = o;
+        if ((u & 3) == 0) xsum[u >> 2] = s8;
+      }
+    }
+    // LDS-only barrier: the weight loads stay in flight.
+    lds_barrier();
+
+    // 3. dot products, chunk by chunk as the loads land (repeated chunks weigh 0).
+    float y = 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int jj = min(j, nmine - 1);
+      const int off = (c0 + jj) * kChunkVals + 32 * g;  // within the block range
+      const u32x4_t* xp = reinterpret_cast<const u32x4_t*>(xs + off / 2);
+      float acc = 0.f;
+      acc = dot8(wv[j].x, xp[0], acc);
+      acc = dot8(wv[j].y, xp[1], acc);
+      acc = dot8(wv[j].z, xp[2], acc);
+      acc = dot8(wv[j].w, xp[3], acc);
+      const float use = j < nmine ? 1.f : 0.f;
+      const float s = use * pick<GPC>(sv[j], g), b = use * pick<GPC>(bv[j], g);
+      y = fmaf(s, acc, y);
+      y = fmaf(fmaf(-128.f, s, b), xsum[off >> 5], y);
+    }
+    // 4. reduce the row's 4 lanes, then the waves in order.
+    y += __shfl_xor(y, 1, 64);
+    y += __shfl_xor(y, 2, 64);
+    if (g == 0) red[wave * 16 + r] = y;
+    lds_barrier();
+    if (tid < 16 && tile * 16 + tid < N) {
+      float v = 0.f;
+      for (int w2 = 0; w2 < W; ++w2) v += red[w2 * 16 + tid];
+      const int64_t p = it.pos0;
+      const int nout = tile * 16 + tid;
+      if (P.ks > 1) {
+        P.part[((int64_t)ks * PT + p) * N + nout] = v;
+      } else {
+        if (!ok) v = __builtin_nanf("");
+        ((uint16_t*)P.y)[p * N + nout] = (uint16_t)f32_to_bf16_bits(v);
+      }
+    }
+    lds_barrier();  // LDS is reused by the next item
+  }
+}
+
+template <int GS, int NC>
+hipError_t launch_nc(const QmvParams& P, dim3 grid, int waves, int xu, size_t lds,
+                     hipStream_t s) {
+  const dim3 block(64 * waves);
+  switch (xu) {
+    case 1: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 1>), grid, block, lds, s, P); break;
+    case 2: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 2>), grid, block, lds, s, P); break;
+    case 3: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 3>), grid, block, lds, s, P); break;
+    case 4: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 4>), grid, block, lds, s, P); break;
+    default: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 8>), grid, block, lds, s, P); break;
+  }
+  return hipGetLastError();
+}
+
+template <int GS>
+hipError_t launch_gs1(const QmvParams& P, dim3 grid, int waves, int nc, int xu, size_t lds,
+                      hipStream_t s) {
+  switch (nc) {
+    case 1: return launch_nc<GS, 1>(P, grid, waves, xu, lds, s);
+    case 2: return launch_nc<GS, 2>(P, grid, waves, xu, lds, s);
+    case 3: return launch_nc<GS, 3>(P, grid, waves, xu, lds, s);
+    case 4: return launch_nc<GS, 4>(P, grid, waves, xu, lds, s);
+    case 5: return launch_nc<GS, 5>(P, grid, waves, xu, lds, s);
+    case 6: return launch_nc<GS, 6>(P, grid, waves, xu, lds, s);
+    case 7: return launch_nc<GS, 7>(P, grid, waves, xu, lds, s);
+    case 8: return launch_nc<GS, 8>(P, grid, waves, xu, lds, s);
+    case 10: return launch_nc<GS, 10>(P, grid, waves, xu, lds, s);
+    case 12: return launch_nc<GS, 12>(P, grid, waves, xu, lds, s);
+    case 14: return launch_nc<GS, 14>(P, grid, waves, xu, lds, s);
+    default: return launch_nc<GS, 16>(P, grid, waves, xu, lds, s);
+  }
+}
+
+}  // namespace
+
+bool qmv1_supported(int K, int gs, int bits, int x_f32) {
+  return bits == 4 && !x_f32 && K % kChunkVals == 0 && (gs == 32 || gs == 64 || gs == 128);
+}
+
+size_t qmv1_lds_bytes(int vals, int waves) {
+  return (size_t)vals * 2 + (size_t)(vals / 32) * 4 + (size_t)waves * 16 * 4;
+}
+
+Qmv1Plan qmv1_plan(int N, int K, int gs, int64_t n_items) {
+  // Chunks per row = ks (block K splits) x waves x chunks per wave, exactly when possible
+  // so no chunk is loaded twice: aim for ~8 chunks (8 KiB of weights) per wave on big
+  // grids and ~4 on small ones, at most 8 waves per block and 16 chunks per wave.
+  static const int nc_set[] = {1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16};
+  const int nch = K / kChunkVals;
+  const int64_t tiles = (N + 15) / 16;
+  const int target = tiles * n_items >= 512 ? 8 : 4;
+  int best_ks = 0, best_w = 0, best_nc = 0;
+  double best = 1e30;
+  for (int ks = 1; ks <= nch; ++ks) {
+    if (nch % ks) continue;
+    const int per_split = nch / ks;
+    for (int w = 1; w <= 8; ++w) {
+      if (per_split % w) continue;
+      const int nc = per_split / w;
+      bool ok = false;
+      for (int v : nc_set) ok |= v == nc;
+      if (!ok) continue;
+      // prefer: no K split (it costs a second launch), chunks per wave near target, then
+      // more waves
+      const double cost = std::abs(nc - target) + 20.0 * (ks - 1) + 0.01 * (8 - w);
+      if (cost < best) {
+        best = cost;
+        best_ks = ks;
+        best_w = w;
+        best_nc = nc;
+      }
+    }
+  }
+  Qmv1Plan p;
+  if (!best_nc) {  // no exact factorization: round up (the last wave repeats a chunk)
+    int w = 1;
+    while (w < 8 && (nch + w - 1) / w > target) w <<= 1;
+    int per = (nch + w - 1) / w;
+    int ks = 1;
+    if (per > 16) {
+      ks = (per + 15) / 16;
+      per = 16;
+    }
+    const int ch_split = (nch + ks - 1) / ks;
+    best_ks = (nch + ch_split - 1) / ch_split;
+    best_w = std::max(1, std::min(w, (ch_split + per - 1) / per));
+    best_nc = (ch_split + best_w - 1) / best_w;
+    if (best_nc > 8 && best_nc < 16 && best_nc % 2) ++best_nc;
+  }
+  const int ch_split = (nch + best_ks - 1) / best_ks;
+  p.ks = (nch + ch_split - 1) / ch_split;
+  p.gps = ch_split * kChunkVals / gs;
+  p.waves = best_w;
+  p.nc = best_nc;
+  const int units = ch_split * kChunkVals / 8;
+  const int xu = (units + 64 * p.waves - 1) / (64 * p.waves);
+  p.xu = xu <= 4 ? xu : 8;
+  p.lds = qmv1_lds_bytes(ch_split * kChunkVals, p.waves);
+  p.tiles = (int)tiles;
+  return p;
+}
+
+hipError_t launch_qmv1(const QmvParams& P, const Qmv1Plan& plan, int grid_z, hipStream_t s) {
+  dim3 grid((unsigned)plan.tiles, (unsigned)P.ks, (unsigned)grid_z);
+  hipError_t e;
+  switch (P.group_size) {
+    case 32: e = launch_gs1<32>(P, grid, plan.waves, plan.nc, plan.xu, plan.lds, s); break;
+    case 64: e = launch_gs1<64>(P, grid, plan.waves, plan.nc, plan.xu, plan.lds, s); break;
+    default: e = launch_gs1<128>(P, grid, plan.waves, plan.nc, plan.xu, plan.lds, s); break;
+  }
+  if (e != hipSuccess || P.ks == 1) return e;
+  return launch_reduce_splits(P, s);
+}
+
+}  // namespace mi
