@@ -11,7 +11,8 @@
 // 0x43qq (= 128 + q exactly) and v_dot2_f32_bf16 multiplies them with the activations,
 // which are staged in the same pair order ([x0,x2,x4,x6,x1,x3,x5,x7] per 8). The affine
 // terms are applied per 32-value slice in fp32: s*sum(x*(128+q)) + (b - 128 s)*sum(x),
-// with sum(x) per slice staged next to x. Rows reduce over their 4 lanes by shuffles and
+// with sum(x) per slice staged next to x. Scales/biases (gs 64/32) are loaded once per
+// wave and row and handed to each chunk by DPP quad broadcasts. Rows reduce over their 4 lanes by shuffles and
 // over the W waves through LDS in wave order (deterministic).
 #include "mi_common.h"
 #include "mi_internal.h"
@@ -36,7 +37,10 @@ MI_DEV float dot2(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// sum over 8 packed nibbles of x*(128+q); x4 holds the 8 activations in pair order.
+// One word of 8 nibbles against its 8 activations: masks split even / odd nibbles into
+// bytes and v_perm pairs each byte with 0x43, giving bf16 0x43qq = 128 + q exactly (q < 16
+// fits the 7-bit mantissa). x4 holds the activations staged in the matching pair order
+// (x0, x2), (x4, x6), (x1, x3), (x5, x7), so acc += sum x_i (128 + q_i).
 MI_DEV float dot8(uint32_t w, u32x4_t x4, float acc) {
   constexpr uint32_t c43 = 0x43434343u;
   const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
@@ -45,6 +49,23 @@ MI_DEV float dot8(uint32_t w, u32x4_t x4, float acc) {
   acc = dot2(perm_b32(c43, hi, 0x04010400u), x4.z, acc);  // (q1, q3)
   acc = dot2(perm_b32(c43, hi, 0x04030402u), x4.w, acc);  // (q5, q7)
   return acc;
+}
+
+// Quad broadcast of lane `src` (0..3) of each group of 4 lanes (DPP quad_perm); `src`
+// is a constant once the chunk loop is unrolled.
+MI_DEV uint32_t quad_bcast(uint32_t v, int src) {
+  switch (src) {
+    case 0: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x00, 0xF, 0xF, false);
+    case 1: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x55, 0xF, 0xF, false);
+    case 2: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xAA, 0xF, 0xF, false);
+    default: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xFF, 0xF, 0xF, false);
+  }
+}
+
+// Lanes 0,1 of each quad take lane a, lanes 2,3 take lane a+1 (a = 0 or 2).
+MI_DEV uint32_t quad_pairs(uint32_t v, int a) {
+  return a == 0 ? (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x50, 0xF, 0xF, false)
+                : (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xFA, 0xF, 0xF, false);
 }
 
 template <int GS>
@@ -103,7 +124,7 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
   const int per = (nchb + W - 1) / W;
   const int c0 = min(wave * per, nchb - 1), nmine = max(1, min(per, nchb - c0));
   const int nvals = kb1 - kb0, nunits = nvals / 8;
-  uint32_t* xs = reinterpret_cast<uint32_t*>(smem);               // nvals bf16, pair order
+  uint32_t* xs = reinterpret_cast<uint32_t*>(smem);               // nvals bf16, dot8 order
   float* xsum = reinterpret_cast<float*>(smem + nvals * 2);        // nvals/32 slice sums
   float* red = xsum + nvals / 32;                                  // [W][16]
   const int n = tile * 16 + r;
@@ -132,15 +153,38 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
     const uint16_t* srow = P.scales + ((uint64_t)e * (uint32_t)N + nn) * (uint32_t)G;
     const uint16_t* brow = P.biases + ((uint64_t)e * (uint32_t)N + nn) * (uint32_t)G;
     u32x4_t wv[NC];
-    SB<GPC> sv[NC], bv[NC];
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
       const int k = kb0 + (c0 + min(j, nmine - 1)) * kChunkVals;
       wv[j] = *reinterpret_cast<const u32x4_t*>(wrow + k / 8 + 4 * g);
-      sv[j] = load_sb<GPC>(srow + k / GS);
-      bv[j] = load_sb<GPC>(brow + k / GS);
     }
-    // 2. stage the activations in pair order, with per-32-value sums.
+    // Scales/biases. gs 64/32: the wave's groups of a row are ND contiguous dwords; lane g
+    // of the row's quad loads dwords g, g+4, ... and chunks take theirs by a quad
+    // broadcast. gs 128: one bf16 per chunk, loaded per chunk.
+    constexpr int ND = GPC >= 2 ? NC * GPC / 2 : 1;
+    constexpr int NSL = (ND + 3) / 4;
+    uint32_t sd[NSL], bd[NSL];
+    SB<GPC> sv[GPC >= 2 ? 1 : NC], bv[GPC >= 2 ? 1 : NC];
+    if constexpr (GPC >= 2) {
+      const int g0 = (kb0 + c0 * kChunkVals) / GS;
+      const int dmax = nmine * GPC / 2 - 1;
+      const uint32_t* s32 = reinterpret_cast<const uint32_t*>(srow + g0);
+      const uint32_t* b32 = reinterpret_cast<const uint32_t*>(brow + g0);
+#pragma unroll
+      for (int i = 0; i < NSL; ++i) {
+        const int d = min(g + 4 * i, dmax);
+        sd[i] = s32[d];
+        bd[i] = b32[d];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const int k = kb0 + (c0 + min(j, nmine - 1)) * kChunkVals;
+        sv[j] = load_sb<GPC>(srow + k / GS);
+        bv[j] = load_sb<GPC>(brow + k / GS);
+      }
+    }
+    // 2. stage the activations in dot8's pair order, with per-32-value sums.
 #pragma unroll
     for (int i = 0; i < XU; ++i) {
       const int u = tid + i * BD;
@@ -177,7 +221,26 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
       acc = dot8(wv[j].z, xp[2], acc);
       acc = dot8(wv[j].w, xp[3], acc);
       const float use = j < nmine ? 1.f : 0.f;
-      const float s = use * pick<GPC>(sv[j], g), b = use * pick<GPC>(bv[j], g);
+      float s, b;
+      if constexpr (GPC == 2) {
+        // chunk j's groups are dword j: lane j % 4, slot j / 4 of the quad
+        const uint32_t sw = quad_bcast(sd[j >> 2], j & 3);
+        const uint32_t bw = quad_bcast(bd[j >> 2], j & 3);
+        s = bf16_bits_to_f32(g >= 2 ? sw >> 16 : sw & 0xFFFFu);
+        b = bf16_bits_to_f32(g >= 2 ? bw >> 16 : bw & 0xFFFFu);
+      } else if constexpr (GPC == 4) {
+        // chunk j's groups are dwords 2j, 2j+1: lanes g<2 take lane (2j)%4, g>=2 the next
+        const int a = (2 * j) & 3;
+        const uint32_t sw = quad_pairs(sd[(2 * j) >> 2], a);
+        const uint32_t bw = quad_pairs(bd[(2 * j) >> 2], a);
+        s = bf16_bits_to_f32((g & 1) ? sw >> 16 : sw & 0xFFFFu);
+        b = bf16_bits_to_f32((g & 1) ? bw >> 16 : bw & 0xFFFFu);
+      } else {
+        s = pick<GPC>(sv[j], g);
+        b = pick<GPC>(bv[j], g);
+      }
+      s *= use;
+      b *= use;
       y = fmaf(s, acc, y);
       y = fmaf(fmaf(-128.f, s, b), xsum[off >> 5], y);
     }
