@@ -107,7 +107,7 @@ MI_DEV float pick(const SB<GPC>& s, int g) {
   }
 }
 
-template <int GS, int NC, int XU>
+template <int GS, int NC, int XU, bool DENSE>
 __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
   constexpr int GPC = groups_per_chunk<GS>();
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -118,11 +118,15 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
   const int K = P.K, N = P.N, G = K / GS;
   const int tile = blockIdx.x, ks = blockIdx.y;
   // Block K range (whole chunks) and this wave's chunks.
+  // (the plan gives every wave NC chunks; only the last split can be shorter)
   const int kb0 = ks * P.gps * GS;
   const int kb1 = min(K, kb0 + P.gps * GS);
   const int nchb = (kb1 - kb0) / kChunkVals;
-  const int per = (nchb + W - 1) / W;
-  const int c0 = min(wave * per, nchb - 1), nmine = max(1, min(per, nchb - c0));
+  // A wave whose range starts past the end (rounded-up plans) loads a valid chunk but
+  // weighs everything 0.
+  const int c0 = min(wave * NC, nchb - 1);
+  const int nmine = wave * NC < nchb ? min(NC, nchb - c0) : 0;
+  const int nload = max(1, nmine);
   const int nvals = kb1 - kb0, nunits = nvals / 8;
   uint32_t* xs = reinterpret_cast<uint32_t*>(smem);               // nvals bf16, dot8 order
   float* xsum = reinterpret_cast<float*>(smem + nvals * 2);        // nvals/32 slice sums
@@ -130,13 +134,23 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
   const int n = tile * 16 + r;
   const uint32_t nn = (uint32_t)min(n, N - 1);
   const int64_t PT = P.n_pairs * P.M;
-  const int n_items = P.items ? (int)*P.item_count : P.n_items_fixed;
+  // Dense calls (one pair, no indices) skip the work-item decode entirely.
+  const int n_items = DENSE ? 1 : P.items ? (int)*P.item_count : P.n_items_fixed;
 
   for (int it_i = blockIdx.z; it_i < n_items; it_i += gridDim.z) {
-    const Item it = decode_item(P, it_i);
-    if (it.cnt <= 0) continue;
-    const int64_t xr = item_x_row(P, it, 0);
-    if (xr == -1) continue;  // block-uniform
+    Item it;
+    int64_t xr = 0;
+    if constexpr (DENSE) {
+      it.pos0 = 0;
+      it.cnt = 1;
+      it.expert = 0;
+      it.expert_ok = true;
+    } else {
+      it = decode_item(P, it_i);
+      if (it.cnt <= 0) continue;
+      xr = item_x_row(P, it, 0);
+      if (xr == -1) continue;  // block-uniform
+    }
     const uint32_t e = it.expert_ok ? it.expert : 0u;
     const bool ok = it.expert_ok && xr >= 0;
 
@@ -155,7 +169,7 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
     u32x4_t wv[NC];
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
-      const int k = kb0 + (c0 + min(j, nmine - 1)) * kChunkVals;
+      const int k = kb0 + (c0 + min(j, nload - 1)) * kChunkVals;
       wv[j] = *reinterpret_cast<const u32x4_t*>(wrow + k / 8 + 4 * g);
     }
     // Scales/biases. gs 64/32: the wave's groups of a row are ND contiguous dwords; lane g
@@ -167,7 +181,7 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
     SB<GPC> sv[GPC >= 2 ? 1 : NC], bv[GPC >= 2 ? 1 : NC];
     if constexpr (GPC >= 2) {
       const int g0 = (kb0 + c0 * kChunkVals) / GS;
-      const int dmax = nmine * GPC / 2 - 1;
+      const int dmax = nload * GPC / 2 - 1;
       const uint32_t* s32 = reinterpret_cast<const uint32_t*>(srow + g0);
       const uint32_t* b32 = reinterpret_cast<const uint32_t*>(brow + g0);
 #pragma unroll
@@ -179,7 +193,7 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
     } else {
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
-        const int k = kb0 + (c0 + min(j, nmine - 1)) * kChunkVals;
+        const int k = kb0 + (c0 + min(j, nload - 1)) * kChunkVals;
         sv[j] = load_sb<GPC>(srow + k / GS);
         bv[j] = load_sb<GPC>(brow + k / GS);
       }
@@ -212,7 +226,7 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
     float y = 0.f;
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
-      const int jj = min(j, nmine - 1);
+      const int jj = min(j, nload - 1);
       const int off = (c0 + jj) * kChunkVals + 32 * g;  // within the block range
       const u32x4_t* xp = reinterpret_cast<const u32x4_t*>(xs + off / 2);
       float acc = 0.f;
@@ -265,17 +279,23 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
   }
 }
 
+template <int GS, int NC, bool DENSE>
+void launch_xu(const QmvParams& P, dim3 grid, dim3 block, int xu, size_t lds, hipStream_t s) {
+  switch (xu) {
+    case 1: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 1, DENSE>), grid, block, lds, s, P); break;
+    case 2: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 2, DENSE>), grid, block, lds, s, P); break;
+    case 4: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 4, DENSE>), grid, block, lds, s, P); break;
+    default: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 8, DENSE>), grid, block, lds, s, P); break;
+  }
+}
+
 template <int GS, int NC>
 hipError_t launch_nc(const QmvParams& P, dim3 grid, int waves, int xu, size_t lds,
                      hipStream_t s) {
   const dim3 block(64 * waves);
-  switch (xu) {
-    case 1: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 1>), grid, block, lds, s, P); break;
-    case 2: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 2>), grid, block, lds, s, P); break;
-    case 3: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 3>), grid, block, lds, s, P); break;
-    case 4: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 4>), grid, block, lds, s, P); break;
-    default: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 8>), grid, block, lds, s, P); break;
-  }
+  const bool dense = !P.items && !P.lhs && !P.rhs && P.n_pairs == 1 && P.M == 1;
+  if (dense) launch_xu<GS, NC, true>(P, grid, block, xu, lds, s);
+  else launch_xu<GS, NC, false>(P, grid, block, xu, lds, s);
   return hipGetLastError();
 }
 
@@ -361,7 +381,7 @@ Qmv1Plan qmv1_plan(int N, int K, int gs, int64_t n_items) {
   p.nc = best_nc;
   const int units = ch_split * kChunkVals / 8;
   const int xu = (units + 64 * p.waves - 1) / (64 * p.waves);
-  p.xu = xu <= 4 ? xu : 8;
+  p.xu = xu <= 2 ? xu : xu <= 4 ? 4 : 8;
   p.lds = qmv1_lds_bytes(ch_split * kChunkVals, p.waves);
   p.tiles = (int)tiles;
   return p;
