@@ -289,7 +289,7 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
   // into single rows) stream through the one-row kernel when it supports the layout.
   static const int use_qmv1 = env_int("MI_QMM_QMV1", 1);
   J.one_row = use_qmv1 && ((J.use_items && P.rpi == 1) || (!J.use_items && M == 1));
-  J.one_row = J.one_row && mi::qmv1_supported(P.K, gs, nb, P.x_f32);
+  J.one_row = J.one_row && mi::qmv1_supported(P.N, P.K, gs, nb, P.x_f32);
   if (J.one_row) {
     P.rpi = 1;
     if (!J.use_items) {

@@ -48,7 +48,7 @@ struct Qmv1Plan {
   int ks, gps, waves, nc, xu, tiles;
   size_t lds;
 };
-bool qmv1_supported(int K, int gs, int bits, int x_f32);
+bool qmv1_supported(int N, int K, int gs, int bits, int x_f32);
 Qmv1Plan qmv1_plan(int N, int K, int gs, int64_t n_items);
 hipError_t launch_qmv1(const QmvParams& P, const Qmv1Plan& plan, int grid_z, hipStream_t s);
 

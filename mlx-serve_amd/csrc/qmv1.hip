@@ -31,6 +31,8 @@ using qmv_detail::lds_barrier;
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kChunkVals = 128;
+// Buffer resource word 3 for raw (untyped) dword access on this target.
+constexpr int kBufFlags = 0x00020000;
 
 MI_DEV float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
@@ -134,68 +136,51 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
   const int n = tile * 16 + r;
   const uint32_t nn = (uint32_t)min(n, N - 1);
   const int64_t PT = P.n_pairs * P.M;
-  // Dense calls (one pair, no indices) skip the work-item decode entirely.
-  const int n_items = DENSE ? 1 : P.items ? (int)*P.item_count : P.n_items_fixed;
 
-  for (int it_i = blockIdx.z; it_i < n_items; it_i += gridDim.z) {
-    Item it;
-    int64_t xr = 0;
-    if constexpr (DENSE) {
-      it.pos0 = 0;
-      it.cnt = 1;
-      it.expert = 0;
-      it.expert_ok = true;
-    } else {
-      it = decode_item(P, it_i);
-      if (it.cnt <= 0) continue;
-      xr = item_x_row(P, it, 0);
-      if (xr == -1) continue;  // block-uniform
-    }
-    const uint32_t e = it.expert_ok ? it.expert : 0u;
+  auto process = [&](const Item& it, int64_t xr) {
+    const uint32_t e = __builtin_amdgcn_readfirstlane(it.expert_ok ? it.expert : 0u);
     const bool ok = it.expert_ok && xr >= 0;
 
-    // 1. every global load of this item, before anything waits: the activation units
-    //    this thread stages (first, so their LDS writes wait on nothing else), then the
-    //    weight words and scale/bias values of this wave's chunks. Indices are clamped so
-    //    no load sits behind a branch (loads beyond the range repeat valid addresses).
-    const uint16_t* xrow = reinterpret_cast<const uint16_t*>(P.x) + (xr < 0 ? 0 : xr) + kb0;
+    // 1. every global load of this item, before anything waits, as buffer loads from
+    //    per-matrix resources: 32-bit lane offsets, chunk / slot strides folded into the
+    //    instructions' immediate offsets. Reads past a wave's range only feed chunks that
+    //    weigh 0, and reads past a resource's end return 0.
+    const uint16_t* xb = reinterpret_cast<const uint16_t*>(P.x) + (xr < 0 ? 0 : xr) + kb0;
+    const __amdgpu_buffer_rsrc_t xres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, nvals * 2, kBufFlags);
+    const size_t mat = (size_t)e * (uint32_t)N;
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.w + mat * (uint32_t)(K / 8)), (short)0, N * (K / 2), kBufFlags);
+    const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.scales + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
+    const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.biases + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
     u32x4_t xv[XU];
 #pragma unroll
     for (int i = 0; i < XU; ++i)
-      xv[i] = *reinterpret_cast<const u32x4_t*>(xrow + 8 * min(tid + i * BD, nunits - 1));
-    const uint32_t* wrow = P.w + ((uint64_t)e * (uint32_t)N + nn) * (uint32_t)(K / 8);
-    const uint16_t* srow = P.scales + ((uint64_t)e * (uint32_t)N + nn) * (uint32_t)G;
-    const uint16_t* brow = P.biases + ((uint64_t)e * (uint32_t)N + nn) * (uint32_t)G;
+      xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xres, (tid + i * BD) * 16, 0, 0);
+    const uint32_t wo = nn * (uint32_t)(K / 2) + (uint32_t)(kb0 + c0 * kChunkVals) / 2 + 16 * g;
     u32x4_t wv[NC];
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      const int k = kb0 + (c0 + min(j, nload - 1)) * kChunkVals;
-      wv[j] = *reinterpret_cast<const u32x4_t*>(wrow + k / 8 + 4 * g);
-    }
-    // Scales/biases. gs 64/32: the wave's groups of a row are ND contiguous dwords; lane g
+    for (int j = 0; j < NC; ++j) wv[j] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * j, 0, 0);
+    // Scales/biases. gs 64/32: the wave's groups of a row are contiguous dwords; lane g
     // of the row's quad loads dwords g, g+4, ... and chunks take theirs by a quad
-    // broadcast. gs 128: one bf16 per chunk, loaded per chunk.
+    // broadcast. gs 128: one bf16 per chunk.
     constexpr int ND = GPC >= 2 ? NC * GPC / 2 : 1;
     constexpr int NSL = (ND + 3) / 4;
-    uint32_t sd[NSL], bd[NSL];
-    SB<GPC> sv[GPC >= 2 ? 1 : NC], bv[GPC >= 2 ? 1 : NC];
+    const uint32_t so = nn * (uint32_t)(G * 2) + (uint32_t)((kb0 + c0 * kChunkVals) / GS) * 2;
+    uint32_t sd[GPC >= 2 ? NSL : NC], bd[GPC >= 2 ? NSL : NC];
     if constexpr (GPC >= 2) {
-      const int g0 = (kb0 + c0 * kChunkVals) / GS;
-      const int dmax = nload * GPC / 2 - 1;
-      const uint32_t* s32 = reinterpret_cast<const uint32_t*>(srow + g0);
-      const uint32_t* b32 = reinterpret_cast<const uint32_t*>(brow + g0);
 #pragma unroll
       for (int i = 0; i < NSL; ++i) {
-        const int d = min(g + 4 * i, dmax);
-        sd[i] = s32[d];
-        bd[i] = b32[d];
+        sd[i] = __builtin_amdgcn_raw_buffer_load_b32(sres, so + 4 * g + 16 * i, 0, 0);
+        bd[i] = __builtin_amdgcn_raw_buffer_load_b32(bres, so + 4 * g + 16 * i, 0, 0);
       }
     } else {
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
-        const int k = kb0 + (c0 + min(j, nload - 1)) * kChunkVals;
-        sv[j] = load_sb<GPC>(srow + k / GS);
-        bv[j] = load_sb<GPC>(brow + k / GS);
+        sd[j] = __builtin_amdgcn_raw_buffer_load_b16(sres, so + 2 * j, 0, 0);
+        bd[j] = __builtin_amdgcn_raw_buffer_load_b16(bres, so + 2 * j, 0, 0);
       }
     }
     // 2. stage the activations in dot8's pair order, with per-32-value sums.
@@ -222,7 +207,7 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
     // LDS-only barrier: the weight loads stay in flight.
     lds_barrier();
 
-    // 3. dot products, chunk by chunk as the loads land (repeated chunks weigh 0).
+    // 3. dot products, chunk by chunk as the loads land (chunks past the range weigh 0).
     float y = 0.f;
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
@@ -250,8 +235,8 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
         s = bf16_bits_to_f32((g & 1) ? sw >> 16 : sw & 0xFFFFu);
         b = bf16_bits_to_f32((g & 1) ? bw >> 16 : bw & 0xFFFFu);
       } else {
-        s = pick<GPC>(sv[j], g);
-        b = pick<GPC>(bv[j], g);
+        s = bf16_bits_to_f32(sd[j] & 0xFFFFu);
+        b = bf16_bits_to_f32(bd[j] & 0xFFFFu);
       }
       s *= use;
       b *= use;
@@ -275,7 +260,26 @@ __global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
         ((uint16_t*)P.y)[p * N + nout] = (uint16_t)f32_to_bf16_bits(v);
       }
     }
-    lds_barrier();  // LDS is reused by the next item
+  };
+
+  if constexpr (DENSE) {
+    // one pair, no indices: straight-line, no work-item decode
+    Item it;
+    it.pos0 = 0;
+    it.cnt = 1;
+    it.expert = 0;
+    it.expert_ok = true;
+    process(it, 0);
+  } else {
+    const int n_items = P.items ? (int)*P.item_count : P.n_items_fixed;
+    for (int it_i = blockIdx.z; it_i < n_items; it_i += gridDim.z) {
+      const Item it = decode_item(P, it_i);
+      if (it.cnt <= 0) continue;
+      const int64_t xr = item_x_row(P, it, 0);
+      if (xr == -1) continue;  // block-uniform
+      process(it, xr);
+      lds_barrier();  // LDS is reused by the next item
+    }
   }
 }
 
@@ -320,8 +324,10 @@ hipError_t launch_gs1(const QmvParams& P, dim3 grid, int waves, int nc, int xu, 
 
 }  // namespace
 
-bool qmv1_supported(int K, int gs, int bits, int x_f32) {
-  return bits == 4 && !x_f32 && K % kChunkVals == 0 && (gs == 32 || gs == 64 || gs == 128);
+bool qmv1_supported(int N, int K, int gs, int bits, int x_f32) {
+  // buffer resources address one expert's matrix with 32-bit byte offsets
+  return bits == 4 && !x_f32 && K % kChunkVals == 0 && (gs == 32 || gs == 64 || gs == 128) &&
+         (int64_t)N * (K / 2) < ((int64_t)1 << 31);
 }
 
 size_t qmv1_lds_bytes(int vals, int waves) {
