@@ -109,8 +109,9 @@ MI_DEV float pick(const SB<GPC>& s, int g) {
   }
 }
 
+// Up to 16 waves per block when a wave holds <= 8 chunks (<= 128 VGPRs), else 8.
 template <int GS, int NC, int XU, bool DENSE>
-__global__ void __launch_bounds__(512) qmv1_kernel(QmvParams P) {
+__global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P) {
   constexpr int GPC = groups_per_chunk<GS>();
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, BD = blockDim.x, W = BD >> 6;
@@ -341,21 +342,30 @@ Qmv1Plan qmv1_plan(int N, int K, int gs, int64_t n_items) {
   static const int nc_set[] = {1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16};
   const int nch = K / kChunkVals;
   const int64_t tiles = (N + 15) / 16;
-  const int target = tiles * n_items >= 512 ? 8 : 4;
+  static const int env_target = [] {
+    const char* v = std::getenv("MI_QMV1_TARGET");
+    return v ? std::atoi(v) : 0;
+  }();
+  static const int env_ks_pen = [] {
+    const char* v = std::getenv("MI_QMV1_KSPEN");
+    return v ? std::atoi(v) : 20;
+  }();
+  const int target = env_target ? env_target : 4;
   int best_ks = 0, best_w = 0, best_nc = 0;
   double best = 1e30;
   for (int ks = 1; ks <= nch; ++ks) {
     if (nch % ks) continue;
     const int per_split = nch / ks;
-    for (int w = 1; w <= 8; ++w) {
+    for (int w = 1; w <= 16; ++w) {
       if (per_split % w) continue;
       const int nc = per_split / w;
+      if (w > 8 && nc > 8) continue;  // 16-wave blocks need <= 8 chunks per wave
       bool ok = false;
       for (int v : nc_set) ok |= v == nc;
       if (!ok) continue;
       // prefer: no K split (it costs a second launch), chunks per wave near target, then
       // more waves
-      const double cost = std::abs(nc - target) + 20.0 * (ks - 1) + 0.01 * (8 - w);
+      const double cost = std::abs(nc - target) + env_ks_pen * (ks - 1) + 0.01 * (16 - w);
       if (cost < best) {
         best = cost;
         best_ks = ks;
