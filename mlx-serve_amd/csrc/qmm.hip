@@ -66,7 +66,10 @@ struct WRegs {
   uint32_t s[TN][kGroups], b[TN][kGroups];  // bf16 bits of scales / biases
 };
 
-template <int BITS, int GS, int BM>
+// SPLIT: this launch is one of several K ranges and writes fp32 partials (a template
+// parameter, so each instance has a single epilogue: a per-element branch there makes the
+// 256-accumulator instance spill).
+template <int BITS, int GS, int BM, bool SPLIT>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 qmm_kernel(QmmParams P) {
   constexpr int TM = BM / 32;  // 32-row MFMA tiles per wave (the wave covers all BM rows)
@@ -291,7 +294,7 @@ qmm_kernel(QmmParams P) {
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + i * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
         if (m >= M) continue;
-        if (P.part) P.part[((int64_t)split * M + m) * N + n] = acc[i][j][r];
+        if constexpr (SPLIT) P.part[((int64_t)split * M + m) * N + n] = acc[i][j][r];
         else P.y[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[i][j][r]);
       }
   }
@@ -301,12 +304,14 @@ template <int BITS, int GS, int BM>
 hipError_t launch_bm(const QmmParams& P, hipStream_t s) {
   const int mtiles = (P.M + BM - 1) / BM, ntiles = (P.N + kBN - 1) / kBN;
   const size_t lds = kRing * (size_t)BM * kRowBytes;
-  auto k = qmm_kernel<BITS, GS, BM>;
+  auto k = P.ks > 1 ? qmm_kernel<BITS, GS, BM, true> : qmm_kernel<BITS, GS, BM, false>;
   static bool attr = false;
   if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
-    if (e != hipSuccess) return e;
+    for (auto kk : {qmm_kernel<BITS, GS, BM, true>, qmm_kernel<BITS, GS, BM, false>}) {
+      hipError_t e = hipFuncSetAttribute((const void*)kk,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+    }
     attr = true;
   }
   hipLaunchKernelGGL(k, dim3((unsigned)(mtiles * ntiles), (unsigned)P.ks), dim3(kThreads), lds, s,
