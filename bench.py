@@ -261,7 +261,7 @@ def shared_expert_8bit(torch, mi, dev, Ts, steps=10, warmup=2):
 def pmc_traffic():
     """HBM bytes per decode launch, from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     summary (counters scaled by a copy kernel of known size); None if absent."""
-    path = os.path.join(ROOT, "profiles", "qmv16_decode_llama8b_mlp_pmc_traffic.md")
+    path = os.path.join(ROOT, "profiles", "qmv1_decode_llama8b_mlp_pmc_traffic.md")
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
@@ -354,7 +354,7 @@ def main():
                    "tokens_per_s": round(head["tokens_per_s"], 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": pmc_traffic(), "kernel": "mi::qmv16_kernel<4, 64, 1, false>",
+                     "traffic": pmc_traffic(), "kernel": "mi::qmv1_kernel<64, NC, XU, true> (dense M=1 instances)",
                      "bytes_per_launch": head["bytes_per_launch"],
                      "avg_launch_us": round(head["avg_launch_us"], 3)},
         "cpu_baseline": cpu,
