@@ -45,12 +45,15 @@ hipError_t launch_reduce_splits(const QmvParams& P, hipStream_t s);
 
 // One-row decode kernel (qmv1.hip): 4-bit, bf16 x, items of exactly one row.
 struct Qmv1Plan {
-  int ks, gps, waves, nc, xu, tiles;
+  int ks, gps, waves, nc, xu, depth, tiles;
   size_t lds;
 };
 bool qmv1_supported(int N, int K, int gs, int bits, int x_f32);
 Qmv1Plan qmv1_plan(int N, int K, int gs, int64_t n_items);
 hipError_t launch_qmv1(const QmvParams& P, const Qmv1Plan& plan, int grid_z, hipStream_t s);
+template <int GS>
+hipError_t launch_qmv1_gs(const QmvParams& P, dim3 grid, int waves, int nc, int xu, int depth,
+                          size_t lds, hipStream_t s);
 
 // Decode-width kernel (qmv16.hip): M <= 16 rows per item, 16-row weight tiles.
 int qmv16_mp_for_rows(int rows);

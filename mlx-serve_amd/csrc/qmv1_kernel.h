@@ -1,0 +1,313 @@
+// Decode GEMV for work items of one activation row (dense M == 1, MoE decode pairs,
+// sorted items of one row), 4-bit affine, bf16 activations: the HBM-streaming kernel.
+//
+// A block owns a 16-row weight tile and W waves split its K range. Lane l of a wave
+// owns row l/4 and the 32-value slice l%4 of every 128-value chunk, so the 4 lanes of a
+// row read its 64 contiguous bytes per chunk. A wave first issues its activation loads
+// and its scale/bias loads, then its weight loads (16 B per chunk per lane): DEPTH
+// chunks up front and one more as each chunk is consumed. The activation row is staged
+// into LDS while the weights are in flight.
+//
+// Per 8 packed values: two masks split even/odd nibbles, v_perm builds bf16 pairs
+// 0x43qq (= 128 + q exactly) and v_dot2_f32_bf16 multiplies them with the activations,
+// which are staged in the same pair order ([x0,x2,x4,x6,x1,x3,x5,x7] per 8). The affine
+// terms are applied per 32-value slice in fp32: s*sum(x*(128+q)) + (b - 128 s)*sum(x),
+// with sum(x) per slice staged next to x. Scales/biases (gs 64/32) are loaded once per
+// wave and row and handed to each chunk by DPP quad broadcasts. Rows reduce over their
+// 4 lanes by shuffles and over the W waves through LDS in wave order (deterministic).
+#pragma once
+#include "mi_common.h"
+#include "mi_internal.h"
+#include "qmv_common.h"
+
+
+namespace mi {
+namespace qmv1_detail {
+
+using qmv_detail::decode_item;
+using qmv_detail::item_x_row;
+using qmv_detail::Item;
+using qmv_detail::lds_barrier;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kChunkVals = 128;
+// Buffer resource word 3 for raw (untyped) dword access on this target.
+constexpr int kBufFlags = 0x00020000;
+
+MI_DEV float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// One word of 8 nibbles against its 8 activations: masks split even / odd nibbles into
+// bytes and v_perm pairs each byte with 0x43, giving bf16 0x43qq = 128 + q exactly (q < 16
+// fits the 7-bit mantissa). x4 holds the activations staged in the matching pair order
+// (x0, x2), (x4, x6), (x1, x3), (x5, x7), so acc += sum x_i (128 + q_i).
+MI_DEV float dot8(uint32_t w, u32x4_t x4, float acc) {
+  constexpr uint32_t c43 = 0x43434343u;
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  acc = dot2(perm_b32(c43, lo, 0x04010400u), x4.x, acc);  // (q0, q2)
+  acc = dot2(perm_b32(c43, lo, 0x04030402u), x4.y, acc);  // (q4, q6)
+  acc = dot2(perm_b32(c43, hi, 0x04010400u), x4.z, acc);  // (q1, q3)
+  acc = dot2(perm_b32(c43, hi, 0x04030402u), x4.w, acc);  // (q5, q7)
+  return acc;
+}
+
+// Quad broadcast of lane `src` (0..3) of each group of 4 lanes (DPP quad_perm); `src`
+// is a constant once the chunk loop is unrolled.
+MI_DEV uint32_t quad_bcast(uint32_t v, int src) {
+  switch (src) {
+    case 0: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x00, 0xF, 0xF, false);
+    case 1: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x55, 0xF, 0xF, false);
+    case 2: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xAA, 0xF, 0xF, false);
+    default: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xFF, 0xF, 0xF, false);
+  }
+}
+
+// Lanes 0,1 of each quad take lane a, lanes 2,3 take lane a+1 (a = 0 or 2).
+MI_DEV uint32_t quad_pairs(uint32_t v, int a) {
+  return a == 0 ? (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x50, 0xF, 0xF, false)
+                : (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xFA, 0xF, 0xF, false);
+}
+
+template <int GS>
+constexpr int groups_per_chunk() {
+  return kChunkVals / GS;
+}
+
+// Up to 16 waves per block when a wave holds <= 8 chunks (<= 128 VGPRs), else 8.
+template <int GS, int NC, int XU, int DEPTH, bool DENSE>
+__global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P) {
+  constexpr int GPC = groups_per_chunk<GS>();
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x, BD = blockDim.x, W = BD >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane >> 2, g = lane & 3;
+  const int K = P.K, N = P.N, G = K / GS;
+  const int tile = blockIdx.x, ks = blockIdx.y;
+  // Block K range (whole chunks) and this wave's chunks.
+  // (the plan gives every wave NC chunks; only the last split can be shorter)
+  const int kb0 = ks * P.gps * GS;
+  const int kb1 = min(K, kb0 + P.gps * GS);
+  const int nchb = (kb1 - kb0) / kChunkVals;
+  // A wave whose range starts past the end (rounded-up plans) loads a valid chunk but
+  // weighs everything 0.
+  const int c0 = min(wave * NC, nchb - 1);
+  const int nmine = wave * NC < nchb ? min(NC, nchb - c0) : 0;
+  const int nload = max(1, nmine);
+  const int nvals = kb1 - kb0, nunits = nvals / 8;
+  uint32_t* xs = reinterpret_cast<uint32_t*>(smem);               // nvals bf16, dot8 order
+  float* xsum = reinterpret_cast<float*>(smem + nvals * 2);        // nvals/32 slice sums
+  float* red = xsum + nvals / 32;                                  // [W][16]
+  const int n = tile * 16 + r;
+  const uint32_t nn = (uint32_t)min(n, N - 1);
+  const int64_t PT = P.n_pairs * P.M;
+
+  auto process = [&](const Item& it, int64_t xr) {
+    const uint32_t e = __builtin_amdgcn_readfirstlane(it.expert_ok ? it.expert : 0u);
+    const bool ok = it.expert_ok && xr >= 0;
+
+    // 1. every global load of this item, before anything waits, as buffer loads from
+    //    per-matrix resources: 32-bit lane offsets, chunk / slot strides folded into the
+    //    instructions' immediate offsets. Reads past a wave's range only feed chunks that
+    //    weigh 0, and reads past a resource's end return 0.
+    const uint16_t* xb = reinterpret_cast<const uint16_t*>(P.x) + (xr < 0 ? 0 : xr) + kb0;
+    const __amdgpu_buffer_rsrc_t xres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, nvals * 2, kBufFlags);
+    const size_t mat = (size_t)e * (uint32_t)N;
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.w + mat * (uint32_t)(K / 8)), (short)0, N * (K / 2), kBufFlags);
+    const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.scales + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
+    const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.biases + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
+    u32x4_t xv[XU];
+#pragma unroll
+    for (int i = 0; i < XU; ++i)
+      xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xres, (tid + i * BD) * 16, 0, 0);
+    const uint32_t wo = nn * (uint32_t)(K / 2) + (uint32_t)(kb0 + c0 * kChunkVals) / 2 + 16 * g;
+    // Scales/biases. gs 64/32: the wave's groups of a row are contiguous dwords; lane g
+    // of the row's quad loads dwords g, g+4, ... and chunks take theirs by a quad
+    // broadcast. gs 128: one bf16 per chunk.
+    constexpr int ND = GPC >= 2 ? NC * GPC / 2 : 1;
+    constexpr int NSL = (ND + 3) / 4;
+    const uint32_t so = nn * (uint32_t)(G * 2) + (uint32_t)((kb0 + c0 * kChunkVals) / GS) * 2;
+    uint32_t sd[GPC >= 2 ? NSL : NC], bd[GPC >= 2 ? NSL : NC];
+    if constexpr (GPC >= 2) {
+#pragma unroll
+      for (int i = 0; i < NSL; ++i) {
+        sd[i] = __builtin_amdgcn_raw_buffer_load_b32(sres, so + 4 * g + 16 * i, 0, 0);
+        bd[i] = __builtin_amdgcn_raw_buffer_load_b32(bres, so + 4 * g + 16 * i, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        sd[j] = __builtin_amdgcn_raw_buffer_load_b16(sres, so + 2 * j, 0, 0);
+        bd[j] = __builtin_amdgcn_raw_buffer_load_b16(bres, so + 2 * j, 0, 0);
+      }
+    }
+    // Weights: the first D chunks now, then one more as each chunk is consumed, so a
+    // wave's data arrives in the order it is used.
+    constexpr int D = DEPTH < NC ? DEPTH : NC;
+    u32x4_t wv[NC];
+#pragma unroll
+    for (int j = 0; j < D; ++j) wv[j] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * j, 0, 0);
+    // 2. stage the activations in dot8's pair order, with per-32-value sums.
+#pragma unroll
+    for (int i = 0; i < XU; ++i) {
+      const int u = tid + i * BD;
+      const u32x4_t X = xv[i];
+      float s8 = ((bf16_bits_to_f32(X.x & 0xFFFFu) + bf16_bits_to_f32(X.x >> 16)) +
+                  (bf16_bits_to_f32(X.y & 0xFFFFu) + bf16_bits_to_f32(X.y >> 16))) +
+                 ((bf16_bits_to_f32(X.z & 0xFFFFu) + bf16_bits_to_f32(X.z >> 16)) +
+                  (bf16_bits_to_f32(X.w & 0xFFFFu) + bf16_bits_to_f32(X.w >> 16)));
+      s8 += __shfl_xor(s8, 1, 64);
+      s8 += __shfl_xor(s8, 2, 64);
+      if (u < nunits) {
+        u32x4_t o;
+        o.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
+        o.y = perm_b32(X.w, X.z, 0x05040100u);  // (x4, x6)
+        o.z = perm_b32(X.y, X.x, 0x07060302u);  // (x1, x3)
+        o.w = perm_b32(X.w, X.z, 0x07060302u);  // (x5, x7)
+        *reinterpret_cast<u32x4_t*>(xs + u * 4) = o;
+        if ((u & 3) == 0) xsum[u >> 2] = s8;
+      }
+    }
+    // LDS-only barrier: the weight loads stay in flight.
+    lds_barrier();
+
+    // 3. dot products, chunk by chunk as the loads land (chunks past the range weigh 0).
+    float y = 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      if constexpr (D < NC) {
+        if (j + D < NC) wv[j + D] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * (j + D), 0, 0);
+      }
+      const int jj = min(j, nload - 1);
+      const int off = (c0 + jj) * kChunkVals + 32 * g;  // within the block range
+      const u32x4_t* xp = reinterpret_cast<const u32x4_t*>(xs + off / 2);
+      float acc = 0.f;
+      acc = dot8(wv[j].x, xp[0], acc);
+      acc = dot8(wv[j].y, xp[1], acc);
+      acc = dot8(wv[j].z, xp[2], acc);
+      acc = dot8(wv[j].w, xp[3], acc);
+      const float use = j < nmine ? 1.f : 0.f;
+      float s, b;
+      if constexpr (GPC == 2) {
+        // chunk j's groups are dword j: lane j % 4, slot j / 4 of the quad
+        const uint32_t sw = quad_bcast(sd[j >> 2], j & 3);
+        const uint32_t bw = quad_bcast(bd[j >> 2], j & 3);
+        s = bf16_bits_to_f32(g >= 2 ? sw >> 16 : sw & 0xFFFFu);
+        b = bf16_bits_to_f32(g >= 2 ? bw >> 16 : bw & 0xFFFFu);
+      } else if constexpr (GPC == 4) {
+        // chunk j's groups are dwords 2j, 2j+1: lanes g<2 take lane (2j)%4, g>=2 the next
+        const int a = (2 * j) & 3;
+        const uint32_t sw = quad_pairs(sd[(2 * j) >> 2], a);
+        const uint32_t bw = quad_pairs(bd[(2 * j) >> 2], a);
+        s = bf16_bits_to_f32((g & 1) ? sw >> 16 : sw & 0xFFFFu);
+        b = bf16_bits_to_f32((g & 1) ? bw >> 16 : bw & 0xFFFFu);
+      } else {
+        s = bf16_bits_to_f32(sd[j] & 0xFFFFu);
+        b = bf16_bits_to_f32(bd[j] & 0xFFFFu);
+      }
+      s *= use;
+      b *= use;
+      y = fmaf(s, acc, y);
+      y = fmaf(fmaf(-128.f, s, b), xsum[off >> 5], y);
+      if constexpr (D < NC) __builtin_amdgcn_sched_barrier(0);  // keep the issue order
+    }
+    // 4. reduce the row's 4 lanes, then the waves in order.
+    y += __shfl_xor(y, 1, 64);
+    y += __shfl_xor(y, 2, 64);
+    if (g == 0) red[wave * 16 + r] = y;
+    lds_barrier();
+    if (tid < 16 && tile * 16 + tid < N) {
+      float v = 0.f;
+      for (int w2 = 0; w2 < W; ++w2) v += red[w2 * 16 + tid];
+      const int64_t p = it.pos0;
+      const int nout = tile * 16 + tid;
+      if (P.ks > 1) {
+        P.part[((int64_t)ks * PT + p) * N + nout] = v;
+      } else {
+        if (!ok) v = __builtin_nanf("");
+        ((uint16_t*)P.y)[p * N + nout] = (uint16_t)f32_to_bf16_bits(v);
+      }
+    }
+  };
+
+  if constexpr (DENSE) {
+    // one pair, no indices: straight-line, no work-item decode
+    Item it;
+    it.pos0 = 0;
+    it.cnt = 1;
+    it.expert = 0;
+    it.expert_ok = true;
+    process(it, 0);
+  } else {
+    const int n_items = P.items ? (int)*P.item_count : P.n_items_fixed;
+    for (int it_i = blockIdx.z; it_i < n_items; it_i += gridDim.z) {
+      const Item it = decode_item(P, it_i);
+      if (it.cnt <= 0) continue;
+      const int64_t xr = item_x_row(P, it, 0);
+      if (xr == -1) continue;  // block-uniform
+      process(it, xr);
+      lds_barrier();  // LDS is reused by the next item
+    }
+  }
+}
+
+template <int GS, int NC, int DEPTH, bool DENSE>
+void launch_xu(const QmvParams& P, dim3 grid, dim3 block, int xu, size_t lds, hipStream_t s) {
+  switch (xu) {
+    case 1: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 1, DEPTH, DENSE>), grid, block, lds, s, P); break;
+    case 2: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 2, DEPTH, DENSE>), grid, block, lds, s, P); break;
+    case 4: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 4, DEPTH, DENSE>), grid, block, lds, s, P); break;
+    default: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 8, DEPTH, DENSE>), grid, block, lds, s, P); break;
+  }
+}
+
+template <int GS, int NC, bool DENSE>
+void launch_depth(const QmvParams& P, dim3 grid, dim3 block, int xu, int depth, size_t lds,
+                  hipStream_t s) {
+  // depth 4 covers "all loads up front" for NC <= 4; NC <= 2 has a single schedule
+  if (NC > 2 && depth == 2) launch_xu<GS, NC, 2, DENSE>(P, grid, block, xu, lds, s);
+  else launch_xu<GS, NC, 4, DENSE>(P, grid, block, xu, lds, s);
+}
+
+template <int GS, int NC>
+hipError_t launch_nc(const QmvParams& P, dim3 grid, int waves, int xu, int depth, size_t lds,
+                     hipStream_t s) {
+  const dim3 block(64 * waves);
+  const bool dense = !P.items && !P.lhs && !P.rhs && P.n_pairs == 1 && P.M == 1;
+  if (dense) launch_depth<GS, NC, true>(P, grid, block, xu, depth, lds, s);
+  else launch_depth<GS, NC, false>(P, grid, block, xu, depth, lds, s);
+  return hipGetLastError();
+}
+
+}  // namespace qmv1_detail
+
+// Launch for one group size; each group size is instantiated in its own translation unit
+// (qmv1_g32.hip, qmv1_g64.hip, qmv1_g128.hip) so the kernel instances compile in parallel.
+template <int GS>
+hipError_t launch_qmv1_gs(const QmvParams& P, dim3 grid, int waves, int nc, int xu, int depth,
+                          size_t lds, hipStream_t s) {
+  using namespace qmv1_detail;
+  switch (nc) {
+    case 1: return launch_nc<GS, 1>(P, grid, waves, xu, depth, lds, s);
+    case 2: return launch_nc<GS, 2>(P, grid, waves, xu, depth, lds, s);
+    case 3: return launch_nc<GS, 3>(P, grid, waves, xu, depth, lds, s);
+    case 4: return launch_nc<GS, 4>(P, grid, waves, xu, depth, lds, s);
+    case 5: return launch_nc<GS, 5>(P, grid, waves, xu, depth, lds, s);
+    case 6: return launch_nc<GS, 6>(P, grid, waves, xu, depth, lds, s);
+    case 7: return launch_nc<GS, 7>(P, grid, waves, xu, depth, lds, s);
+    case 8: return launch_nc<GS, 8>(P, grid, waves, xu, depth, lds, s);
+    case 10: return launch_nc<GS, 10>(P, grid, waves, xu, depth, lds, s);
+    case 12: return launch_nc<GS, 12>(P, grid, waves, xu, depth, lds, s);
+    case 14: return launch_nc<GS, 14>(P, grid, waves, xu, depth, lds, s);
+    default: return launch_nc<GS, 16>(P, grid, waves, xu, depth, lds, s);
+  }
+}
+
+}  // namespace mi
