@@ -416,6 +416,21 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
     hipError_t e = mi::launch_qmm(Q, s);
     return e == hipSuccess ? MI_OK : hip_fail(e, "qmm launch");
   }
+  static const int use_qmvm = env_int("MI_QMM_QMVM", 1);
+  mi::QmvmPlan qp{};
+  if (use_qmvm && x_dtype == MI_DTYPE_BFLOAT16 && M >= 2 && M <= 32 &&
+      mi::qmvm_plan((int)M, (int)N, (int)K, gs, nb, &qp)) {
+    mi::QmvmParams Q{x, w, (const uint16_t*)scales, (const uint16_t*)biases, (uint16_t*)y,
+                     nullptr, (int)M, (int)N, (int)K, gs, qp.kr, qp.wr};
+    if (qp.part_bytes) {
+      void* data = nullptr;
+      rc = workspace(s, qp.part_bytes, &data);
+      if (rc) return rc;
+      Q.part = (float*)data;
+    }
+    hipError_t e = mi::launch_qmvm(Q, qp, s);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "qmvm launch");
+  }
   // Dense = gather with a single pair on expert 0; M rows ride in one x batch.
   return mi_gather_qmm(y, x, w, scales, biases, nullptr, nullptr, 1, 1, 1, M, N, K, 1, transpose,
                        group_size, bits, mode, false, x_dtype, sb_dtype, stream);

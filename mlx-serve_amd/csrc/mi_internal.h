@@ -55,6 +55,24 @@ template <int GS>
 hipError_t launch_qmv1_gs(const QmvParams& P, dim3 grid, int waves, int nc, int xu, int depth,
                           size_t lds, hipStream_t s);
 
+// Few-row dense decode kernel (qmvm.hip): 2 <= M <= 32, 4-bit gs 64, bf16 x and y.
+struct QmvmParams {
+  const void* x;
+  const uint32_t* w;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  uint16_t* y;
+  float* part;  // ks > 1: fp32 partials [ks][M][N]
+  int M, N, K, group_size, kr, wr;
+  uint32_t upr_mr, spr_mr;  // set by launch_qmvm: ceil(2^32 / d) for the staging divisions
+};
+struct QmvmPlan {
+  int wr, ks, kr, waves, nc, xu, depth, tiles, mt, lds, sbf32;
+  size_t part_bytes;
+};
+bool qmvm_plan(int M, int N, int K, int gs, int bits, QmvmPlan* out);
+hipError_t launch_qmvm(const QmvmParams& P, const QmvmPlan& plan, hipStream_t s);
+
 // Decode-width kernel (qmv16.hip): M <= 16 rows per item, 16-row weight tiles.
 int qmv16_mp_for_rows(int rows);
 int qmv16_groups_per_chunk(int bits, int gs);
