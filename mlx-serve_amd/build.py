@@ -16,7 +16,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HOST = os.path.join(HERE, "host")
 ROOT = os.path.dirname(HERE)
 SOURCES = ["csrc/qmv1_g64.hip", "csrc/qmv1_g32.hip", "csrc/qmv1_g128.hip", "csrc/qmv1.hip", "csrc/qmvm.hip", "csrc/qmv.hip", "csrc/qmv16.hip", "csrc/qmm.hip", "csrc/quant.hip", "csrc/moe.hip",
-           "csrc/api.cpp", "host/mi_host.cpp"]
+           "csrc/blas.cpp", "csrc/api.cpp", "host/mi_host.cpp"]
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I", os.path.join(ROOT, "include"), "-I", HOST]
@@ -43,7 +43,8 @@ def build(verbose=True):
     with cf.ThreadPoolExecutor(max_workers=min(os.cpu_count() or 8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs + [
+        "-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stderr)

@@ -403,6 +403,25 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   if (!y || !x || !w || !scales || !biases) return fail(MI_ERR_INVALID, "null tensor pointer");
   if (N > (int64_t)1 << 30 || M > (int64_t)1 << 30) return fail(MI_ERR_INVALID, "N or M too large");
   hipStream_t s = (hipStream_t)stream;
+  // Large M: dequantize once into the workspace and run a dense bf16 GEMM (the reference's
+  // prefillDqGemm shape, src/transformer.zig:20987-21011); below the threshold the fused
+  // dequant-in-register kernel is faster.
+  static const int dq_min = env_int("MI_QMM_DQGEMM_MIN", 1024);
+  if (x_dtype == MI_DTYPE_BFLOAT16 && dq_min > 0 && M >= dq_min && K <= INT32_MAX &&
+      N * K * 2 <= ((int64_t)1 << 34)) {
+    const size_t wbytes = round256((size_t)N * K * 2);
+    void* data = nullptr;
+    rc = workspace(s, wbytes + mi::kDqGemmBlasWs, &data);
+    if (rc) return rc;
+    hipError_t e = mi::launch_dequantize(data, w, (const uint16_t*)scales, (const uint16_t*)biases,
+                                         N, K, gs, nb, 0, 0, s);
+    if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+    const char* err = nullptr;
+    if (mi::dq_gemm((const uint16_t*)x, (const uint16_t*)data, (uint16_t*)y, (int)M, (int)N,
+                    (int)K, (char*)data + wbytes, mi::kDqGemmBlasWs, s, &err) != 0)
+      return fail(MI_ERR_HIP, "hipBLASLt GEMM: %s", err ? err : "error");
+    return MI_OK;
+  }
   if (x_dtype == MI_DTYPE_BFLOAT16 && M > 32 && mi::qmm_supported((int)M, (int)N, (int)K, nb, gs)) {
     mi::QmmParams Q{w, (const uint16_t*)scales, (const uint16_t*)biases, (const uint16_t*)x,
                     (uint16_t*)y, (int)M, (int)N, (int)K, nb, gs, nullptr, 1, 0, 0};

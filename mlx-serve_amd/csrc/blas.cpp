@@ -1,0 +1,104 @@
+// Large-M prefill as dequantize + dense GEMM: the packed weight is expanded once into a
+// bf16 [N, K] workspace and y[M, N] = x[M, K] @ W^T runs as a plain bf16 GEMM (fp32
+// accumulation) on hipBLASLt. This is the shape of the reference's prefillDqGemm
+// (src/transformer.zig:20987-21011), which switches to dequantize + dense GEMM for
+// large M; on MI355X the library GEMM sustains more MFMA throughput at M >= ~1024 than the
+// fused dequant-in-register kernel (qmm.hip), which keeps the smaller M.
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "mi_internal.h"
+
+namespace mi {
+
+namespace {
+
+struct DqGemmPlan {
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  size_t ws = 0;
+  bool ok = false;
+};
+
+std::mutex g_mu;
+std::map<int, hipblasLtHandle_t> g_handles;
+std::map<std::tuple<int, int, int, int>, DqGemmPlan> g_plans;
+
+const char* status_name(hipblasStatus_t st) {
+  switch (st) {
+    case HIPBLAS_STATUS_SUCCESS: return "success";
+    case HIPBLAS_STATUS_NOT_INITIALIZED: return "not initialized";
+    case HIPBLAS_STATUS_ALLOC_FAILED: return "alloc failed";
+    case HIPBLAS_STATUS_INVALID_VALUE: return "invalid value";
+    case HIPBLAS_STATUS_EXECUTION_FAILED: return "execution failed";
+    case HIPBLAS_STATUS_NOT_SUPPORTED: return "not supported";
+    default: return "error";
+  }
+}
+
+}  // namespace
+
+// Column-major view: y^T [N x M] (ld N) = W (col-major K x N, op T) x x^T (col-major K x M).
+int dq_gemm(const uint16_t* x, const uint16_t* wd, uint16_t* y, int M, int N, int K,
+            void* blas_ws, size_t blas_ws_bytes, hipStream_t s, const char** err) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    *err = "hipGetDevice failed";
+    return -1;
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  hipblasLtHandle_t& h = g_handles[dev];
+  if (!h) {
+    const hipblasStatus_t st = hipblasLtCreate(&h);
+    if (st != HIPBLAS_STATUS_SUCCESS) {
+      h = nullptr;
+      *err = status_name(st);
+      return -1;
+    }
+  }
+  DqGemmPlan& p = g_plans[std::make_tuple(dev, M, N, K)];
+  if (!p.ok) {
+    hipblasStatus_t st = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    if (st == HIPBLAS_STATUS_SUCCESS)
+      st = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta));
+    if (st == HIPBLAS_STATUS_SUCCESS)
+      st = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb));
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, N, K);
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, K, M, K);
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_16BF, N, M, N);
+    hipblasLtMatmulPreference_t pref = nullptr;
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatmulPreferenceCreate(&pref);
+    const uint64_t max_ws = blas_ws_bytes;
+    if (st == HIPBLAS_STATUS_SUCCESS)
+      st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                                 &max_ws, sizeof(max_ws));
+    hipblasLtMatmulHeuristicResult_t res[1];
+    int found = 0;
+    if (st == HIPBLAS_STATUS_SUCCESS)
+      st = hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, res, &found);
+    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+    if (st != HIPBLAS_STATUS_SUCCESS || found < 1) {
+      *err = st != HIPBLAS_STATUS_SUCCESS ? status_name(st) : "no hipBLASLt algorithm";
+      g_plans.erase(std::make_tuple(dev, M, N, K));
+      return -1;
+    }
+    p.algo = res[0].algo;
+    p.ws = res[0].workspaceSize;
+    p.ok = true;
+  }
+  const float alpha = 1.f, beta = 0.f;
+  const hipblasStatus_t st = hipblasLtMatmul(h, p.desc, &alpha, wd, p.la, x, p.lb, &beta, y, p.lc, y,
+                                             p.lc, &p.algo, blas_ws, p.ws, s);
+  if (st != HIPBLAS_STATUS_SUCCESS) {
+    *err = status_name(st);
+    return -1;
+  }
+  return 0;
+}
+
+}  // namespace mi

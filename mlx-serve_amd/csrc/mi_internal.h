@@ -118,6 +118,12 @@ size_t qmm_plan(QmmParams& P);
 hipError_t launch_qmm(const QmmParams& P, hipStream_t s);
 bool qmm_supported(int M, int N, int K, int bits, int gs);
 
+// Dequantize + hipBLASLt bf16 GEMM for large M (blas.cpp): y = x @ wd^T with wd the
+// dequantized bf16 [N, K] weight; blas_ws is the library's scratch. 0 or -1 (err set).
+constexpr size_t kDqGemmBlasWs = (size_t)32 << 20;
+int dq_gemm(const uint16_t* x, const uint16_t* wd, uint16_t* y, int M, int N, int K,
+            void* blas_ws, size_t blas_ws_bytes, hipStream_t s, const char** err);
+
 // Quantize / dequantize / generator (quant.hip).
 hipError_t launch_dequantize(void* out, const uint32_t* w, const uint16_t* s, const uint16_t* b,
                              int64_t rows, int64_t K, int gs, int bits, int out_f32, int rounding,
