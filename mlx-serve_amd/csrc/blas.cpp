@@ -77,18 +77,50 @@ int dq_gemm(const uint16_t* x, const uint16_t* wd, uint16_t* y, int M, int N, in
     if (st == HIPBLAS_STATUS_SUCCESS)
       st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
                                                  &max_ws, sizeof(max_ws));
-    hipblasLtMatmulHeuristicResult_t res[1];
+    constexpr int kCand = 8;
+    hipblasLtMatmulHeuristicResult_t res[kCand];
     int found = 0;
     if (st == HIPBLAS_STATUS_SUCCESS)
-      st = hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, res, &found);
+      st = hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref, kCand, res,
+                                           &found);
     if (pref) hipblasLtMatmulPreferenceDestroy(pref);
     if (st != HIPBLAS_STATUS_SUCCESS || found < 1) {
       *err = st != HIPBLAS_STATUS_SUCCESS ? status_name(st) : "no hipBLASLt algorithm";
       g_plans.erase(std::make_tuple(dev, M, N, K));
       return -1;
     }
-    p.algo = res[0].algo;
-    p.ws = res[0].workspaceSize;
+    int pick = 0;
+    // Outside stream capture, time the candidates once on the call's own buffers (each run
+    // writes the same y) and keep the fastest; under capture take the library's first.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (found > 1 && hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
+      hipEvent_t e0 = nullptr, e1 = nullptr;
+      if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
+        const float one = 1.f, zero = 0.f;
+        float best_ms = 1e30f;
+        for (int c = 0; c < found; ++c) {
+          if (res[c].state != HIPBLAS_STATUS_SUCCESS || res[c].workspaceSize > blas_ws_bytes) continue;
+          bool ok = hipblasLtMatmul(h, p.desc, &one, wd, p.la, x, p.lb, &zero, y, p.lc, y, p.lc,
+                                    &res[c].algo, blas_ws, res[c].workspaceSize, s) ==
+                    HIPBLAS_STATUS_SUCCESS;
+          ok = ok && hipEventRecord(e0, s) == hipSuccess;
+          for (int r = 0; ok && r < 3; ++r)
+            ok = hipblasLtMatmul(h, p.desc, &one, wd, p.la, x, p.lb, &zero, y, p.lc, y, p.lc,
+                                 &res[c].algo, blas_ws, res[c].workspaceSize, s) ==
+                 HIPBLAS_STATUS_SUCCESS;
+          ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+          float ms = 0.f;
+          if (ok && hipEventElapsedTime(&ms, e0, e1) == hipSuccess && ms < best_ms) {
+            best_ms = ms;
+            pick = c;
+          }
+        }
+      }
+      if (e0) (void)hipEventDestroy(e0);
+      if (e1) (void)hipEventDestroy(e1);
+    }
+    p.algo = res[pick].algo;
+    p.ws = res[pick].workspaceSize;
     p.ok = true;
   }
   const float alpha = 1.f, beta = 0.f;
