@@ -280,6 +280,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--prefill-only", type=int, default=0, metavar="M",
+                    help="only run the configs[2] prefill shapes at this M (for rocprofv3)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 4 device copies of 256 MiB (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes)")
@@ -301,6 +303,10 @@ def main():
         print(json.dumps({"copy_calibration_bytes_each_way": a.numel() * 2, "copies": 4}))
         return
     import mi_qmm as mi
+    if args.prefill_only:
+        print(json.dumps(prefill(torch, mi, dev, (args.prefill_only,), steps=args.steps,
+                                 warmup=args.warmup)))
+        return
     bits, gs = 4, 64
     layers = build_mlp_layers(torch, mi, args.layers, bits, gs, dev)
     head = decode_mlp(torch, mi, layers, 1, bits, gs, dev, args.steps, args.warmup)
