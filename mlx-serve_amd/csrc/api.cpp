@@ -200,7 +200,8 @@ struct GatherJob {
   mi::QmvParams P{};
   QmvPlan plan{};
   mi::Qmv1Plan plan1{};
-  bool empty = false, narrow = false, use_items = false, one_row = false;
+  mi::QmvmPlan planm{};
+  bool empty = false, narrow = false, use_items = false, one_row = false, multi_row = false;
   int64_t max_items = 0;
   size_t items_bytes = 0, part_bytes = 0;
   size_t items_region() const { return ((items_bytes + 255) / 256) * 256; }
@@ -303,9 +304,15 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
     P.row_blocks = J.plan1.tiles;
     J.plan.cfg.grid_z = (int)(n_items < 65535 ? n_items : 65535);
   } else {
-    J.plan = J.narrow ? qmv16_plan(P.N, P.K, gs, nb, J.use_items ? P.rpi : rows, n_items, P.x_f32)
-                      : qmv_plan(P.N, P.K, gs, nb, J.use_items ? P.rpi : rows, n_items, P.x_f32);
-    P.ks = J.plan.ks;
+    // Items of 2..32 rows: the MFMA few-row kernel when it supports the layout.
+    static const int use_qmvm = env_int("MI_QMM_QMVM_GATHER", 1);
+    const int item_rows = J.use_items ? P.rpi : rows;
+    J.multi_row = use_qmvm && !P.x_f32 && item_rows >= 2 &&
+                  x_batch * M * K * 2 < ((int64_t)1 << 32) &&
+                  mi::qmvm_plan(item_rows, P.N, P.K, gs, nb, n_items, &J.planm);
+    J.plan = J.narrow ? qmv16_plan(P.N, P.K, gs, nb, item_rows, n_items, P.x_f32)
+                      : qmv_plan(P.N, P.K, gs, nb, item_rows, n_items, P.x_f32);
+    P.ks = J.multi_row ? J.planm.ks : J.plan.ks;
     P.gps = J.plan.gps;
     P.row_blocks = J.plan.row_blocks;
   }
@@ -329,9 +336,10 @@ int gather_launch(GatherJob& J, void* ws, hipStream_t s) {
       P.item_count = count;
     }
   }
-  hipError_t e = J.one_row ? mi::launch_qmv1(P, J.plan1, J.plan.cfg.grid_z, s)
-                 : J.narrow  ? mi::launch_qmv16(P, J.plan.cfg, s)
-                             : mi::launch_qmv(P, J.plan.cfg, s);
+  hipError_t e = J.one_row     ? mi::launch_qmv1(P, J.plan1, J.plan.cfg.grid_z, s)
+                 : J.multi_row ? mi::launch_qmvm_gather(P, J.planm, J.plan.cfg.grid_z, s)
+                 : J.narrow    ? mi::launch_qmv16(P, J.plan.cfg, s)
+                               : mi::launch_qmv(P, J.plan.cfg, s);
   return e == hipSuccess ? MI_OK : hip_fail(e, "qmv launch");
 }
 
@@ -438,7 +446,7 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   static const int use_qmvm = env_int("MI_QMM_QMVM", 1);
   mi::QmvmPlan qp{};
   if (use_qmvm && x_dtype == MI_DTYPE_BFLOAT16 && M >= 2 && M <= 32 &&
-      mi::qmvm_plan((int)M, (int)N, (int)K, gs, nb, &qp)) {
+      mi::qmvm_plan((int)M, (int)N, (int)K, gs, nb, 1, &qp)) {
     mi::QmvmParams Q{x, w, (const uint16_t*)scales, (const uint16_t*)biases, (uint16_t*)y,
                      nullptr, (int)M, (int)N, (int)K, gs, qp.kr, qp.wr};
     if (qp.part_bytes) {

@@ -67,11 +67,13 @@ struct QmvmParams {
   uint32_t upr_mr, spr_mr;  // set by launch_qmvm: ceil(2^32 / d) for the staging divisions
 };
 struct QmvmPlan {
-  int wr, ks, kr, waves, nc, xu, depth, tiles, mt, lds, sbf32;
+  int wr, ks, kr, waves, nc, xu, depth, tiles, mt, lds, sbf32, rows;
   size_t part_bytes;
 };
-bool qmvm_plan(int M, int N, int K, int gs, int bits, QmvmPlan* out);
+// rows = activation rows per call (dense) or per work item (gathers, n_items items).
+bool qmvm_plan(int rows, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan* out);
 hipError_t launch_qmvm(const QmvmParams& P, const QmvmPlan& plan, hipStream_t s);
+hipError_t launch_qmvm_gather(const QmvParams& G, const QmvmPlan& plan, int grid_z, hipStream_t s);
 
 // Decode-width kernel (qmv16.hip): M <= 16 rows per item, 16-row weight tiles.
 int qmv16_mp_for_rows(int rows);

@@ -1,0 +1,413 @@
+// Few-row decode GEMM, 4-bit affine gs 64, bf16 activations, on the 16x16x32 bf16 MFMA:
+// dense quantized_matmul (2 <= M <= 32) and gather_qmm work items of 2..32 rows (sorted
+// expert runs). The weights stream straight into registers the way the one-row kernel
+// streams them (no LDS copy of the weights).
+//
+// Block = WR weight tiles of 16 rows x one K range (x one work item for gathers); its W
+// waves are WR x WK: wave (rt, kp) owns tile rt and the kp-th run of NC 128-value chunks
+// of the range. The block stages the range's activations (its rows, nibble-pair order)
+// and the tiles' scale/bias pairs into LDS once; every wave reads them from there. A
+// gather block first resolves its item's activation rows (sorted runs keep only the rows
+// whose pair maps to the item's expert) into a small LDS table.
+//
+// Loads: lane l of a wave reads 16 B of weight row l%16 at byte 16*(l/16) of each
+// 64-byte chunk (one b128 per chunk; 16 rows x 64 contiguous bytes per instruction),
+// DEPTH chunks ahead. After two permlane swaps (a 4x4 dword transpose across the four
+// 16-lane rows) lane l holds, in register t, dword l/16 of the 32-value run t of its row,
+// so each MFMA step covers one run of 32 consecutive values, inside one group.
+//
+// MFMA (16x16x32 bf16) layout: lane l holds 8 k values of A row l%16 / B column l%16 for
+// k block l/16; C lane l register r is row 4(l/16)+r, column l%16. A = weights as bf16
+// 0x43qq (= 128+q exactly, v_perm against 0x43 bytes), k order [0,2,4,6,1,3,5,7] per 8;
+// B = activations staged in that same order; C = sum x*(128+q) for one group, to which
+// the group's affine terms are applied in fp32: s*C + (b - 128 s)*X, X = sum of x over
+// the group, from a second MFMA of the same B against an all-ones A. Columns are
+// activation rows (16 per MFMA; more than 16 rows run a second MFMA on rows 16..31).
+//
+// The waves' partial sums of a tile are added in wave order through LDS; K ranges beyond
+// one (activations too large for LDS) write fp32 partials that a second kernel sums in
+// range order. Every sum has a fixed order: results are deterministic.
+#pragma once
+#include "qmv_common.h"
+
+#include <cstdint>
+
+namespace mi {
+namespace qmvm_detail {
+
+using qmv_detail::decode_item;
+using qmv_detail::item_x_row;
+using qmv_detail::Item;
+using qmv_detail::lds_barrier;
+
+typedef __bf16 bf16x8m __attribute__((ext_vector_type(8)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kChunkVals = 128;
+constexpr int kBufFlags = 0x00020000;  // raw (untyped) dword buffer access on this target
+constexpr uint32_t kOOB = 0x7FFFFFF0u;  // buffer offset past any resource: the load returns 0
+constexpr int kMaxRows = 32;
+
+MI_DEV f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8m, a),
+                                                  __builtin_bit_cast(bf16x8m, b), c, 0, 0, 0);
+}
+
+// 8 nibbles -> bf16 pairs (128+q0, 128+q2), (q4, q6), (q1, q3), (q5, q7).
+MI_DEV u32x4_t unpack8(uint32_t w) {
+  constexpr uint32_t c43 = 0x43434343u;
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  return u32x4_t{perm_b32(c43, lo, 0x04010400u), perm_b32(c43, lo, 0x04030402u),
+                 perm_b32(c43, hi, 0x04010400u), perm_b32(c43, hi, 0x04030402u)};
+}
+
+// 4x4 transpose of dwords across the four 16-lane rows of the wave: on return, register
+// t of row q holds what register q of row t held.
+MI_DEV u32x4_t xpose4(u32x4_t v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  return u32x4_t{c[0], c[1], d[0], d[1]};
+}
+
+MI_DEV float lo_bf16(uint32_t v) { return __uint_as_float(v << 16); }
+MI_DEV float hi_bf16(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
+
+// LDS plan of one block, shared by the kernel and the host.
+struct QmvmLds {
+  int xstride;  // bytes per staged activation row
+  int xbytes, sbbytes, redbytes;
+  __host__ __device__ int total() const {
+    const int a = xbytes + sbbytes;
+    return a > redbytes ? a : redbytes;
+  }
+};
+
+__host__ __device__ inline QmvmLds qmvm_lds(int M, int nvals, int gs, int rows, int waves, int mt,
+                                            bool sbf32) {
+  QmvmLds L;
+  L.xstride = nvals * 2 + 16;  // +16 B: the 16 rows of a B read start in different banks
+  L.xbytes = M * L.xstride;
+  // per group and row: fp32 (s, b - 128 s), or the bf16 pair (s, b) when LDS is tight
+  L.sbbytes = (nvals / gs) * rows * (sbf32 ? 8 : 4);
+  L.redbytes = waves * 16 * mt * 4;
+  return L;
+}
+
+// G is read only by gathers (work items, index arrays, expert bank); dense calls pass
+// their shapes in P.
+template <int GS, int NC, int XU, int DEPTH, int MT, bool SBF32, bool GATHER>
+__global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) {
+  constexpr int SPG = GS / 32;  // 32-value MFMA steps per group
+  constexpr int D = DEPTH < NC ? DEPTH : NC;
+  constexpr int GPC = kChunkVals / GS;  // groups per chunk
+  constexpr int SBW = SBF32 ? 2 : 1;    // LDS words per (group, row)
+  constexpr int SU = 4;                 // scale/bias loads per thread
+  constexpr bool PAIRS = GS <= 64;      // scale/bias as dwords (two groups) or halves
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  __shared__ int64_t rowtab[kMaxRows];  // gathers: element offset of each item row's x
+  const int tid = threadIdx.x, BD = blockDim.x, W = BD >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int WR = P.wr;
+  const int rt = wave % WR, kp = wave / WR;
+  const int i = lane & 15, q = lane >> 4;
+  const int N = P.N, K = P.K, G = K / GS;
+  const int kb0 = blockIdx.y * P.kr;
+  const int nvals = min(K - kb0, P.kr);
+  const int gr = nvals / GS, g0 = kb0 / GS;
+  const int rows = 16 * WR;
+  const int row0 = blockIdx.x * rows;
+  const int upr = nvals / 8;  // staging units per activation row
+  const int spr = PAIRS ? gr / 2 : gr;  // scale/bias loads per row
+  const int c0 = kp * NC;     // first chunk of this wave within the range
+  const int64_t PT = GATHER ? Gp.n_pairs * Gp.M : 0;
+  const int n_items = GATHER ? (Gp.items ? (int)*Gp.item_count : Gp.n_items_fixed) : 1;
+
+  for (int it_i = GATHER ? (int)blockIdx.z : 0; it_i < n_items;
+       it_i += GATHER ? (int)gridDim.z : 1) {
+    int M = P.M;
+    uint32_t e = 0;
+    bool eok = true;
+    int64_t pos0 = 0;
+    if constexpr (GATHER) {
+      const Item it = decode_item(Gp, it_i);
+      if (it.cnt <= 0) continue;  // block-uniform
+      M = min(it.cnt, MT);
+      e = __builtin_amdgcn_readfirstlane(it.expert_ok ? it.expert : 0u);
+      eok = it.expert_ok;
+      pos0 = it.pos0;
+      if (wave == 0 && lane < M) rowtab[lane] = item_x_row(Gp, it, lane);  // -1 skip, -2 NaN
+    }
+    const QmvmLds L = qmvm_lds(M, nvals, GS, rows, W, MT, SBF32);
+    unsigned char* xs = smem;
+    float* sb = reinterpret_cast<float*>(smem + L.xbytes);
+    float* red = reinterpret_cast<float*>(smem);  // reused after the dot products
+
+    const size_t mat = (size_t)e * (uint32_t)N;
+    const uint32_t xbytes_all =
+        GATHER ? (uint32_t)(Gp.x_batch * Gp.M * (int64_t)K * 2) : (uint32_t)(M * K * 2);
+    const __amdgpu_buffer_rsrc_t xres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)P.x, (short)0, xbytes_all, kBufFlags);
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.w + mat * (uint32_t)(K / 8)), (short)0, N * (K / 2), kBufFlags);
+    const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.scales + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
+    const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.biases + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
+
+    // 1. loads. Dense: activations, scale/bias, then the first D chunks (nothing waits
+    //    before all are issued). Gather: the chunks and scale/bias first, then (after the
+    //    row table is visible) the activations.
+    u32x4_t xv[XU];
+    auto load_x = [&]() {
+#pragma unroll
+      for (int t = 0; t < XU; ++t) {
+        const int u = tid + t * BD;
+        const int m = (int)__umulhi((uint32_t)u, P.upr_mr), k8 = u - m * upr;
+        uint32_t off = kOOB;
+        if constexpr (GATHER) {
+          const int64_t ro = m < M ? rowtab[m] : -1;
+          if (ro >= 0) off = (uint32_t)(ro + kb0 + 8 * k8) * 2;
+        } else {
+          if (m < M) off = (uint32_t)(m * K + kb0 + 8 * k8) * 2;
+        }
+        xv[t] = __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0);
+      }
+    };
+    if constexpr (!GATHER) load_x();
+    uint32_t sv[SU], bv[SU];
+#pragma unroll
+    for (int t = 0; t < SU; ++t) {
+      const int v = tid + t * BD;
+      const int rr = spr == 1 ? v : (int)__umulhi((uint32_t)v, P.spr_mr), gp = v - rr * spr;
+      const bool ok = rr < rows && row0 + rr < N;
+      if constexpr (PAIRS) {
+        const uint32_t off = ok ? (uint32_t)((row0 + rr) * G + g0 + 2 * gp) * 2 : kOOB;
+        sv[t] = __builtin_amdgcn_raw_buffer_load_b32(sres, off, 0, 0);
+        bv[t] = __builtin_amdgcn_raw_buffer_load_b32(bres, off, 0, 0);
+      } else {
+        const uint32_t off = ok ? (uint32_t)((row0 + rr) * G + g0 + gp) * 2 : kOOB;
+        sv[t] = __builtin_amdgcn_raw_buffer_load_b16(sres, off, 0, 0);
+        bv[t] = __builtin_amdgcn_raw_buffer_load_b16(bres, off, 0, 0);
+      }
+    }
+    const int wrow = min(row0 + rt * 16 + i, N - 1);
+    const uint32_t wo = (uint32_t)wrow * (uint32_t)(K / 2) +
+                        (uint32_t)(kb0 + c0 * kChunkVals) / 2 + 16 * q;
+    u32x4_t wv[NC];
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+      wv[j] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * j, 0, 0);
+    if constexpr (GATHER) {
+      lds_barrier();  // the row table
+      load_x();
+    }
+
+    // 2. stage activations (pair order) and scale/bias pairs.
+#pragma unroll
+    for (int t = 0; t < XU; ++t) {
+      const int u = tid + t * BD;
+      const int m = (int)__umulhi((uint32_t)u, P.upr_mr), k8 = u - m * upr;
+      const u32x4_t X = xv[t];
+      if (m < M) {
+        u32x4_t p;
+        p.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
+        p.y = perm_b32(X.w, X.z, 0x05040100u);  // (x4, x6)
+        p.z = perm_b32(X.y, X.x, 0x07060302u);  // (x1, x3)
+        p.w = perm_b32(X.w, X.z, 0x07060302u);  // (x5, x7)
+        *reinterpret_cast<u32x4_t*>(xs + m * L.xstride + k8 * 16) = p;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < SU; ++t) {
+      const int v = tid + t * BD;
+      const int rr = spr == 1 ? v : (int)__umulhi((uint32_t)v, P.spr_mr), gp = v - rr * spr;
+      if (rr < rows) {
+        if constexpr (!SBF32) {
+          uint32_t* sbu = reinterpret_cast<uint32_t*>(sb);
+          if constexpr (PAIRS) {
+            sbu[(2 * gp) * rows + rr] = perm_b32(bv[t], sv[t], 0x05040100u);
+            sbu[(2 * gp + 1) * rows + rr] = perm_b32(bv[t], sv[t], 0x07060302u);
+          } else {
+            sbu[gp * rows + rr] = (sv[t] & 0xFFFFu) | (bv[t] << 16);
+          }
+        } else if constexpr (PAIRS) {
+          const float s0 = lo_bf16(sv[t]), s1 = hi_bf16(sv[t]);
+          *reinterpret_cast<f32x2_t*>(sb + 2 * ((2 * gp) * rows + rr)) =
+              f32x2_t{s0, fmaf(-128.f, s0, lo_bf16(bv[t]))};
+          *reinterpret_cast<f32x2_t*>(sb + 2 * ((2 * gp + 1) * rows + rr)) =
+              f32x2_t{s1, fmaf(-128.f, s1, hi_bf16(bv[t]))};
+        } else {
+          const float s0 = lo_bf16(sv[t]);
+          *reinterpret_cast<f32x2_t*>(sb + 2 * (gp * rows + rr)) =
+              f32x2_t{s0, fmaf(-128.f, s0, lo_bf16(bv[t]))};
+        }
+      }
+    }
+    lds_barrier();
+
+    // 3. MFMA over the wave's chunks as they land.
+    const int jj = min(i, M - 1);
+    const int jj2 = min(16 + i, M - 1);
+    const unsigned char* xrow = xs + jj * L.xstride + 16 * q;
+    const unsigned char* xrow2 = xs + jj2 * L.xstride + 16 * q;
+    // per-group pointer, stepped by one group at a time (no multiplies in the loop)
+    const float* sbp = sb + SBW * ((c0 * GPC) * rows + rt * 16 + 4 * q);
+    // A operand of ones (bf16 1.0 = 0x3F80): ones x B puts each column's group sum X in
+    // every row of C, i.e. in the accumulator layout of the outputs
+    const u32x4_t ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      if constexpr (D < NC) {
+        if (j + D < NC)
+          wv[j + D] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * (j + D), 0, 0);
+      }
+      const u32x4_t tw = xpose4(wv[j]);
+      const int kc = (c0 + j) * kChunkVals;  // chunk start within the range
+      f32x4_t c = zero, c2 = zero, cx = zero, cx2 = zero;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t d = t == 0 ? tw.x : t == 1 ? tw.y : t == 2 ? tw.z : tw.w;
+        const u32x4_t a = unpack8(d);
+        const int kb = (kc + 32 * t) * 2;  // byte offset of run t in a staged row (+16q)
+        const u32x4_t b = *reinterpret_cast<const u32x4_t*>(xrow + kb);
+        c = mfma16(a, b, t % SPG == 0 ? zero : c);
+        cx = mfma16(ones, b, t % SPG == 0 ? zero : cx);
+        if constexpr (MT == 32) {
+          const u32x4_t b2 = *reinterpret_cast<const u32x4_t*>(xrow2 + kb);
+          c2 = mfma16(a, b2, t % SPG == 0 ? zero : c2);
+          cx2 = mfma16(ones, b2, t % SPG == 0 ? zero : cx2);
+        }
+        if (t % SPG == SPG - 1) {
+          f32x4_t sb01, sb23;  // (s, b - 128 s) of rows 4q, 4q+1 and 4q+2, 4q+3
+          if constexpr (SBF32) {
+            sb01 = *reinterpret_cast<const f32x4_t*>(sbp);
+            sb23 = *reinterpret_cast<const f32x4_t*>(sbp + 4);
+          } else {
+            const u32x4_t ev = *reinterpret_cast<const u32x4_t*>(sbp);
+            sb01.x = lo_bf16(ev.x);
+            sb01.y = fmaf(-128.f, sb01.x, hi_bf16(ev.x));
+            sb01.z = lo_bf16(ev.y);
+            sb01.w = fmaf(-128.f, sb01.z, hi_bf16(ev.y));
+            sb23.x = lo_bf16(ev.z);
+            sb23.y = fmaf(-128.f, sb23.x, hi_bf16(ev.z));
+            sb23.z = lo_bf16(ev.w);
+            sb23.w = fmaf(-128.f, sb23.z, hi_bf16(ev.w));
+          }
+          sbp += SBW * rows;
+          const float X = cx[0];
+          acc[0] = fmaf(sb01.x, c[0], fmaf(sb01.y, X, acc[0]));
+          acc[1] = fmaf(sb01.z, c[1], fmaf(sb01.w, X, acc[1]));
+          acc[2] = fmaf(sb23.x, c[2], fmaf(sb23.y, X, acc[2]));
+          acc[3] = fmaf(sb23.z, c[3], fmaf(sb23.w, X, acc[3]));
+          if constexpr (MT == 32) {
+            const float X2 = cx2[0];
+            acc2[0] = fmaf(sb01.x, c2[0], fmaf(sb01.y, X2, acc2[0]));
+            acc2[1] = fmaf(sb01.z, c2[1], fmaf(sb01.w, X2, acc2[1]));
+            acc2[2] = fmaf(sb23.x, c2[2], fmaf(sb23.y, X2, acc2[2]));
+            acc2[3] = fmaf(sb23.z, c2[3], fmaf(sb23.w, X2, acc2[3]));
+          }
+        }
+      }
+      if constexpr (D < NC) __builtin_amdgcn_sched_barrier(0);  // keep the issue order
+    }
+
+    // 4. sum the WK waves of each tile in wave order, write y (or the range's partial).
+    lds_barrier();  // LDS reads of step 3 are done: reuse it
+    // red[kp][rt][col][row16] : lane holds rows 4q..4q+3 of column i
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      red[((kp * WR + rt) * MT + i) * 16 + 4 * q + r] = acc[r];
+      if constexpr (MT == 32) red[((kp * WR + rt) * MT + 16 + i) * 16 + 4 * q + r] = acc2[r];
+    }
+    lds_barrier();
+    const int WK = W / WR;
+    const int nout = rows * M;
+    for (int o = tid; o < nout; o += BD) {
+      const int m = o / rows, rr = o - m * rows;  // consecutive threads: consecutive rows
+      const int t2 = rr >> 4, r16 = rr & 15;
+      const int n = row0 + rr;
+      if (n >= N) continue;
+      float v = 0.f;
+      for (int k2 = 0; k2 < WK; ++k2) v += red[((k2 * WR + t2) * MT + m) * 16 + r16];
+      int64_t pos = m;
+      if constexpr (GATHER) {
+        const int64_t ro = rowtab[m];
+        if (ro == -1) continue;  // this row belongs to another item
+        if (ro == -2 || !eok) v = __builtin_nanf("");
+        pos = pos0 + m;
+      }
+      if (gridDim.y > 1) {
+        const int64_t npos = GATHER ? PT : M;
+        P.part[((int64_t)blockIdx.y * npos + pos) * N + n] = v;
+      } else {
+        P.y[pos * N + n] = (uint16_t)f32_to_bf16_bits(v);
+      }
+    }
+    if constexpr (GATHER) lds_barrier();  // LDS and the row table are reused by the next item
+  }
+}
+
+// Launches one instance family; explicitly instantiated per (MT, SBF32, GATHER) in
+// qmvm.hip (dense) and qmvm_gather.hip (gathers) so the instances compile in parallel.
+template <int MT, bool SBF32, bool GATHER>
+void launch_family(const QmvmParams& P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
+                   hipStream_t s);
+
+template <int NC, int MT, bool SBF32, bool GATHER>
+void launch_xd(const QmvmParams& P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
+               hipStream_t s) {
+  const dim3 block(64 * pl.waves);
+  const size_t lds = (size_t)pl.lds;
+#define MI_QMVM_LAUNCH(XU, DP)                                                              \
+  do {                                                                                      \
+    auto k = qmvm_kernel<64, NC, XU, DP, MT, SBF32, GATHER>;                                \
+    static bool attr = false; /* LDS above 64 KiB needs the attribute, once per kernel */ \
+    if (!attr) {                                                                            \
+      (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                160 * 1024 - 512);                                          \
+      attr = true;                                                                          \
+    }                                                                                       \
+    hipLaunchKernelGGL(k, grid, block, lds, s, P, G);                                       \
+  } while (0)
+  bool d2 = false;
+  if constexpr (NC > 2) d2 = pl.depth == 2;
+  if (d2) {
+    switch (pl.xu) {
+      case 1: MI_QMVM_LAUNCH(1, 2); break;
+      case 2: MI_QMVM_LAUNCH(2, 2); break;
+      case 4: MI_QMVM_LAUNCH(4, 2); break;
+      default: MI_QMVM_LAUNCH(8, 2); break;
+    }
+  } else {
+    switch (pl.xu) {
+      case 1: MI_QMVM_LAUNCH(1, 4); break;
+      case 2: MI_QMVM_LAUNCH(2, 4); break;
+      case 4: MI_QMVM_LAUNCH(4, 4); break;
+      default: MI_QMVM_LAUNCH(8, 4); break;
+    }
+  }
+#undef MI_QMVM_LAUNCH
+}
+
+template <int MT, bool SBF32, bool GATHER>
+void launch_family(const QmvmParams& P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
+                   hipStream_t s) {
+  switch (pl.nc) {
+    case 1: launch_xd<1, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 2: launch_xd<2, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 3: launch_xd<3, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 4: launch_xd<4, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 5: launch_xd<5, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 6: launch_xd<6, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 7: launch_xd<7, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    default: launch_xd<8, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+  }
+}
+
+}  // namespace qmvm_detail
+}  // namespace mi

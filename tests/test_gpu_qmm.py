@@ -132,10 +132,11 @@ def test_gather_decode_broadcast(dev):
                                           (1, 1024, 8, 40, 3), (2, 2048, 8, 40, 3),
                                           (1, 512, 64, 20, 2), (1, 512, 40, 30, 2),
                                           (1, 1024, 32, 40, 3), (2, 512, 16, 24, 2),
-                                          (1, 512, 4, 64, 4)])
+                                          (1, 512, 4, 64, 4), (1, 8192, 4, 64, 4)])
 def test_gather_sorted_matches_unsorted(dev, M, K, E, T, topk):
     """Sorted (grouped) path and unsorted path both match truth; the shapes cover work
-    items of 1, 2, 4 rows (16-row-tile kernel) and 8..32 rows (32-row-tile kernel)."""
+    items of 1 row (one-row kernel), 2..32 rows (few-row MFMA kernel, K split across
+    blocks for K=8192) and the older 16/32-row-tile kernels."""
     _print_case(t="gather_sorted", M=M, K=K, E=E, T=T, topk=topk)
     N = 64
     wq, s, b = weights(E, N, K, 4, 64, 77)
@@ -174,6 +175,27 @@ def test_gather_out_of_range_is_nan(dev):
     assert np.isnan(yf[1]).all() and np.isnan(yf[2]).all()
     truth = O.gather_qmm_f64(x, wq, s, b, lhs[:1], rhs[:1], 1)
     assert max_err_ratio(yf[:1], truth) <= BF16_TOL
+
+
+def test_gather_sorted_multirow_nan_rows(dev):
+    """Sorted runs of several rows: a run on an unknown expert and a row whose lhs index
+    is out of range come out NaN; the other rows of the same runs are exact."""
+    _print_case(t="gather_sorted_nan")
+    E, N, K = 4, 64, 256
+    wq, s, b = weights(E, N, K, 4, 64, 92)
+    x = O.make_x_bf16(6, K, 93).reshape(6, 1, K)
+    rhs = np.array([0, 0, 0, 1, 1, 9, 9], np.uint32)
+    lhs = np.array([0, 1, 7, 2, 3, 4, 5], np.uint32)
+    y = mi_qmm.gather_qmm(to_dev_bf16(x, dev), to_dev_u32(wq, dev), to_dev_bf16(s, dev),
+                          to_dev_bf16(b, dev), lhs_indices=to_dev_u32(lhs, dev),
+                          rhs_indices=to_dev_u32(rhs, dev), group_size=64, bits=4,
+                          sorted_indices=True)
+    yf = to_f64(y)
+    for r in (2, 5, 6):
+        assert np.isnan(yf[r]).all()
+    ok = np.array([0, 1, 3, 4])
+    truth = O.gather_qmm_f64(x, wq, s, b, lhs[ok], rhs[ok], len(ok))
+    assert max_err_ratio(yf[ok], truth) <= BF16_TOL
 
 
 def test_deterministic(dev):
