@@ -46,10 +46,12 @@ __global__ void dequant_kernel(void* __restrict__ out, const uint32_t* __restric
   }
 }
 
-// 4-bit to bf16 with one rounding, gs in {32, 64, 128}: a thread expands 4 packed words
-// (32 values, all in one quantization group) into 64 bytes. Unit i of the flattened
-// [rows, K/32] array belongs to group i >> log2(gs/32) of the flattened [rows, K/gs]
-// scales, so no index division is needed. v_cvt_pk_bf16_f32 rounds to nearest even.
+// 4-bit to bf16 with one rounding, gs in {32, 64, 128}. A block expands 1024 consecutive
+// packed words: per step a wave reads 64 consecutive words (256 B) and writes their 512
+// values as 1 KiB of consecutive bf16, so loads and stores are both contiguous per
+// instruction. Word i of the flattened [rows, K/8] array belongs to group i >> log2(gs/8)
+// of the flattened [rows, K/gs] scales (gs divides K), so no index division is needed.
+// v_cvt_pk_bf16_f32 rounds to nearest even.
 typedef __bf16 bf16x2q __attribute__((ext_vector_type(2)));
 typedef float f32x2q __attribute__((ext_vector_type(2)));
 MI_DEV uint32_t pk_bf16(float lo, float hi) {
@@ -60,25 +62,31 @@ template <int k>
 MI_DEV float ubyte_f(uint32_t w) { return (float)((w >> (8 * k)) & 0xFFu); }
 
 __global__ void __launch_bounds__(256) dequant4_bf16_kernel(u32x4_t* __restrict__ out,
-                                                           const u32x4_t* __restrict__ w,
+                                                           const uint32_t* __restrict__ w,
                                                            const uint16_t* __restrict__ s,
                                                            const uint16_t* __restrict__ b,
-                                                           int64_t n_units, int ushift) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_units;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const u32x4_t q = w[i];
-    const int64_t gi = i >> ushift;
-    const float sc = bf16_bits_to_f32(s[gi]), bi = bf16_bits_to_f32(b[gi]);
+                                                           int64_t n_words, int wshift) {
+  for (int64_t base = blockIdx.x * (int64_t)1024; base < n_words;
+       base += (int64_t)gridDim.x * 1024) {
+    uint32_t wd[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t wd = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
-      const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+      const int64_t i = base + j * 256 + threadIdx.x;
+      wd[j] = i < n_words ? w[i] : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t i = base + j * 256 + threadIdx.x;
+      if (i >= n_words) break;
+      const int64_t gi = i >> wshift;
+      const float sc = bf16_bits_to_f32(s[gi]), bi = bf16_bits_to_f32(b[gi]);
+      const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = (wd[j] >> 4) & 0x0F0F0F0Fu;
       u32x4_t o;
       o.x = pk_bf16(fmaf(sc, ubyte_f<0>(lo), bi), fmaf(sc, ubyte_f<0>(hi), bi));
       o.y = pk_bf16(fmaf(sc, ubyte_f<1>(lo), bi), fmaf(sc, ubyte_f<1>(hi), bi));
       o.z = pk_bf16(fmaf(sc, ubyte_f<2>(lo), bi), fmaf(sc, ubyte_f<2>(hi), bi));
       o.w = pk_bf16(fmaf(sc, ubyte_f<3>(lo), bi), fmaf(sc, ubyte_f<3>(hi), bi));
-      out[4 * i + j] = o;
+      out[i] = o;
     }
   }
 }
@@ -262,13 +270,12 @@ hipError_t launch_dequantize(void* out, const uint32_t* w, const uint16_t* s, co
   if (out_f32) rounding = 0;  // the fp32 result is exact; rounding applies to bf16 only
   const int bs = 256;
   if (bits == 4 && !out_f32 && rounding == 0 && (gs == 32 || gs == 64 || gs == 128) &&
-      ((uintptr_t)out | (uintptr_t)w) % 16 == 0) {
-    const int64_t n_units = n_words / 4;  // K % 32 == 0, so rows * K / 32 units
-    const int ushift = gs == 32 ? 0 : gs == 64 ? 1 : 2;
-    int64_t g = (n_units + bs - 1) / bs;
+      (uintptr_t)out % 16 == 0) {
+    const int wshift = gs == 32 ? 2 : gs == 64 ? 3 : 4;  // log2(gs / 8)
+    int64_t g = (n_words + 1023) / 1024;
     if (g > (int64_t)1 << 20) g = (int64_t)1 << 20;
     hipLaunchKernelGGL(dequant4_bf16_kernel, dim3((unsigned)g), dim3(bs), 0, st, (u32x4_t*)out,
-                       (const u32x4_t*)w, s, b, n_units, ushift);
+                       w, s, b, n_words, wshift);
     return hipGetLastError();
   }
   if (bits == 4)
