@@ -426,7 +426,7 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
     if (e != hipSuccess) return hip_fail(e, "dequantize launch");
     const char* err = nullptr;
     if (mi::dq_gemm((const uint16_t*)x, (const uint16_t*)data, (uint16_t*)y, (int)M, (int)N,
-                    (int)K, (char*)data + wbytes, mi::kDqGemmBlasWs, s, &err) != 0)
+                    (int)K, (int)N, (char*)data + wbytes, mi::kDqGemmBlasWs, s, &err) != 0)
       return fail(MI_ERR_HIP, "hipBLASLt GEMM: %s", err ? err : "error");
     return MI_OK;
   }

@@ -26,7 +26,7 @@ struct DqGemmPlan {
 
 std::mutex g_mu;
 std::map<int, hipblasLtHandle_t> g_handles;
-std::map<std::tuple<int, int, int, int>, DqGemmPlan> g_plans;
+std::map<std::tuple<int, int, int, int, int>, DqGemmPlan> g_plans;
 
 const char* status_name(hipblasStatus_t st) {
   switch (st) {
@@ -42,8 +42,8 @@ const char* status_name(hipblasStatus_t st) {
 
 }  // namespace
 
-// Column-major view: y^T [N x M] (ld N) = W (col-major K x N, op T) x x^T (col-major K x M).
-int dq_gemm(const uint16_t* x, const uint16_t* wd, uint16_t* y, int M, int N, int K,
+// Column-major view: y^T [N x M] (ld ldy) = W (col-major K x N, op T) x x^T (col-major K x M).
+int dq_gemm(const uint16_t* x, const uint16_t* wd, uint16_t* y, int M, int N, int K, int ldy,
             void* blas_ws, size_t blas_ws_bytes, hipStream_t s, const char** err) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
@@ -60,7 +60,8 @@ int dq_gemm(const uint16_t* x, const uint16_t* wd, uint16_t* y, int M, int N, in
       return -1;
     }
   }
-  DqGemmPlan& p = g_plans[std::make_tuple(dev, M, N, K)];
+  const auto key = std::make_tuple(dev, M, N, K, ldy);
+  DqGemmPlan& p = g_plans[key];
   if (!p.ok) {
     hipblasStatus_t st = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
     const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
@@ -70,7 +71,7 @@ int dq_gemm(const uint16_t* x, const uint16_t* wd, uint16_t* y, int M, int N, in
       st = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb));
     if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, N, K);
     if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, K, M, K);
-    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_16BF, N, M, N);
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_16BF, N, M, ldy);
     hipblasLtMatmulPreference_t pref = nullptr;
     if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatmulPreferenceCreate(&pref);
     const uint64_t max_ws = blas_ws_bytes;
@@ -86,7 +87,7 @@ int dq_gemm(const uint16_t* x, const uint16_t* wd, uint16_t* y, int M, int N, in
     if (pref) hipblasLtMatmulPreferenceDestroy(pref);
     if (st != HIPBLAS_STATUS_SUCCESS || found < 1) {
       *err = st != HIPBLAS_STATUS_SUCCESS ? status_name(st) : "no hipBLASLt algorithm";
-      g_plans.erase(std::make_tuple(dev, M, N, K));
+      g_plans.erase(key);
       return -1;
     }
     int pick = 0;

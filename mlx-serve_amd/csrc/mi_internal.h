@@ -123,7 +123,8 @@ bool qmm_supported(int M, int N, int K, int bits, int gs);
 // Dequantize + hipBLASLt bf16 GEMM for large M (blas.cpp): y = x @ wd^T with wd the
 // dequantized bf16 [N, K] weight; blas_ws is the library's scratch. 0 or -1 (err set).
 constexpr size_t kDqGemmBlasWs = (size_t)32 << 20;
-int dq_gemm(const uint16_t* x, const uint16_t* wd, uint16_t* y, int M, int N, int K,
+// y^T is N x M with leading dimension ldy (N for a whole y, the full width for a slice).
+int dq_gemm(const uint16_t* x, const uint16_t* wd, uint16_t* y, int M, int N, int K, int ldy,
             void* blas_ws, size_t blas_ws_bytes, hipStream_t s, const char** err);
 
 // Quantize / dequantize / generator (quant.hip).
