@@ -307,7 +307,7 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
     // Items of 2..32 rows: the MFMA few-row kernel when it supports the layout.
     static const int use_qmvm = env_int("MI_QMM_QMVM_GATHER", 1);
     const int item_rows = J.use_items ? P.rpi : rows;
-    J.multi_row = use_qmvm && !P.x_f32 && item_rows >= 2 &&
+    J.multi_row = use_qmvm && !P.x_f32 && nb == 4 && item_rows >= 2 &&
                   x_batch * M * K * 2 < ((int64_t)1 << 32) &&
                   mi::qmvm_plan(item_rows, P.N, P.K, gs, nb, n_items, &J.planm);
     J.plan = J.narrow ? qmv16_plan(P.N, P.K, gs, nb, item_rows, n_items, P.x_f32)

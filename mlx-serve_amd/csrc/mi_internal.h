@@ -55,7 +55,8 @@ template <int GS>
 hipError_t launch_qmv1_gs(const QmvParams& P, dim3 grid, int waves, int nc, int xu, int depth,
                           size_t lds, hipStream_t s);
 
-// Few-row dense decode kernel (qmvm.hip): 2 <= M <= 32, 4-bit gs 64, bf16 x and y.
+// Few-row decode kernel (qmvm*.hip): 2 <= M <= 32 rows, gs 64, bf16 x and y; dense 4-/8-bit,
+// gathers 4-bit.
 struct QmvmParams {
   const void* x;
   const uint32_t* w;
@@ -67,7 +68,7 @@ struct QmvmParams {
   uint32_t upr_mr, spr_mr;  // set by launch_qmvm: ceil(2^32 / d) for the staging divisions
 };
 struct QmvmPlan {
-  int wr, ks, kr, waves, nc, xu, depth, tiles, mt, lds, sbf32, rows;
+  int wr, ks, kr, waves, nc, xu, depth, tiles, mt, lds, sbf32, rows, bits;
   size_t part_bytes;
 };
 // rows = activation rows per call (dense) or per work item (gathers, n_items items).

@@ -9,18 +9,24 @@
 namespace mi {
 
 namespace qmvm_detail {
-template void launch_family<16, true, false>(const QmvmParams&, const QmvParams&, const QmvmPlan&,
+template void launch_family<4, 16, true, false>(const QmvmParams&, const QmvParams&, const QmvmPlan&,
                                              dim3, hipStream_t);
-template void launch_family<16, false, false>(const QmvmParams&, const QmvParams&,
+template void launch_family<4, 16, false, false>(const QmvmParams&, const QmvParams&,
                                               const QmvmPlan&, dim3, hipStream_t);
-template void launch_family<32, false, false>(const QmvmParams&, const QmvParams&,
+template void launch_family<4, 32, false, false>(const QmvmParams&, const QmvParams&,
                                               const QmvmPlan&, dim3, hipStream_t);
-extern template void launch_family<16, true, true>(const QmvmParams&, const QmvParams&,
+extern template void launch_family<4, 16, true, true>(const QmvmParams&, const QmvParams&,
                                                    const QmvmPlan&, dim3, hipStream_t);
-extern template void launch_family<16, false, true>(const QmvmParams&, const QmvParams&,
+extern template void launch_family<4, 16, false, true>(const QmvmParams&, const QmvParams&,
                                                     const QmvmPlan&, dim3, hipStream_t);
-extern template void launch_family<32, false, true>(const QmvmParams&, const QmvParams&,
+extern template void launch_family<4, 32, false, true>(const QmvmParams&, const QmvParams&,
                                                     const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<8, 16, true, false>(const QmvmParams&, const QmvParams&,
+                                                    const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<8, 16, false, false>(const QmvmParams&, const QmvParams&,
+                                                     const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<8, 32, false, false>(const QmvmParams&, const QmvParams&,
+                                                     const QmvmPlan&, dim3, hipStream_t);
 }  // namespace qmvm_detail
 
 namespace {
@@ -52,24 +58,34 @@ void launch_any(QmvmParams P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
   using namespace qmvm_detail;
   P.upr_mr = div_magic((uint32_t)(pl.kr / 8));
   P.spr_mr = div_magic((uint32_t)(pl.kr / P.group_size / 2));
-  if (pl.mt == 16 && pl.sbf32) launch_family<16, true, GATHER>(P, G, pl, grid, s);
-  else if (pl.mt == 16) launch_family<16, false, GATHER>(P, G, pl, grid, s);
-  else launch_family<32, false, GATHER>(P, G, pl, grid, s);
+  if (pl.bits == 8) {
+    if constexpr (!GATHER) {  // 8-bit instances are dense only
+      if (pl.mt == 16 && pl.sbf32) launch_family<8, 16, true, false>(P, G, pl, grid, s);
+      else if (pl.mt == 16) launch_family<8, 16, false, false>(P, G, pl, grid, s);
+      else launch_family<8, 32, false, false>(P, G, pl, grid, s);
+    }
+    return;
+  }
+  if (pl.mt == 16 && pl.sbf32) launch_family<4, 16, true, GATHER>(P, G, pl, grid, s);
+  else if (pl.mt == 16) launch_family<4, 16, false, GATHER>(P, G, pl, grid, s);
+  else launch_family<4, 32, false, GATHER>(P, G, pl, grid, s);
 }
 
 }  // namespace
 
 bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan* out) {
-  if (bits != 4 || M < 2 || M > 32 || K % qmvm_detail::kChunkVals != 0) return false;
+  if ((bits != 4 && bits != 8) || M < 2 || M > 32) return false;
+  const int cv = 512 / bits;  // values per 64-byte chunk of a row
+  if (K % cv != 0) return false;
   if (gs != 64) return false;  // the other group sizes take the general decode kernels
-  if ((int64_t)N * (K / 2) >= ((int64_t)1 << 31) || (int64_t)M * K * 2 >= ((int64_t)1 << 31))
+  if ((int64_t)N * (K * bits / 8) >= ((int64_t)1 << 31) || (int64_t)M * K * 2 >= ((int64_t)1 << 31))
     return false;
   static const int env_wr = env_or("MI_QMVM_WR", 0);
   static const int env_target = env_or("MI_QMVM_TARGET", 0);
   static const int env_depth = env_or("MI_QMVM_DEPTH", 0);
   const int mt = M <= 16 ? 16 : 32;
   const size_t lds_max = 160 * 1024 - 512;  // the kernel's static row table
-  const int nch = K / qmvm_detail::kChunkVals;
+  const int nch = K / cv;
   const int target = env_target ? env_target : 8;
   // Weight tiles per block (WR): the staged activations are re-read from L2 once per
   // block, M / (4 WR) times the weight bytes, so take the most tiles that fit; then the
@@ -84,7 +100,8 @@ bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan*
     for (int ks = 1; ks <= nch; ++ks) {
       if (nch % ks) continue;
       const int chs = nch / ks;  // chunks per range
-      const int nvals = chs * qmvm_detail::kChunkVals;
+      const int nvals = chs * cv;
+      if (gs <= 64 && (nvals / gs) % 2) continue;  // scale/bias pairs: an even group count
       for (int wk = 1; wk * wr <= 16; ++wk) {
         if (chs % wk) continue;
         const int nc = chs / wk;
@@ -124,6 +141,7 @@ bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan*
   // two chunks in flight per wave: measured best for every M on this kernel
   best.depth = env_depth ? env_depth : 2;
   best.rows = M;
+  best.bits = bits;
   best.part_bytes = best.ks > 1 ? (size_t)best.ks * M * N * 4 : 0;
   static const int verbose = env_or("MI_QMVM_VERBOSE", 0);
   static int64_t last_key = -1;

@@ -4,11 +4,11 @@
 
 namespace mi {
 namespace qmvm_detail {
-template void launch_family<16, true, true>(const QmvmParams&, const QmvParams&, const QmvmPlan&,
+template void launch_family<4, 16, true, true>(const QmvmParams&, const QmvParams&, const QmvmPlan&,
                                             dim3, hipStream_t);
-template void launch_family<16, false, true>(const QmvmParams&, const QmvParams&,
+template void launch_family<4, 16, false, true>(const QmvmParams&, const QmvParams&,
                                              const QmvmPlan&, dim3, hipStream_t);
-template void launch_family<32, false, true>(const QmvmParams&, const QmvParams&,
+template void launch_family<4, 32, false, true>(const QmvmParams&, const QmvParams&,
                                              const QmvmPlan&, dim3, hipStream_t);
 }  // namespace qmvm_detail
 }  // namespace mi

@@ -1,4 +1,4 @@
-// Few-row decode GEMM, 4-bit affine gs 64, bf16 activations, on the 16x16x32 bf16 MFMA:
+// Few-row decode GEMM, 4- or 8-bit affine gs 64, bf16 activations, on the 16x16x32 bf16 MFMA:
 // dense quantized_matmul (2 <= M <= 32) and gather_qmm work items of 2..32 rows (sorted
 // expert runs). The weights stream straight into registers the way the one-row kernel
 // streams them (no LDS copy of the weights).
@@ -23,6 +23,9 @@
 // the group's affine terms are applied in fp32: s*C + (b - 128 s)*X, X = sum of x over
 // the group, from a second MFMA of the same B against an all-ones A. Columns are
 // activation rows (16 per MFMA; more than 16 rows run a second MFMA on rows 16..31).
+// 8-bit weights: a 64-byte chunk is 64 values, exactly one group of 64, so no transpose is
+// needed: step t takes words 2t, 2t+1 of the lane's 16 bytes as exact bf16 bytes q, the
+// activations stay in natural order and the group adds s*C + b*X.
 //
 // The waves' partial sums of a tile are added in wave order through LDS; K ranges beyond
 // one (activations too large for LDS) write fp32 partials that a second kernel sums in
@@ -42,6 +45,7 @@ using qmv_detail::lds_barrier;
 
 typedef __bf16 bf16x8m __attribute__((ext_vector_type(8)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2m __attribute__((ext_vector_type(2)));
 
 constexpr int kChunkVals = 128;
 constexpr int kBufFlags = 0x00020000;  // raw (untyped) dword buffer access on this target
@@ -59,6 +63,18 @@ MI_DEV u32x4_t unpack8(uint32_t w) {
   const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
   return u32x4_t{perm_b32(c43, lo, 0x04010400u), perm_b32(c43, lo, 0x04030402u),
                  perm_b32(c43, hi, 0x04010400u), perm_b32(c43, hi, 0x04030402u)};
+}
+
+// 8 bytes (two words) -> bf16 pairs (q0, q1), (q2, q3), (q4, q5), (q6, q7), exact.
+MI_DEV uint32_t pk_bf16(float lo, float hi) {
+  f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2m));
+}
+template <int k>
+MI_DEV float ubyte_f(uint32_t w) { return (float)((w >> (8 * k)) & 0xFFu); }
+MI_DEV u32x4_t unpack8b(uint32_t w0, uint32_t w1) {
+  return u32x4_t{pk_bf16(ubyte_f<0>(w0), ubyte_f<1>(w0)), pk_bf16(ubyte_f<2>(w0), ubyte_f<3>(w0)),
+                 pk_bf16(ubyte_f<0>(w1), ubyte_f<1>(w1)), pk_bf16(ubyte_f<2>(w1), ubyte_f<3>(w1))};
 }
 
 // 4x4 transpose of dwords across the four 16-lane rows of the wave: on return, register
@@ -97,11 +113,14 @@ __host__ __device__ inline QmvmLds qmvm_lds(int M, int nvals, int gs, int rows, 
 
 // G is read only by gathers (work items, index arrays, expert bank); dense calls pass
 // their shapes in P.
-template <int GS, int NC, int XU, int DEPTH, int MT, bool SBF32, bool GATHER>
+template <int BITS, int GS, int NC, int XU, int DEPTH, int MT, bool SBF32, bool GATHER>
 __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) {
+  constexpr int CV = 512 / BITS;        // values per 64-byte chunk of a row
+  constexpr int NSTEP = CV / 32;        // MFMA steps per chunk
+  constexpr float BOFF = BITS == 4 ? -128.f : 0.f;  // 4-bit A holds 128 + q
   constexpr int SPG = GS / 32;  // 32-value MFMA steps per group
   constexpr int D = DEPTH < NC ? DEPTH : NC;
-  constexpr int GPC = kChunkVals / GS;  // groups per chunk
+  constexpr int GPC = CV / GS;  // groups per chunk (GS <= CV)
   constexpr int SBW = SBF32 ? 2 : 1;    // LDS words per (group, row)
   constexpr int SU = 4;                 // scale/bias loads per thread
   constexpr bool PAIRS = GS <= 64;      // scale/bias as dwords (two groups) or halves
@@ -151,7 +170,7 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
     const __amdgpu_buffer_rsrc_t xres =
         __builtin_amdgcn_make_buffer_rsrc((void*)P.x, (short)0, xbytes_all, kBufFlags);
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(P.w + mat * (uint32_t)(K / 8)), (short)0, N * (K / 2), kBufFlags);
+        (void*)(P.w + mat * (uint32_t)(K * BITS / 32)), (short)0, N * (K * BITS / 8), kBufFlags);
     const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(P.scales + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
     const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
@@ -194,8 +213,8 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
       }
     }
     const int wrow = min(row0 + rt * 16 + i, N - 1);
-    const uint32_t wo = (uint32_t)wrow * (uint32_t)(K / 2) +
-                        (uint32_t)(kb0 + c0 * kChunkVals) / 2 + 16 * q;
+    const uint32_t wo = (uint32_t)wrow * (uint32_t)(K * BITS / 8) +
+                        (uint32_t)(kb0 + c0 * CV) * BITS / 8 + 16 * q;
     u32x4_t wv[NC];
 #pragma unroll
     for (int j = 0; j < D; ++j)
@@ -212,11 +231,13 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
       const int m = (int)__umulhi((uint32_t)u, P.upr_mr), k8 = u - m * upr;
       const u32x4_t X = xv[t];
       if (m < M) {
-        u32x4_t p;
-        p.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
-        p.y = perm_b32(X.w, X.z, 0x05040100u);  // (x4, x6)
-        p.z = perm_b32(X.y, X.x, 0x07060302u);  // (x1, x3)
-        p.w = perm_b32(X.w, X.z, 0x07060302u);  // (x5, x7)
+        u32x4_t p = X;  // 8-bit: natural order
+        if constexpr (BITS == 4) {
+          p.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
+          p.y = perm_b32(X.w, X.z, 0x05040100u);  // (x4, x6)
+          p.z = perm_b32(X.y, X.x, 0x07060302u);  // (x1, x3)
+          p.w = perm_b32(X.w, X.z, 0x07060302u);  // (x5, x7)
+        }
         *reinterpret_cast<u32x4_t*>(xs + m * L.xstride + k8 * 16) = p;
       }
     }
@@ -236,13 +257,13 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
         } else if constexpr (PAIRS) {
           const float s0 = lo_bf16(sv[t]), s1 = hi_bf16(sv[t]);
           *reinterpret_cast<f32x2_t*>(sb + 2 * ((2 * gp) * rows + rr)) =
-              f32x2_t{s0, fmaf(-128.f, s0, lo_bf16(bv[t]))};
+              f32x2_t{s0, fmaf(BOFF, s0, lo_bf16(bv[t]))};
           *reinterpret_cast<f32x2_t*>(sb + 2 * ((2 * gp + 1) * rows + rr)) =
-              f32x2_t{s1, fmaf(-128.f, s1, hi_bf16(bv[t]))};
+              f32x2_t{s1, fmaf(BOFF, s1, hi_bf16(bv[t]))};
         } else {
           const float s0 = lo_bf16(sv[t]);
           *reinterpret_cast<f32x2_t*>(sb + 2 * (gp * rows + rr)) =
-              f32x2_t{s0, fmaf(-128.f, s0, lo_bf16(bv[t]))};
+              f32x2_t{s0, fmaf(BOFF, s0, lo_bf16(bv[t]))};
         }
       }
     }
@@ -251,8 +272,11 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
     // 3. MFMA over the wave's chunks as they land.
     const int jj = min(i, M - 1);
     const int jj2 = min(16 + i, M - 1);
-    const unsigned char* xrow = xs + jj * L.xstride + 16 * q;
-    const unsigned char* xrow2 = xs + jj2 * L.xstride + 16 * q;
+    // 4-bit: lane block q of step t is values 32t + 8q.. of the chunk (after the
+    // transpose); 8-bit: values 16q + 8t.. (two words of the lane's own 16 bytes)
+    constexpr int QB = BITS == 4 ? 16 : 32;  // bytes between the lane blocks of a row
+    const unsigned char* xrow = xs + jj * L.xstride + QB * q;
+    const unsigned char* xrow2 = xs + jj2 * L.xstride + QB * q;
     // per-group pointer, stepped by one group at a time (no multiplies in the loop)
     const float* sbp = sb + SBW * ((c0 * GPC) * rows + rt * 16 + 4 * q);
     // A operand of ones (bf16 1.0 = 0x3F80): ones x B puts each column's group sum X in
@@ -266,14 +290,18 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
         if (j + D < NC)
           wv[j + D] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * (j + D), 0, 0);
       }
-      const u32x4_t tw = xpose4(wv[j]);
-      const int kc = (c0 + j) * kChunkVals;  // chunk start within the range
+      const u32x4_t tw = BITS == 4 ? xpose4(wv[j]) : wv[j];
+      const int kc = (c0 + j) * CV;  // chunk start within the range
       f32x4_t c = zero, c2 = zero, cx = zero, cx2 = zero;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const uint32_t d = t == 0 ? tw.x : t == 1 ? tw.y : t == 2 ? tw.z : tw.w;
-        const u32x4_t a = unpack8(d);
-        const int kb = (kc + 32 * t) * 2;  // byte offset of run t in a staged row (+16q)
+      for (int t = 0; t < NSTEP; ++t) {
+        u32x4_t a;
+        if constexpr (BITS == 4) {
+          a = unpack8(t == 0 ? tw.x : t == 1 ? tw.y : t == 2 ? tw.z : tw.w);
+        } else {
+          a = t == 0 ? unpack8b(tw.x, tw.y) : unpack8b(tw.z, tw.w);
+        }
+        const int kb = (kc + (BITS == 4 ? 32 : 8) * t) * 2;  // byte offset in a staged row
         const u32x4_t b = *reinterpret_cast<const u32x4_t*>(xrow + kb);
         c = mfma16(a, b, t % SPG == 0 ? zero : c);
         cx = mfma16(ones, b, t % SPG == 0 ? zero : cx);
@@ -290,13 +318,13 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
           } else {
             const u32x4_t ev = *reinterpret_cast<const u32x4_t*>(sbp);
             sb01.x = lo_bf16(ev.x);
-            sb01.y = fmaf(-128.f, sb01.x, hi_bf16(ev.x));
+            sb01.y = fmaf(BOFF, sb01.x, hi_bf16(ev.x));
             sb01.z = lo_bf16(ev.y);
-            sb01.w = fmaf(-128.f, sb01.z, hi_bf16(ev.y));
+            sb01.w = fmaf(BOFF, sb01.z, hi_bf16(ev.y));
             sb23.x = lo_bf16(ev.z);
-            sb23.y = fmaf(-128.f, sb23.x, hi_bf16(ev.z));
+            sb23.y = fmaf(BOFF, sb23.x, hi_bf16(ev.z));
             sb23.z = lo_bf16(ev.w);
-            sb23.w = fmaf(-128.f, sb23.z, hi_bf16(ev.w));
+            sb23.w = fmaf(BOFF, sb23.z, hi_bf16(ev.w));
           }
           sbp += SBW * rows;
           const float X = cx[0];
@@ -354,18 +382,18 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
 
 // Launches one instance family; explicitly instantiated per (MT, SBF32, GATHER) in
 // qmvm.hip (dense) and qmvm_gather.hip (gathers) so the instances compile in parallel.
-template <int MT, bool SBF32, bool GATHER>
+template <int BITS, int MT, bool SBF32, bool GATHER>
 void launch_family(const QmvmParams& P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
                    hipStream_t s);
 
-template <int NC, int MT, bool SBF32, bool GATHER>
+template <int BITS, int NC, int MT, bool SBF32, bool GATHER>
 void launch_xd(const QmvmParams& P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
                hipStream_t s) {
   const dim3 block(64 * pl.waves);
   const size_t lds = (size_t)pl.lds;
 #define MI_QMVM_LAUNCH(XU, DP)                                                              \
   do {                                                                                      \
-    auto k = qmvm_kernel<64, NC, XU, DP, MT, SBF32, GATHER>;                                \
+    auto k = qmvm_kernel<BITS, 64, NC, XU, DP, MT, SBF32, GATHER>;                          \
     static bool attr = false; /* LDS above 64 KiB needs the attribute, once per kernel */ \
     if (!attr) {                                                                            \
       (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, \
@@ -394,18 +422,18 @@ void launch_xd(const QmvmParams& P, const QmvParams& G, const QmvmPlan& pl, dim3
 #undef MI_QMVM_LAUNCH
 }
 
-template <int MT, bool SBF32, bool GATHER>
+template <int BITS, int MT, bool SBF32, bool GATHER>
 void launch_family(const QmvmParams& P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
                    hipStream_t s) {
   switch (pl.nc) {
-    case 1: launch_xd<1, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    case 2: launch_xd<2, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    case 3: launch_xd<3, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    case 4: launch_xd<4, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    case 5: launch_xd<5, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    case 6: launch_xd<6, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    case 7: launch_xd<7, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    default: launch_xd<8, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 1: launch_xd<BITS, 1, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 2: launch_xd<BITS, 2, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 3: launch_xd<BITS, 3, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 4: launch_xd<BITS, 4, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 5: launch_xd<BITS, 5, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 6: launch_xd<BITS, 6, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 7: launch_xd<BITS, 7, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    default: launch_xd<BITS, 8, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
   }
 }
 
