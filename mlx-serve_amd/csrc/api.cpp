@@ -610,8 +610,15 @@ int mi_gather_qmv_gate_up_swiglu(void* y, const void* x, const uint32_t* w_gate,
   uint16_t* u = (uint16_t*)((char*)data + half);
   void* rest = (char*)data + 2 * half;
   G.P.y = g;
-  U.P.y = u;
   if ((rc = gather_launch(G, rest, s)) != MI_OK) return rc;
+  // The one-row and few-row kernels (and the K-split reduce) apply SwiGLU as they write the
+  // up projection; the other kernels write u and a SwiGLU pass follows.
+  if (U.one_row || U.multi_row) {
+    U.P.y = y;
+    U.P.swiglu_gate = g;
+    return gather_launch(U, rest, s);
+  }
+  U.P.y = u;
   if ((rc = gather_launch(U, rest, s)) != MI_OK) return rc;
   hipError_t e = mi::launch_swiglu((uint16_t*)y, g, u, n_idx * N, s);
   return e == hipSuccess ? MI_OK : hip_fail(e, "swiglu launch");

@@ -22,6 +22,25 @@ MI_DEV uint32_t f32_to_bf16_bits(float f) {
 }
 
 // Eight bf16 values held in four dwords, as an MFMA A/B operand.
+// bf16 x bf16 is exact in fp32; one rounding to bf16.
+MI_DEV uint16_t bf16_mul(uint16_t a, uint16_t b) {
+  return (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(a) * bf16_bits_to_f32(b));
+}
+
+// Sigmoid of a bf16 value, rounded once to fp32 from a double evaluation and then to
+// bf16: the correctly rounded table value for all but astronomically rare inputs.
+MI_DEV uint16_t sigmoid_bf16(uint16_t g) {
+  const double v = (double)bf16_bits_to_f32(g);
+  const float s = (float)(1.0 / (1.0 + exp(-v)));
+  return (uint16_t)f32_to_bf16_bits(s);
+}
+
+// SwiGLU with the bf16 rounding points of the reference (src/transformer.zig:19846-19884):
+// bf16(bf16(g * sigmoid(g)) * u).
+MI_DEV uint16_t swiglu_bf16(uint16_t g, uint16_t u) {
+  return bf16_mul(bf16_mul(g, sigmoid_bf16(g)), u);
+}
+
 MI_DEV bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
 
 // v_perm_b32: bytes 0-3 of the 64-bit pool are `lo`, bytes 4-7 are `hi`.

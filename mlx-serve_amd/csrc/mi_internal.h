@@ -19,6 +19,8 @@ struct QmvParams {
   const uint32_t* items;   // nullable: sorted work list, 4 u32 per item (expert, pos0, cnt, 0)
   const uint32_t* item_count;  // device count for `items`
   float* part;             // ks > 1: fp32 partials [ks][n_pairs*M][N] (summed by a 2nd kernel)
+  // nullable, bf16 outputs only: y = swiglu(swiglu_gate, result) (the fused up projection)
+  const uint16_t* swiglu_gate;
   int64_t n_pairs, lhs_div, x_batch, n_experts;
   int M, N, K;
   int bits, group_size, x_f32;

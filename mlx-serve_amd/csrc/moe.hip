@@ -11,21 +11,8 @@
 namespace mi {
 namespace {
 
-MI_DEV uint16_t bf16_mul(uint16_t a, uint16_t b) {
-  // bf16 x bf16 is exact in fp32; one rounding to bf16.
-  return (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(a) * bf16_bits_to_f32(b));
-}
-
 MI_DEV uint16_t bf16_add(uint16_t a, uint16_t b) {
   return (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(a) + bf16_bits_to_f32(b));
-}
-
-// Sigmoid of a bf16 value, rounded once to fp32 from a double evaluation and then to
-// bf16: the correctly rounded table value for all but astronomically rare inputs.
-MI_DEV uint16_t sigmoid_bf16(uint16_t g) {
-  const double v = (double)bf16_bits_to_f32(g);
-  const float s = (float)(1.0 / (1.0 + exp(-v)));
-  return (uint16_t)f32_to_bf16_bits(s);
 }
 
 // (value, index) ordering of the top-k selection: larger value first, lower index on
@@ -212,7 +199,7 @@ __global__ void swiglu_kernel(uint16_t* __restrict__ y, const uint16_t* __restri
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
     const uint16_t gv = g[i];
-    y[i] = bf16_mul(bf16_mul(gv, sigmoid_bf16(gv)), u[i]);
+    y[i] = swiglu_bf16(gv, u[i]);
   }
 }
 

@@ -362,8 +362,13 @@ __global__ void reduce_splits_kernel(QmvParams P) {
     const uint32_t e = P.rhs ? P.rhs[pair] : pair;
     const uint32_t l = P.lhs ? P.lhs[pair] : pair / (uint32_t)P.lhs_div;
     if (e >= (uint32_t)P.n_experts || (int64_t)l >= P.x_batch) v = __builtin_nanf("");
-    if constexpr (XF32) ((float*)P.y)[i] = v;
-    else ((uint16_t*)P.y)[i] = (uint16_t)f32_to_bf16_bits(v);
+    if constexpr (XF32) {
+      ((float*)P.y)[i] = v;
+    } else {
+      uint16_t o = (uint16_t)f32_to_bf16_bits(v);
+      if (P.swiglu_gate) o = swiglu_bf16(P.swiglu_gate[i], o);
+      ((uint16_t*)P.y)[i] = o;
+    }
   }
 }
 

@@ -232,7 +232,9 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
         P.part[((int64_t)ks * PT + p) * N + nout] = v;
       } else {
         if (!ok) v = __builtin_nanf("");
-        ((uint16_t*)P.y)[p * N + nout] = (uint16_t)f32_to_bf16_bits(v);
+        uint16_t o = (uint16_t)f32_to_bf16_bits(v);
+        if (P.swiglu_gate) o = swiglu_bf16(P.swiglu_gate[p * N + nout], o);
+        ((uint16_t*)P.y)[p * N + nout] = o;
       }
     }
   };

@@ -373,7 +373,11 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
         const int64_t npos = GATHER ? PT : M;
         P.part[((int64_t)blockIdx.y * npos + pos) * N + n] = v;
       } else {
-        P.y[pos * N + n] = (uint16_t)f32_to_bf16_bits(v);
+        uint16_t o = (uint16_t)f32_to_bf16_bits(v);
+        if constexpr (GATHER) {
+          if (Gp.swiglu_gate) o = swiglu_bf16(Gp.swiglu_gate[pos * N + n], o);
+        }
+        P.y[pos * N + n] = o;
       }
     }
     if constexpr (GATHER) lds_barrier();  // LDS and the row table are reused by the next item
