@@ -88,11 +88,12 @@ bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan*
   const int nch = K / cv;
   const int target = env_target ? env_target : 8;
   // Weight tiles per block (WR): the staged activations are re-read from L2 once per
-  // block, M / (4 WR) times the weight bytes, so take the most tiles that fit; then the
+  // block, M / (4 WR) times the weight bytes, so take the most tiles that fit (measured:
+  // 1 for M <= 2, 4 up to 16 rows, 8 above); then the
   // fewest K ranges (each range beyond one writes fp32 partials and needs the reduce
   // launch); then chunks per wave near `target` and more waves. Scale/bias pairs are
   // staged as fp32 (s, b - 128 s) when LDS allows, else as bf16 pairs.
-  const int wr0 = env_wr ? env_wr : M <= 2 ? 1 : 4;
+  const int wr0 = env_wr ? env_wr : M <= 2 ? 1 : M <= 16 ? 4 : 8;
   QmvmPlan best{};
   double best_cost = 1e30;
   for (int wr = wr0; wr >= 1 && !best.nc; wr >>= 1) {
