@@ -411,10 +411,10 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   if (!y || !x || !w || !scales || !biases) return fail(MI_ERR_INVALID, "null tensor pointer");
   if (N > (int64_t)1 << 30 || M > (int64_t)1 << 30) return fail(MI_ERR_INVALID, "N or M too large");
   hipStream_t s = (hipStream_t)stream;
-  // Large M: dequantize once into the workspace and run a dense bf16 GEMM (the reference's
+  // M >= 256: dequantize once into the workspace and run a dense bf16 GEMM (the reference's
   // prefillDqGemm shape, src/transformer.zig:20987-21011); below the threshold the fused
   // dequant-in-register kernel is faster.
-  static const int dq_min = env_int("MI_QMM_DQGEMM_MIN", 1024);
+  static const int dq_min = env_int("MI_QMM_DQGEMM_MIN", 256);
   if (x_dtype == MI_DTYPE_BFLOAT16 && dq_min > 0 && M >= dq_min && K <= INT32_MAX &&
       N * K * 2 <= ((int64_t)1 << 34)) {
     const size_t wbytes = round256((size_t)N * K * 2);

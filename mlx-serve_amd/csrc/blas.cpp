@@ -2,7 +2,7 @@
 // bf16 [N, K] workspace and y[M, N] = x[M, K] @ W^T runs as a plain bf16 GEMM (fp32
 // accumulation) on hipBLASLt. This is the shape of the reference's prefillDqGemm
 // (src/transformer.zig:20987-21011), which switches to dequantize + dense GEMM for
-// large M; on MI355X the library GEMM sustains more MFMA throughput at M >= ~1024 than the
+// large M; on MI355X the library GEMM sustains more MFMA throughput at M >= ~256 than the
 // fused dequant-in-register kernel (qmm.hip), which keeps the smaller M.
 #include <hipblaslt/hipblaslt.h>
 

@@ -218,14 +218,14 @@ def test_fill_randn_matches_oracle_stream(dev):
 
 
 PREFILL_CASES = [(33, 64, 256), (128, 256, 512), (257, 300, 1024), (512, 520, 2048), (300, 200, 768),
-                 (640, 256, 4096), (1024, 256, 512)]
+                 (640, 256, 4096), (1024, 256, 512), (200, 512, 4096)]
 
 
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("gs", [32, 64, 128])
 @pytest.mark.parametrize("M,N,K", PREFILL_CASES)
 def test_prefill_qmm(dev, M, N, K, bits, gs):
-    """Large-M paths: the fused MFMA GEMM (M < 1024) and dequantize + hipBLASLt (M >= 1024)."""
+    """Large-M paths: the fused MFMA GEMM (M < 256) and dequantize + hipBLASLt (M >= 256)."""
     _print_case(t="prefill", M=M, N=N, K=K, bits=bits, gs=gs)
     wq, s, b = weights(1, N, K, bits, gs, 5000 + M)
     x = O.make_x_bf16(M, K, 6000 + N)
