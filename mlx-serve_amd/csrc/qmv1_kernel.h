@@ -65,6 +65,14 @@ MI_DEV uint32_t quad_bcast(uint32_t v, int src) {
   }
 }
 
+// Value of lane ^ 1 / lane ^ 2 within the quad (DPP quad_perm, no LDS round trip).
+MI_DEV float quad_xor1(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+MI_DEV float quad_xor2(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+
 // Lanes 0,1 of each quad take lane a, lanes 2,3 take lane a+1 (a = 0 or 2).
 MI_DEV uint32_t quad_pairs(uint32_t v, int a) {
   return a == 0 ? (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x50, 0xF, 0xF, false)
@@ -163,8 +171,8 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
                   (bf16_bits_to_f32(X.y & 0xFFFFu) + bf16_bits_to_f32(X.y >> 16))) +
                  ((bf16_bits_to_f32(X.z & 0xFFFFu) + bf16_bits_to_f32(X.z >> 16)) +
                   (bf16_bits_to_f32(X.w & 0xFFFFu) + bf16_bits_to_f32(X.w >> 16)));
-      s8 += __shfl_xor(s8, 1, 64);
-      s8 += __shfl_xor(s8, 2, 64);
+      s8 += quad_xor1(s8);
+      s8 += quad_xor2(s8);
       if (u < nunits) {
         u32x4_t o;
         o.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
@@ -219,8 +227,8 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
       if constexpr (D < NC) __builtin_amdgcn_sched_barrier(0);  // keep the issue order
     }
     // 4. reduce the row's 4 lanes, then the waves in order.
-    y += __shfl_xor(y, 1, 64);
-    y += __shfl_xor(y, 2, 64);
+    y += quad_xor1(y);
+    y += quad_xor2(y);
     if (g == 0) red[wave * 16 + r] = y;
     lds_barrier();
     if (tid < 16 && tile * 16 + tid < N) {
