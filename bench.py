@@ -280,6 +280,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--decode-only", type=int, default=0, metavar="M",
+                    help="only run the configs[1] decode step at this M (for rocprofv3)")
+    ap.add_argument("--bits", type=int, default=4, choices=(4, 8),
+                    help="weight bits of --decode-only")
     ap.add_argument("--prefill-only", type=int, default=0, metavar="M",
                     help="only run the configs[2] prefill shapes at this M (for rocprofv3)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -303,6 +307,14 @@ def main():
         print(json.dumps({"copy_calibration_bytes_each_way": a.numel() * 2, "copies": 4}))
         return
     import mi_qmm as mi
+    if args.decode_only:
+        layers = build_mlp_layers(torch, mi, args.layers, args.bits, 64, dev)
+        r = decode_mlp(torch, mi, layers, args.decode_only, args.bits, 64, dev, args.steps,
+                       args.warmup)
+        print(json.dumps({"M": args.decode_only, "bits": args.bits,
+                          "GBs": round(r["GBs"], 1), "avg_launch_us": round(r["avg_launch_us"], 3),
+                          "bytes_per_launch": r["bytes_per_launch"]}))
+        return
     if args.prefill_only:
         print(json.dumps(prefill(torch, mi, dev, (args.prefill_only,), steps=args.steps,
                                  warmup=args.warmup)))
