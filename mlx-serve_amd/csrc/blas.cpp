@@ -78,7 +78,7 @@ int dq_gemm(const uint16_t* x, const uint16_t* wd, uint16_t* y, int M, int N, in
     if (st == HIPBLAS_STATUS_SUCCESS)
       st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
                                                  &max_ws, sizeof(max_ws));
-    constexpr int kCand = 8;
+    constexpr int kCand = 32;
     hipblasLtMatmulHeuristicResult_t res[kCand];
     int found = 0;
     if (st == HIPBLAS_STATUS_SUCCESS)
@@ -91,7 +91,7 @@ int dq_gemm(const uint16_t* x, const uint16_t* wd, uint16_t* y, int M, int N, in
       return -1;
     }
     int pick = 0;
-    // Outside stream capture, time the candidates once on the call's own buffers (each run
+    // Outside stream capture, time up to 32 candidates once on the call's own buffers (each run
     // writes the same y) and keep the fastest; under capture take the library's first.
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (found > 1 && hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
