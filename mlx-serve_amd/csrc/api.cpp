@@ -609,6 +609,16 @@ int mi_gather_qmv_gate_up_swiglu(void* y, const void* x, const uint32_t* w_gate,
   uint16_t* g = (uint16_t*)data;
   uint16_t* u = (uint16_t*)((char*)data + half);
   void* rest = (char*)data + 2 * half;
+  // One launch for gate, up and SwiGLU when both run on the one-row kernel, gs 64, with a
+  // single K range (same shapes, so G's plan is U's plan).
+  if (G.one_row && U.one_row && G.P.group_size == 64 && G.P.ks == 1 && !G.P.x_f32) {
+    G.P.w2 = w_up;
+    G.P.scales2 = (const uint16_t*)s_up;
+    G.P.biases2 = (const uint16_t*)b_up;
+    G.P.dual = 1;
+    G.P.y = y;
+    return gather_launch(G, rest, s);
+  }
   G.P.y = g;
   if ((rc = gather_launch(G, rest, s)) != MI_OK) return rc;
   // The one-row and few-row kernels (and the K-split reduce) apply SwiGLU as they write the

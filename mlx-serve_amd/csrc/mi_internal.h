@@ -21,6 +21,12 @@ struct QmvParams {
   float* part;             // ks > 1: fp32 partials [ks][n_pairs*M][N] (summed by a 2nd kernel)
   // nullable, bf16 outputs only: y = swiglu(swiglu_gate, result) (the fused up projection)
   const uint16_t* swiglu_gate;
+  // dual (one-row kernel, gs 64, one K range): w/scales/biases is the gate bank, these the
+  // up bank, and y = swiglu(gate, up) in one launch
+  const uint32_t* w2;
+  const uint16_t* scales2;
+  const uint16_t* biases2;
+  int dual;
   int64_t n_pairs, lhs_div, x_batch, n_experts;
   int M, N, K;
   int bits, group_size, x_f32;

@@ -20,6 +20,8 @@
 #include "mi_internal.h"
 #include "qmv_common.h"
 
+#include <type_traits>
+
 
 namespace mi {
 namespace qmv1_detail {
@@ -85,7 +87,7 @@ constexpr int groups_per_chunk() {
 }
 
 // Up to 16 waves per block when a wave holds <= 8 chunks (<= 128 VGPRs), else 8.
-template <int GS, int NC, int XU, int DEPTH, bool DENSE>
+template <int GS, int NC, int XU, int DEPTH, bool DENSE, bool DUAL = false>
 __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P) {
   constexpr int GPC = groups_per_chunk<GS>();
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -113,7 +115,14 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
   const uint32_t nn = (uint32_t)min(n, N - 1);
   const int64_t PT = P.n_pairs * P.M;
 
-  auto process = [&](const Item& it, int64_t xr) {
+  // DUAL: gate (bank 0) then up (bank 1) for the same item; the gate sums wait in gsave and
+  // the up pass writes swiglu(gate, up) with the reference's rounding points.
+  __shared__ float gsave[16];
+  auto process = [&](const Item& it, int64_t xr, auto bank_c) {
+    constexpr int BANK = decltype(bank_c)::value;
+    const uint32_t* Pw = BANK ? P.w2 : P.w;
+    const uint16_t* Ps = BANK ? P.scales2 : P.scales;
+    const uint16_t* Pb = BANK ? P.biases2 : P.biases;
     const uint32_t e = __builtin_amdgcn_readfirstlane(it.expert_ok ? it.expert : 0u);
     const bool ok = it.expert_ok && xr >= 0;
 
@@ -126,15 +135,18 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
         __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, nvals * 2, kBufFlags);
     const size_t mat = (size_t)e * (uint32_t)N;
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(P.w + mat * (uint32_t)(K / 8)), (short)0, N * (K / 2), kBufFlags);
+        (void*)(Pw + mat * (uint32_t)(K / 8)), (short)0, N * (K / 2), kBufFlags);
     const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(P.scales + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
+        (void*)(Ps + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
     const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(P.biases + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
+        (void*)(Pb + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
+    constexpr bool STAGE = BANK == 0;  // the up pass reuses the staged activations
     u32x4_t xv[XU];
+    if constexpr (STAGE) {
 #pragma unroll
-    for (int i = 0; i < XU; ++i)
-      xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xres, (tid + i * BD) * 16, 0, 0);
+      for (int i = 0; i < XU; ++i)
+        xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xres, (tid + i * BD) * 16, 0, 0);
+    }
     const uint32_t wo = nn * (uint32_t)(K / 2) + (uint32_t)(kb0 + c0 * kChunkVals) / 2 + 16 * g;
     // Scales/biases. gs 64/32: the wave's groups of a row are contiguous dwords; lane g
     // of the row's quad loads dwords g, g+4, ... and chunks take theirs by a quad
@@ -162,6 +174,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     u32x4_t wv[NC];
 #pragma unroll
     for (int j = 0; j < D; ++j) wv[j] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * j, 0, 0);
+    if constexpr (STAGE) {
     // 2. stage the activations in dot8's pair order, with per-32-value sums.
 #pragma unroll
     for (int i = 0; i < XU; ++i) {
@@ -182,6 +195,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
         *reinterpret_cast<u32x4_t*>(xs + u * 4) = o;
         if ((u & 3) == 0) xsum[u >> 2] = s8;
       }
+    }
     }
     // LDS-only barrier: the weight loads stay in flight.
     lds_barrier();
@@ -236,16 +250,23 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
       for (int w2 = 0; w2 < W; ++w2) v += red[w2 * 16 + tid];
       const int64_t p = it.pos0;
       const int nout = tile * 16 + tid;
-      if (P.ks > 1) {
+      if (!DUAL && P.ks > 1) {
         P.part[((int64_t)ks * PT + p) * N + nout] = v;
       } else {
         if (!ok) v = __builtin_nanf("");
-        uint16_t o = (uint16_t)f32_to_bf16_bits(v);
-        if (P.swiglu_gate) o = swiglu_bf16(P.swiglu_gate[p * N + nout], o);
-        ((uint16_t*)P.y)[p * N + nout] = o;
+        if (DUAL && BANK == 0) {
+          gsave[tid] = v;
+        } else {
+          uint16_t o = (uint16_t)f32_to_bf16_bits(v);
+          if (DUAL) o = swiglu_bf16((uint16_t)f32_to_bf16_bits(gsave[tid]), o);
+          else if (P.swiglu_gate) o = swiglu_bf16(P.swiglu_gate[p * N + nout], o);
+          ((uint16_t*)P.y)[p * N + nout] = o;
+        }
       }
     }
   };
+  using bank0 = std::integral_constant<int, 0>;
+  using bank1 = std::integral_constant<int, 1>;
 
   if constexpr (DENSE) {
     // one pair, no indices: straight-line, no work-item decode
@@ -254,7 +275,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     it.cnt = 1;
     it.expert = 0;
     it.expert_ok = true;
-    process(it, 0);
+    process(it, 0, bank0{});
   } else {
     const int n_items = P.items ? (int)*P.item_count : P.n_items_fixed;
     for (int it_i = blockIdx.z; it_i < n_items; it_i += gridDim.z) {
@@ -262,20 +283,33 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
       if (it.cnt <= 0) continue;
       const int64_t xr = item_x_row(P, it, 0);
       if (xr == -1) continue;  // block-uniform
-      process(it, xr);
+      process(it, xr, bank0{});
+      if constexpr (DUAL) {
+        lds_barrier();  // gsave and the reduction buffer
+        process(it, xr, bank1{});
+      }
       lds_barrier();  // LDS is reused by the next item
     }
   }
 }
 
+template <int GS, int NC, int DEPTH, bool DENSE, bool DUAL>
+void launch_xu2(const QmvParams& P, dim3 grid, dim3 block, int xu, size_t lds, hipStream_t s) {
+  switch (xu) {
+    case 1: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 1, DEPTH, DENSE, DUAL>), grid, block, lds, s, P); break;
+    case 2: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 2, DEPTH, DENSE, DUAL>), grid, block, lds, s, P); break;
+    case 4: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 4, DEPTH, DENSE, DUAL>), grid, block, lds, s, P); break;
+    default: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 8, DEPTH, DENSE, DUAL>), grid, block, lds, s, P); break;
+  }
+}
+
 template <int GS, int NC, int DEPTH, bool DENSE>
 void launch_xu(const QmvParams& P, dim3 grid, dim3 block, int xu, size_t lds, hipStream_t s) {
-  switch (xu) {
-    case 1: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 1, DEPTH, DENSE>), grid, block, lds, s, P); break;
-    case 2: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 2, DEPTH, DENSE>), grid, block, lds, s, P); break;
-    case 4: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 4, DEPTH, DENSE>), grid, block, lds, s, P); break;
-    default: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 8, DEPTH, DENSE>), grid, block, lds, s, P); break;
+  // gate + up + SwiGLU in one launch: group size 64 work items only
+  if constexpr (GS == 64 && !DENSE) {
+    if (P.dual) return launch_xu2<GS, NC, DEPTH, false, true>(P, grid, block, xu, lds, s);
   }
+  launch_xu2<GS, NC, DEPTH, DENSE, false>(P, grid, block, xu, lds, s);
 }
 
 template <int GS, int NC, bool DENSE>

@@ -110,7 +110,8 @@ def _bank(E, N, K, seed, bits=4):
     return wq, s, b
 
 
-@pytest.mark.parametrize("T,E,k,N,K", [(1, 16, 8, 192, 512), (3, 12, 4, 128, 256)])
+@pytest.mark.parametrize("T,E,k,N,K", [(1, 16, 8, 192, 512), (3, 12, 4, 128, 256),
+                                       (2, 8, 4, 256, 2048)])
 def test_fused_decode_mlp_matches_split(dev, T, E, k, N, K):
     """gate+up+SwiGLU and down+reduce entry points == split gather_qmm + glue, bit for bit;
     and the split path matches the oracle composition within tolerance."""
