@@ -155,18 +155,28 @@ __global__ void __launch_bounds__(kSortThreads) sort_dispatch_kernel(
   const int b0 = min(tid * per, NB), b1 = min(b0 + per, NB);
   uint32_t local = 0;
   for (int b = b0; b < b1; ++b) local += cnt[b];
-  part[tid] = local;
+  // Block exclusive scan of `local`: inclusive scan within each wave, then the waves'
+  // totals (16) scanned by the first wave.
+  uint32_t incl = local;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) part[wave] = incl;
   __syncthreads();
-  if (tid == 0) {
-    uint32_t run = 0;
-    for (int i = 0; i < kSortThreads; ++i) {
-      const uint32_t c = part[i];
-      part[i] = run;
-      run += c;
+  if (wave == 0) {
+    uint32_t wt = lane < kSortThreads / 64 ? part[lane] : 0u;
+    uint32_t wi = wt;
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) {
+      const uint32_t o = __shfl_up(wi, d, 64);
+      if (lane >= d) wi += o;
     }
+    if (lane < kSortThreads / 64) part[kSortThreads / 64 + lane] = wi - wt;  // exclusive
   }
   __syncthreads();
-  uint32_t run = part[tid];
+  uint32_t run = part[kSortThreads / 64 + wave] + incl - local;
   for (int b = b0; b < b1; ++b) {
     const uint32_t c = cnt[b];
     cnt[b] = run;  // cnt now holds the next free position of each bucket
@@ -198,7 +208,7 @@ __global__ void __launch_bounds__(kSortThreads) sort_dispatch_kernel(
         const uint32_t pos = start + (uint32_t)rank;
         order[pos] = (uint32_t)i;
         sorted[pos] = raw;
-        lhs[pos] = (uint32_t)(i / k);
+        lhs[pos] = (uint32_t)i / (uint32_t)k;
         inv[i] = pos;
         if (lead) cnt[b] = start + (uint32_t)__popcll(peers);
       }

@@ -182,6 +182,7 @@ constexpr int kBT = 1024;
 template <bool MAX>
 __device__ int64_t block_scan_incl(int64_t v, int64_t* sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int NW = kBT / 64;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     const int64_t o = __shfl_up(v, d, 64);
@@ -189,12 +190,21 @@ __device__ int64_t block_scan_incl(int64_t v, int64_t* sh) {
   }
   if (lane == 63) sh[wave] = v;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int i = 1; i < kBT / 64; ++i) sh[i] = MAX ? (sh[i - 1] > sh[i] ? sh[i - 1] : sh[i]) : sh[i - 1] + sh[i];
+  if (wave == 0) {  // exclusive scan of the wave totals, by shuffles in the first wave
+    const int64_t id = MAX ? INT64_MIN : 0;
+    const int64_t t = lane < NW ? sh[lane] : id;
+    int64_t w = t;
+#pragma unroll
+    for (int d = 1; d < NW; d <<= 1) {
+      const int64_t o = __shfl_up(w, d, 64);
+      if (lane >= d) w = MAX ? (o > w ? o : w) : w + o;
+    }
+    const int64_t prev = __shfl_up(w, 1, 64);  // inclusive value of the lane before
+    if (lane < NW) sh[NW + lane] = MAX ? (lane ? prev : id) : w - t;
   }
   __syncthreads();
   if (wave > 0) {
-    const int64_t p = sh[wave - 1];
+    const int64_t p = sh[NW + wave];
     v = MAX ? (p > v ? p : v) : v + p;
   }
   __syncthreads();
@@ -206,7 +216,7 @@ __global__ void __launch_bounds__(kBT) build_items_kernel(const uint32_t* __rest
                                                           uint32_t* __restrict__ items,
                                                           uint32_t* __restrict__ count,
                                                           int64_t max_items) {
-  __shared__ int64_t sh[kBT / 64];
+  __shared__ int64_t sh[2 * (kBT / 64)];
   __shared__ int64_t carry_a, carry_n;
   if (threadIdx.x == 0) { carry_a = 0; carry_n = 0; }
   __syncthreads();
@@ -219,15 +229,16 @@ __global__ void __launch_bounds__(kBT) build_items_kernel(const uint32_t* __rest
     const int64_t ca = carry_a;
     if (a < ca) a = ca;
     int64_t c = 0;
+    const int rs = __builtin_ctz((unsigned)R);  // rows per item: a power of two
     if (in) {
       const int64_t o = j - a;
-      c = ((o + 1) * M + R - 1) / R - (o * M + R - 1) / R;
+      c = (((o + 1) * M + R - 1) >> rs) - ((o * M + R - 1) >> rs);
     }
     const int64_t incl = block_scan_incl<false>(c, sh);
     const int64_t off = carry_n + incl - c;
     if (in) {
       const int64_t o = j - a;
-      int64_t first = (o * M + R - 1) / R;
+      int64_t first = (o * M + R - 1) >> rs;
       for (int64_t t = 0; t < c; ++t) {
         const int64_t idx = off + t;
         if (idx < max_items) {
