@@ -650,6 +650,17 @@ int mi_gather_qmv_down_reduce(void* y, const void* act, const uint32_t* w_down,
                           MI_DTYPE_BFLOAT16);
   if (rc || D.empty) return rc;
   hipStream_t s = (hipStream_t)stream;
+  // Few tokens: one launch computes each token's k down rows and their weighted sum (the
+  // experts' tiles are read once per token either way at this size).
+  static const int fused_max_t = env_int("MI_MOE_DOWN_FUSED_MAXT", 4);
+  if (T <= fused_max_t && D.one_row && D.plan1.ks == 1 && !D.P.x_f32 &&
+      mi::moe_down_supported(T, k, N, K, D.P.group_size, D.P.bits, D.plan1.waves, D.plan1.nc)) {
+    hipError_t e = mi::launch_moe_down((uint16_t*)y, (const uint16_t*)act, w_down,
+                                       (const uint16_t*)s_down, (const uint16_t*)b_down, inds,
+                                       (const uint16_t*)scores, T, k, N, K, n_experts, D.plan1.waves,
+                                       D.plan1.nc, s);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "moe_down launch");
+  }
   const size_t vb = round256((size_t)n_idx * N * 2);
   void* data = nullptr;
   rc = workspace(s, vb + D.ws_bytes(), &data);

@@ -109,6 +109,12 @@ hipError_t launch_swiglu(uint16_t* y, const uint16_t* g, const uint16_t* u, int6
                          hipStream_t s);
 hipError_t launch_down_reduce(uint16_t* y, const uint16_t* v, const uint16_t* scores, int64_t T,
                               int k, int64_t N, hipStream_t s);
+// Decode MoE down projection + score-weighted slot sum in one launch (moe_down.hip).
+bool moe_down_supported(int64_t T, int k, int64_t N, int64_t K, int gs, int bits, int ws, int nc);
+hipError_t launch_moe_down(uint16_t* y, const uint16_t* act, const uint32_t* w,
+                           const uint16_t* scales, const uint16_t* biases, const uint32_t* inds,
+                           const uint16_t* scores, int64_t T, int k, int64_t N, int64_t K,
+                           int64_t E, int ws, int nc, hipStream_t s);
 
 // Prefill GEMM (qmm.hip). Returns hipErrorNotSupported if the shape is not handled.
 struct QmmParams {

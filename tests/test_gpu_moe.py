@@ -111,7 +111,8 @@ def _bank(E, N, K, seed, bits=4):
 
 
 @pytest.mark.parametrize("T,E,k,N,K", [(1, 16, 8, 192, 512), (3, 12, 4, 128, 256),
-                                       (2, 8, 4, 256, 2048)])
+                                       (2, 8, 4, 256, 2048), (1, 32, 8, 768, 2048),
+                                       (4, 24, 6, 512, 1024)])
 def test_fused_decode_mlp_matches_split(dev, T, E, k, N, K):
     """gate+up+SwiGLU and down+reduce entry points == split gather_qmm + glue, bit for bit;
     and the split path matches the oracle composition within tolerance."""
@@ -149,6 +150,33 @@ def test_fused_decode_mlp_matches_split(dev, T, E, k, N, K):
                                               bf16_bits(u_split).reshape(T * k, N)))
     tv = O.gather_qmm_f64(a_np.reshape(T * k, 1, N), dq, ds, db, None, inds.reshape(-1), T * k)
     assert max_err_ratio(to_f64(v_split).reshape(T * k, 1, K), tv) <= BF16_TOL
+
+
+def test_down_reduce_out_of_range_expert(dev):
+    """An expert id >= E gives NaN for its slot (the one-row kernel's rule), so the token's
+    row is NaN; the other tokens are unaffected. One-launch and split paths agree bitwise."""
+    _print_case(t="down_oob")
+    T, E, k, N, K = 3, 16, 8, 768, 2048
+    rng = np.random.default_rng(5)
+    dq, ds, db = _bank(E, K, N, 31)
+    a = O.make_x_bf16(T * k, N, 32)
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.uint32)
+    inds[1, 3] = E + 7
+    sc = O.f32_to_bf16(rng.random((T, k)).astype(np.float32))
+    Dn = [to_dev_u32(dq, dev), to_dev_bf16(ds, dev), to_dev_bf16(db, dev)]
+    ad, idd, scd = to_dev_bf16(a, dev), to_dev_u32(inds, dev), to_dev_bf16(sc, dev)
+    y = mi_qmm.gather_qmv_down_reduce(ad.reshape(T, k, N), *Dn, idd, scd, group_size=64, bits=4)
+    v_split = mi_qmm.gather_qmm(ad.reshape(T * k, 1, N), *Dn, rhs_indices=idd.reshape(-1),
+                                group_size=64, bits=4)
+    y_split = mi_qmm.moe_down_reduce(v_split.reshape(T, k, K), scd)
+    assert torch.equal(y.view(torch.int16), y_split.view(torch.int16))
+    yf = to_f64(y)
+    assert np.isnan(yf[1]).all() and not np.isnan(yf[0]).any() and not np.isnan(yf[2]).any()
+    ok = inds.copy()
+    ok[1, 3] = 0
+    tv = O.gather_qmm_f64(a.reshape(T * k, 1, N), dq, ds, db, None, ok.reshape(-1), T * k)
+    assert max_err_ratio(to_f64(v_split).reshape(T * k, 1, K)[[0, 1, 2, 16, 17]],
+                         tv[[0, 1, 2, 16, 17]]) <= BF16_TOL
 
 
 def test_sorted_moe_pipeline_end_to_end(dev):
