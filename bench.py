@@ -286,6 +286,9 @@ def main():
                     help="weight bits of --decode-only")
     ap.add_argument("--prefill-only", type=int, default=0, metavar="M",
                     help="only run the configs[2] prefill shapes at this M (for rocprofv3)")
+    ap.add_argument("--moe-only", type=int, default=0, choices=(0, 3, 4), metavar="CFG",
+                    help="only run the MoE layer of configs[CFG] (3 or 4; for rocprofv3)")
+    ap.add_argument("--tokens", type=int, default=0, help="T of --moe-only (default: all)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 4 device copies of 256 MiB (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes)")
@@ -318,6 +321,16 @@ def main():
     if args.prefill_only:
         print(json.dumps(prefill(torch, mi, dev, (args.prefill_only,), steps=args.steps,
                                  warmup=args.warmup)))
+        return
+    if args.moe_only:
+        if args.moe_only == 3:
+            Ts = (args.tokens,) if args.tokens else (1, 512)
+            r = moe_layer(torch, mi, dev, 3, 128, 2048, 768, 8, Ts)
+        else:
+            Ts = (args.tokens,) if args.tokens else (1, 8, 64)
+            r = moe_layer(torch, mi, dev, 4, 256, 7168, 2048, 8, Ts, skew=True)
+            r.update(shared_expert_8bit(torch, mi, dev, Ts))
+        print(json.dumps(r))
         return
     bits, gs = 4, 64
     layers = build_mlp_layers(torch, mi, args.layers, bits, gs, dev)

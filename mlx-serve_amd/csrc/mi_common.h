@@ -51,3 +51,23 @@ MI_DEV uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
 MI_DEV f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+
+// Inclusive wave scan (sum, or max when MAX) of 32-bit ints without LDS: Hillis-Steele
+// over each 16-lane row with DPP row_shr 1/2/4/8 (lanes whose source is outside the row
+// keep the identity), then each row adds the totals of the rows before it, read with
+// v_readlane (scalar, no LDS round trip).
+template <bool MAX>
+MI_DEV int wave_scan_incl_i32(int v) {
+  constexpr int id = MAX ? INT32_MIN : 0;
+  auto op = [](int a, int b) { return MAX ? (a > b ? a : b) : a + b; };
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x111, 0xF, 0xF, false));
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x112, 0xF, 0xF, false));
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x114, 0xF, 0xF, false));
+  v = op(v, __builtin_amdgcn_update_dpp(id, v, 0x118, 0xF, 0xF, false));
+  const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31),
+            r2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = (int)(threadIdx.x & 63) >> 4;
+  const int p01 = op(r0, r1), p012 = op(p01, r2);
+  const int before = row == 0 ? id : row == 1 ? r0 : row == 2 ? p01 : p012;
+  return op(v, before);
+}

@@ -134,20 +134,41 @@ __global__ void __launch_bounds__(256) route_topk_kernel(const float* __restrict
 // sorted position of expert e and seg[E] the number of in-range ids.
 constexpr int kSortThreads = 1024;
 
+// WAVE_COUNTS: the scatter of a 1024-id chunk takes 3 barriers: each wave's per-bucket
+// counts go to an LDS table wc[16][E+1] (16-bit) and an id's position adds the counts of
+// the waves before its own. Otherwise the 16 waves take turns (16 barriers per chunk),
+// for expert counts whose table does not fit in LDS.
+constexpr int kSortWaves = kSortThreads / 64;
+constexpr int kSortMaxWaveCountE = 4000;
+
+template <bool WAVE_COUNTS>
 __global__ void __launch_bounds__(kSortThreads) sort_dispatch_kernel(
     const uint32_t* __restrict__ flat, int64_t n, int k, int E, uint32_t* __restrict__ order,
     uint32_t* __restrict__ inv, uint32_t* __restrict__ sorted, uint32_t* __restrict__ lhs,
     uint32_t* __restrict__ seg) {
-  extern __shared__ uint32_t sh[];  // cnt[E+1] then part[kSortThreads]
+  extern __shared__ uint32_t sh[];  // cnt[E+1], part[kSortThreads], then wc[16][E+1] u16
   uint32_t* cnt = sh;
   uint32_t* part = sh + (E + 1);
+  uint16_t* wc = reinterpret_cast<uint16_t*>(part + kSortThreads);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NB = E + 1;
+  const int nbits = 32 - __builtin_clz((unsigned)E);  // bits of the largest bucket id, E
   for (int b = tid; b < NB; b += kSortThreads) cnt[b] = 0;
+  if constexpr (WAVE_COUNTS)
+    for (int b = tid; b < kSortWaves * NB; b += kSortThreads) wc[b] = 0;
   __syncthreads();
-  for (int64_t i = tid; i < n; i += kSortThreads) {
-    const uint32_t v = flat[i];
-    atomicAdd(&cnt[v < (uint32_t)E ? v : (uint32_t)E], 1u);
+  // 8 loads in flight per thread before the first atomic
+  for (int64_t i0 = tid; i0 < n; i0 += 8 * kSortThreads) {
+    uint32_t v[8];
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const int64_t i = i0 + (int64_t)p * kSortThreads;
+      v[p] = i < n ? flat[i] : 0xFFFFFFFFu;
+    }
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+      if (i0 + (int64_t)p * kSortThreads < n)
+        atomicAdd(&cnt[v[p] < (uint32_t)E ? v[p] : (uint32_t)E], 1u);
   }
   __syncthreads();
   // Exclusive scan of cnt: each thread owns a contiguous run of buckets.
@@ -155,25 +176,15 @@ __global__ void __launch_bounds__(kSortThreads) sort_dispatch_kernel(
   const int b0 = min(tid * per, NB), b1 = min(b0 + per, NB);
   uint32_t local = 0;
   for (int b = b0; b < b1; ++b) local += cnt[b];
-  // Block exclusive scan of `local`: inclusive scan within each wave, then the waves'
-  // totals (16) scanned by the first wave.
-  uint32_t incl = local;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t o = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += o;
-  }
+  // Block exclusive scan of `local`: DPP scan within each wave, then the 16 wave totals
+  // scanned by the first wave.
+  const uint32_t incl = (uint32_t)wave_scan_incl_i32<false>((int)local);
   if (lane == 63) part[wave] = incl;
   __syncthreads();
   if (wave == 0) {
-    uint32_t wt = lane < kSortThreads / 64 ? part[lane] : 0u;
-    uint32_t wi = wt;
-#pragma unroll
-    for (int d = 1; d < 16; d <<= 1) {
-      const uint32_t o = __shfl_up(wi, d, 64);
-      if (lane >= d) wi += o;
-    }
-    if (lane < kSortThreads / 64) part[kSortThreads / 64 + lane] = wi - wt;  // exclusive
+    const uint32_t wt = lane < kSortWaves ? part[lane] : 0u;
+    const uint32_t wi = (uint32_t)wave_scan_incl_i32<false>((int)wt);
+    if (lane < kSortWaves) part[kSortWaves + lane] = wi - wt;  // exclusive
   }
   __syncthreads();
   uint32_t run = part[kSortThreads / 64 + wave] + incl - local;
@@ -185,23 +196,44 @@ __global__ void __launch_bounds__(kSortThreads) sort_dispatch_kernel(
   }
   __syncthreads();
   // Stable scatter, 1024 ids at a time; waves of a chunk take their turn in order.
+  // the next chunk's id is loaded while this chunk is scattered
+  uint32_t next = tid < n ? flat[tid] : 0u;
   for (int64_t base = 0; base < n; base += kSortThreads) {
     const int64_t i = base + tid;
     const bool valid = i < n;
-    const uint32_t raw = valid ? flat[i] : 0u;
+    const uint32_t raw = valid ? next : 0u;
+    next = i + kSortThreads < n ? flat[i + kSortThreads] : 0u;
     const uint32_t b = valid ? (raw < (uint32_t)E ? raw : (uint32_t)E) : 0xFFFFFFFFu;
-    // Lanes of this wave holding the same bucket.
-    uint64_t remaining = __ballot(1);
-    uint64_t peers = 0;
-    while (remaining) {
-      const int leader = __ffsll((unsigned long long)remaining) - 1;
-      const uint32_t lb = __shfl(b, leader, 64);
-      const uint64_t m = __ballot(b == lb);
-      if (b == lb) peers = m;
-      remaining &= ~m;
+    // Lanes of this wave holding the same bucket: one ballot per bit of the bucket id,
+    // each lane keeping the lanes that agree with it on every bit (invalid lanes removed).
+    uint64_t peers = __ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool one = (b >> bit) & 1u;
+      const uint64_t m = __ballot(one);
+      peers &= one ? m : ~m;
     }
     const int rank = __popcll(peers & ((1ull << lane) - 1ull));
     const bool lead = rank == 0;
+    if constexpr (WAVE_COUNTS) {
+      const uint32_t nb = (uint32_t)__popcll(peers);
+      if (valid && lead) wc[wave * NB + b] = (uint16_t)nb;
+      __syncthreads();
+      if (valid) {
+        uint32_t pos = cnt[b] + (uint32_t)rank;
+        for (int w = 0; w < wave; ++w) pos += wc[w * NB + b];
+        order[pos] = (uint32_t)i;
+        sorted[pos] = raw;
+        lhs[pos] = (uint32_t)i / (uint32_t)k;
+        inv[i] = pos;
+      }
+      __syncthreads();  // every read of cnt / wc for this chunk is done
+      if (valid && lead) {
+        atomicAdd(&cnt[b], nb);
+        wc[wave * NB + b] = 0;
+      }
+      __syncthreads();
+      continue;
+    }
     for (int w = 0; w < kSortThreads / 64; ++w) {
       if (wave == w && valid) {
         const uint32_t start = cnt[b];
@@ -241,6 +273,23 @@ __global__ void take_rows_kernel(void* __restrict__ out, const void* __restrict_
   }
 }
 
+// 8 values per thread with 16-byte loads and stores (n % 8 == 0, 16-byte aligned).
+__global__ void swiglu8_kernel(u32x4_t* __restrict__ y, const u32x4_t* __restrict__ g,
+                               const u32x4_t* __restrict__ u, int64_t n8) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const u32x4_t gv = g[i], uv = u[i];
+    u32x4_t o;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t lo = swiglu_bf16((uint16_t)(gv[c] & 0xFFFFu), (uint16_t)(uv[c] & 0xFFFFu));
+      const uint32_t hi = swiglu_bf16((uint16_t)(gv[c] >> 16), (uint16_t)(uv[c] >> 16));
+      o[c] = lo | (hi << 16);
+    }
+    y[i] = o;
+  }
+}
+
 __global__ void swiglu_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ g,
                               const uint16_t* __restrict__ u, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -264,6 +313,29 @@ __global__ void down_reduce_kernel(uint16_t* __restrict__ y, const uint16_t* __r
       total = bf16_add(total, bf16_mul(v[p * N + n], scores[p]));
     }
     y[t * N + n] = total;
+  }
+}
+
+// 8 outputs per thread with 16-byte loads (N % 8 == 0, 16-byte aligned rows).
+__global__ void down_reduce8_kernel(u32x4_t* __restrict__ y, const u32x4_t* __restrict__ v,
+                                    const uint16_t* __restrict__ scores, int64_t T, int k,
+                                    int64_t N8) {
+  const int64_t t = blockIdx.y;
+  for (int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; n < N8;
+       n += (int64_t)gridDim.x * blockDim.x) {
+    u32x4_t total = {0u, 0u, 0u, 0u};
+    for (int s = 0; s < k; ++s) {
+      const int64_t p = t * k + s;
+      const u32x4_t x = v[p * N8 + n];
+      const uint16_t sc = scores[p];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t lo = bf16_add((uint16_t)(total[c] & 0xFFFFu), bf16_mul((uint16_t)(x[c] & 0xFFFFu), sc));
+        const uint32_t hi = bf16_add((uint16_t)(total[c] >> 16), bf16_mul((uint16_t)(x[c] >> 16), sc));
+        total[c] = lo | (hi << 16);
+      }
+    }
+    y[t * N8 + n] = total;
   }
 }
 
@@ -291,13 +363,26 @@ hipError_t launch_route_topk(const float* logits, int64_t T, int E, int k, uint3
   return hipGetLastError();
 }
 
-size_t sort_dispatch_lds_bytes(int E) { return ((size_t)E + 1 + kSortThreads) * 4; }
+size_t sort_dispatch_lds_bytes(int E) {
+  const size_t base = ((size_t)E + 1 + kSortThreads) * 4;
+  return E <= kSortMaxWaveCountE ? base + (size_t)kSortWaves * (E + 1) * 2 : base;
+}
 
 hipError_t launch_sort_dispatch(const uint32_t* flat, int64_t n, int k, int E, uint32_t* order,
                                 uint32_t* inv, uint32_t* sorted, uint32_t* lhs, uint32_t* seg,
                                 hipStream_t s) {
-  hipLaunchKernelGGL(sort_dispatch_kernel, dim3(1), dim3(kSortThreads),
-                     sort_dispatch_lds_bytes(E), s, flat, n, k, E, order, inv, sorted, lhs, seg);
+  const size_t lds = sort_dispatch_lds_bytes(E);
+  if (E <= kSortMaxWaveCountE) {
+    static const bool attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&sort_dispatch_kernel<true>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    (void)attr;  // a failure shows as a launch error for tables above 64 KiB
+    hipLaunchKernelGGL(sort_dispatch_kernel<true>, dim3(1), dim3(kSortThreads), lds, s, flat, n,
+                       k, E, order, inv, sorted, lhs, seg);
+  } else {
+    hipLaunchKernelGGL(sort_dispatch_kernel<false>, dim3(1), dim3(kSortThreads), lds, s, flat, n,
+                       k, E, order, inv, sorted, lhs, seg);
+  }
   return hipGetLastError();
 }
 
@@ -313,6 +398,11 @@ hipError_t launch_take_rows(void* out, const void* in, const uint32_t* idx, int6
 hipError_t launch_swiglu(uint16_t* y, const uint16_t* g, const uint16_t* u, int64_t n,
                          hipStream_t s) {
   if (n == 0) return hipSuccess;
+  if (n % 8 == 0 && ((uintptr_t)y | (uintptr_t)g | (uintptr_t)u) % 16 == 0) {
+    hipLaunchKernelGGL(swiglu8_kernel, dim3(grid_for(n / 8, 256)), dim3(256), 0, s, (u32x4_t*)y,
+                       (const u32x4_t*)g, (const u32x4_t*)u, n / 8);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, y, g, u, n);
   return hipGetLastError();
 }
@@ -320,6 +410,11 @@ hipError_t launch_swiglu(uint16_t* y, const uint16_t* g, const uint16_t* u, int6
 hipError_t launch_down_reduce(uint16_t* y, const uint16_t* v, const uint16_t* scores, int64_t T,
                               int k, int64_t N, hipStream_t s) {
   if (T == 0 || N == 0) return hipSuccess;
+  if (N % 8 == 0 && ((uintptr_t)y | (uintptr_t)v) % 16 == 0) {
+    hipLaunchKernelGGL(down_reduce8_kernel, dim3(grid_for(N / 8, 256), (unsigned)T), dim3(256), 0,
+                       s, (u32x4_t*)y, (const u32x4_t*)v, scores, T, k, N / 8);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(down_reduce_kernel, dim3(grid_for(N, 256), (unsigned)T), dim3(256), 0, s, y,
                      v, scores, T, k, N);
   return hipGetLastError();

@@ -179,32 +179,24 @@ __global__ void randn_kernel(void* out, int64_t n, uint64_t seed, float mean, fl
 // positions: ceil((o+1)M/R) - ceil(oM/R) with o = j - a.
 constexpr int kBT = 1024;
 
+// Inclusive block scan of 32-bit ints: DPP scans inside each wave, the 16 wave totals
+// scanned by the first wave the same way.
 template <bool MAX>
-__device__ int64_t block_scan_incl(int64_t v, int64_t* sh) {
+__device__ int block_scan_incl(int v, int* sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   constexpr int NW = kBT / 64;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int64_t o = __shfl_up(v, d, 64);
-    if (lane >= d) v = MAX ? (o > v ? o : v) : v + o;
-  }
+  constexpr int id = MAX ? INT32_MIN : 0;
+  v = wave_scan_incl_i32<MAX>(v);
   if (lane == 63) sh[wave] = v;
   __syncthreads();
-  if (wave == 0) {  // exclusive scan of the wave totals, by shuffles in the first wave
-    const int64_t id = MAX ? INT64_MIN : 0;
-    const int64_t t = lane < NW ? sh[lane] : id;
-    int64_t w = t;
-#pragma unroll
-    for (int d = 1; d < NW; d <<= 1) {
-      const int64_t o = __shfl_up(w, d, 64);
-      if (lane >= d) w = MAX ? (o > w ? o : w) : w + o;
-    }
-    const int64_t prev = __shfl_up(w, 1, 64);  // inclusive value of the lane before
-    if (lane < NW) sh[NW + lane] = MAX ? (lane ? prev : id) : w - t;
+  if (wave == 0) {
+    const int t = lane < NW ? sh[lane] : id;
+    const int w = wave_scan_incl_i32<MAX>(t);
+    if (lane < NW) sh[NW + lane] = w;  // inclusive totals through wave `lane`
   }
   __syncthreads();
   if (wave > 0) {
-    const int64_t p = sh[NW + wave];
+    const int p = sh[NW + wave - 1];
     v = MAX ? (p > v ? p : v) : v + p;
   }
   __syncthreads();
@@ -216,35 +208,40 @@ __global__ void __launch_bounds__(kBT) build_items_kernel(const uint32_t* __rest
                                                           uint32_t* __restrict__ items,
                                                           uint32_t* __restrict__ count,
                                                           int64_t max_items) {
-  __shared__ int64_t sh[2 * (kBT / 64)];
-  __shared__ int64_t carry_a, carry_n;
+  __shared__ int sh[2 * (kBT / 64)];
+  __shared__ int carry_a, carry_n;
   if (threadIdx.x == 0) { carry_a = 0; carry_n = 0; }
   __syncthreads();
   const int64_t total = n_pairs * M;
-  for (int64_t t0 = 0; t0 < n_pairs; t0 += kBT) {
-    const int64_t j = t0 + threadIdx.x;
+  // rhs[j] and rhs[j-1] of the next chunk are loaded while this chunk is processed, so
+  // only the first chunk waits for memory.
+  int64_t j = threadIdx.x;
+  uint32_t cur = j < n_pairs ? rhs[j] : 0u, prv = j > 0 && j < n_pairs ? rhs[j - 1] : 0u;
+  for (int64_t t0 = 0; t0 < n_pairs; t0 += kBT, j += kBT) {
+    const int64_t jn = j + kBT;
+    const uint32_t ncur = jn < n_pairs ? rhs[jn] : 0u, nprv = jn < n_pairs ? rhs[jn - 1] : 0u;
     const bool in = j < n_pairs;
-    const bool start = in && (j == 0 || rhs[j] != rhs[j - 1]);
-    int64_t a = block_scan_incl<true>(start ? j : -1, sh);
-    const int64_t ca = carry_a;
+    const bool start = in && (j == 0 || cur != prv);
+    int a = block_scan_incl<true>(start ? (int)j : -1, sh);
+    const int ca = carry_a;
     if (a < ca) a = ca;
-    int64_t c = 0;
+    int c = 0;
     const int rs = __builtin_ctz((unsigned)R);  // rows per item: a power of two
     if (in) {
       const int64_t o = j - a;
-      c = (((o + 1) * M + R - 1) >> rs) - ((o * M + R - 1) >> rs);
+      c = (int)((((o + 1) * M + R - 1) >> rs) - ((o * M + R - 1) >> rs));
     }
-    const int64_t incl = block_scan_incl<false>(c, sh);
-    const int64_t off = carry_n + incl - c;
+    const int incl = block_scan_incl<false>(c, sh);
+    const int64_t off = (int64_t)carry_n + incl - c;
     if (in) {
       const int64_t o = j - a;
       int64_t first = (o * M + R - 1) >> rs;
-      for (int64_t t = 0; t < c; ++t) {
+      for (int t = 0; t < c; ++t) {
         const int64_t idx = off + t;
         if (idx < max_items) {
           const int64_t pos0 = a * M + (first + t) * R;
           const int64_t lim = total - pos0 < R ? total - pos0 : R;
-          items[4 * idx + 0] = rhs[j];
+          items[4 * idx + 0] = cur;
           items[4 * idx + 1] = (uint32_t)pos0;
           items[4 * idx + 2] = (uint32_t)lim;
           items[4 * idx + 3] = 0u;
@@ -254,9 +251,11 @@ __global__ void __launch_bounds__(kBT) build_items_kernel(const uint32_t* __rest
     __syncthreads();
     if (threadIdx.x == kBT - 1) {
       carry_a = a;
-      carry_n = off + c;
+      carry_n = (int)(off + c);
     }
     __syncthreads();
+    cur = ncur;
+    prv = nprv;
   }
   if (threadIdx.x == 0) {
     const int64_t n = carry_n < max_items ? carry_n : max_items;
@@ -320,6 +319,8 @@ hipError_t launch_randn(void* out, int64_t n, uint64_t seed, float mean, float s
 hipError_t launch_build_items(const uint32_t* rhs, int64_t n_pairs, int M, int rows_per_item,
                               uint32_t* items, uint32_t* item_count, int64_t max_items,
                               hipStream_t s) {
+  // the block scans run on 32-bit ints: pair indices and item counts stay below 2^31
+  if (n_pairs * (int64_t)M >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(build_items_kernel, dim3(1), dim3(kBT), 0, s, rhs, n_pairs, M, rows_per_item,
                      items, item_count, max_items);
   return hipGetLastError();

@@ -41,7 +41,8 @@ def test_route_topk(dev, T, E, k):
 
 @pytest.mark.parametrize("n,E,k,skew", [(1, 128, 1, False), (8, 128, 8, False),
                                         (1000, 128, 8, False), (4096, 128, 8, True),
-                                        (5000, 256, 8, True), (512, 8192, 4, False)])
+                                        (5000, 256, 8, True), (512, 8192, 4, False),
+                                        (20000, 4000, 8, True), (3000, 4001, 2, False)])
 def test_sort_dispatch(dev, n, E, k, skew):
     _print_case(t="sort", n=n, E=E, k=k, skew=skew)
     rng = np.random.default_rng(n + E)
@@ -92,11 +93,16 @@ def test_swiglu_exhaustive(dev):
     u = O.f32_to_bf16(np.random.default_rng(2).standard_normal(g.size).astype(np.float32))
     y = mi_qmm.swiglu(to_dev_bf16(g, dev), to_dev_bf16(u, dev))
     assert np.array_equal(bf16_bits(y), O.swiglu_bf16(g, u))
+    # a length divisible by 8 takes the 16-byte vector kernel
+    g8, u8 = g[: g.size // 8 * 8], u[: g.size // 8 * 8]
+    y8 = mi_qmm.swiglu(to_dev_bf16(g8, dev), to_dev_bf16(u8, dev))
+    assert np.array_equal(bf16_bits(y8), O.swiglu_bf16(g8, u8))
 
 
-def test_down_reduce_bit_exact(dev):
-    _print_case(t="down_reduce")
-    T, k, N = 6, 8, 2048
+@pytest.mark.parametrize("N", [2048, 2044])
+def test_down_reduce_bit_exact(dev, N):
+    _print_case(t="down_reduce", N=N)
+    T, k = 6, 8
     rng = np.random.default_rng(3)
     v = O.f32_to_bf16(rng.standard_normal((T, k, N)).astype(np.float32))
     sc = O.f32_to_bf16(rng.random((T, k)).astype(np.float32))
