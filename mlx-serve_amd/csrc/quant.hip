@@ -203,59 +203,81 @@ __device__ int block_scan_incl(int v, int* sh) {
   return v;
 }
 
+constexpr int kBPT = 4;  // pairs per thread per pass
+
 __global__ void __launch_bounds__(kBT) build_items_kernel(const uint32_t* __restrict__ rhs,
                                                           int64_t n_pairs, int M, int R,
                                                           uint32_t* __restrict__ items,
                                                           uint32_t* __restrict__ count,
                                                           int64_t max_items) {
   __shared__ int sh[2 * (kBT / 64)];
+  __shared__ int prev_a[kBT];
   __shared__ int carry_a, carry_n;
   if (threadIdx.x == 0) { carry_a = 0; carry_n = 0; }
   __syncthreads();
   const int64_t total = n_pairs * M;
-  // rhs[j] and rhs[j-1] of the next chunk are loaded while this chunk is processed, so
-  // only the first chunk waits for memory.
-  int64_t j = threadIdx.x;
-  uint32_t cur = j < n_pairs ? rhs[j] : 0u, prv = j > 0 && j < n_pairs ? rhs[j - 1] : 0u;
-  for (int64_t t0 = 0; t0 < n_pairs; t0 += kBT, j += kBT) {
-    const int64_t jn = j + kBT;
-    const uint32_t ncur = jn < n_pairs ? rhs[jn] : 0u, nprv = jn < n_pairs ? rhs[jn - 1] : 0u;
-    const bool in = j < n_pairs;
-    const bool start = in && (j == 0 || cur != prv);
-    int a = block_scan_incl<true>(start ? (int)j : -1, sh);
-    const int ca = carry_a;
-    if (a < ca) a = ca;
-    int c = 0;
-    const int rs = __builtin_ctz((unsigned)R);  // rows per item: a power of two
-    if (in) {
-      const int64_t o = j - a;
-      c = (int)((((o + 1) * M + R - 1) >> rs) - ((o * M + R - 1) >> rs));
+  const int rs = __builtin_ctz((unsigned)R);  // rows per item: a power of two
+  // Each pass covers kBT * kBPT pairs; thread t owns pairs j0 .. j0 + kBPT - 1.
+  for (int64_t base = 0; base < n_pairs; base += (int64_t)kBT * kBPT) {
+    const int64_t j0 = base + (int64_t)threadIdx.x * kBPT;
+    uint32_t cur[kBPT];
+#pragma unroll
+    for (int q = 0; q < kBPT; ++q) cur[q] = j0 + q < n_pairs ? rhs[j0 + q] : 0u;
+    const uint32_t prv0 = j0 > 0 && j0 < n_pairs ? rhs[j0 - 1] : 0u;
+    // run start of each owned pair, as far as this thread can see (-1: an earlier thread's)
+    int amine[kBPT];
+    int la = -1;
+#pragma unroll
+    for (int q = 0; q < kBPT; ++q) {
+      const int64_t j = j0 + q;
+      const bool start = j < n_pairs && (j == 0 || cur[q] != (q ? cur[q - 1] : prv0));
+      if (start) la = (int)j;
+      amine[q] = la;
     }
-    const int incl = block_scan_incl<false>(c, sh);
-    const int64_t off = (int64_t)carry_n + incl - c;
-    if (in) {
-      const int64_t o = j - a;
-      int64_t first = (o * M + R - 1) >> rs;
-      for (int t = 0; t < c; ++t) {
+    const int incl_a = block_scan_incl<true>(la, sh);
+    prev_a[threadIdx.x] = incl_a;
+    __syncthreads();
+    int excl_a = threadIdx.x ? prev_a[threadIdx.x - 1] : -1;
+    const int ca = carry_a;
+    if (excl_a < ca) excl_a = ca;
+    int a[kBPT], c[kBPT];
+    int csum = 0;
+#pragma unroll
+    for (int q = 0; q < kBPT; ++q) {
+      const int64_t j = j0 + q;
+      a[q] = amine[q] >= 0 ? amine[q] : excl_a;
+      c[q] = 0;
+      if (j < n_pairs) {
+        const int64_t o = j - a[q];
+        c[q] = (int)((((o + 1) * M + R - 1) >> rs) - ((o * M + R - 1) >> rs));
+      }
+      csum += c[q];
+    }
+    const int incl = block_scan_incl<false>(csum, sh);
+    int64_t off = (int64_t)carry_n + incl - csum;
+#pragma unroll
+    for (int q = 0; q < kBPT; ++q) {
+      const int64_t o = j0 + q - a[q];
+      const int64_t first = (o * M + R - 1) >> rs;
+      for (int t = 0; t < c[q]; ++t) {
         const int64_t idx = off + t;
         if (idx < max_items) {
-          const int64_t pos0 = a * M + (first + t) * R;
+          const int64_t pos0 = (int64_t)a[q] * M + (first + t) * R;
           const int64_t lim = total - pos0 < R ? total - pos0 : R;
-          items[4 * idx + 0] = cur;
+          items[4 * idx + 0] = cur[q];
           items[4 * idx + 1] = (uint32_t)pos0;
           items[4 * idx + 2] = (uint32_t)lim;
           items[4 * idx + 3] = 0u;
         }
       }
+      off += c[q];
     }
     __syncthreads();
     if (threadIdx.x == kBT - 1) {
-      carry_a = a;
-      carry_n = (int)(off + c);
+      carry_a = incl_a > ca ? incl_a : ca;
+      carry_n = (int)off;
     }
     __syncthreads();
-    cur = ncur;
-    prv = nprv;
   }
   if (threadIdx.x == 0) {
     const int64_t n = carry_n < max_items ? carry_n : max_items;

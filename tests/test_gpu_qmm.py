@@ -132,11 +132,13 @@ def test_gather_decode_broadcast(dev):
                                           (1, 1024, 8, 40, 3), (2, 2048, 8, 40, 3),
                                           (1, 512, 64, 20, 2), (1, 512, 40, 30, 2),
                                           (1, 1024, 32, 40, 3), (2, 512, 16, 24, 2),
-                                          (1, 512, 4, 64, 4), (1, 8192, 4, 64, 4)])
+                                          (1, 512, 4, 64, 4), (1, 8192, 4, 64, 4),
+                                          (1, 256, 16, 3000, 4), (2, 256, 300, 2600, 2)])
 def test_gather_sorted_matches_unsorted(dev, M, K, E, T, topk):
     """Sorted (grouped) path and unsorted path both match truth; the shapes cover work
     items of 1 row (one-row kernel), 2..32 rows (few-row MFMA kernel, K split across
-    blocks for K=8192) and the older 16/32-row-tile kernels."""
+    blocks for K=8192) and the older 16/32-row-tile kernels; 12000 and 5200 pairs take
+    several passes of the work-item builder."""
     _print_case(t="gather_sorted", M=M, K=K, E=E, T=T, topk=topk)
     N = 64
     wq, s, b = weights(E, N, K, 4, 64, 77)
