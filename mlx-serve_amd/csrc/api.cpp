@@ -265,6 +265,8 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
     int64_t avg = (PT + runs - 1) / runs;
     if (item_rows > 0) avg = item_rows;
     J.narrow = q16 && avg <= 4;
+    // (64-row items on the two-pass few-row kernel measured slower than 32-row items
+    // that re-read a long run's expert: they need a K split at K = 2048)
     P.rpi = avg <= 1 ? 1 : avg <= 2 ? 2 : avg <= 4 ? 4 : avg <= 8 ? 8 : avg <= 16 ? 16 : 32;
     if (!J.narrow && P.rpi < 8) P.rpi = 8;
   } else {
@@ -430,6 +432,23 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
       return fail(MI_ERR_HIP, "hipBLASLt GEMM: %s", err ? err : "error");
     return MI_OK;
   }
+  // 2..64 rows: the few-row MFMA kernel (33..64 rows as two 32-row passes per block)
+  static const int use_qmvm = env_int("MI_QMM_QMVM", 1);
+  static const int qmvm_max = env_int("MI_QMM_QMVM_MAX", 64);
+  mi::QmvmPlan qp{};
+  if (use_qmvm && x_dtype == MI_DTYPE_BFLOAT16 && M >= 2 && M <= qmvm_max &&
+      mi::qmvm_plan((int)M, (int)N, (int)K, gs, nb, 1, &qp)) {
+    mi::QmvmParams Q{x, w, (const uint16_t*)scales, (const uint16_t*)biases, (uint16_t*)y,
+                     nullptr, (int)M, (int)N, (int)K, gs, qp.kr, qp.wr};
+    if (qp.part_bytes) {
+      void* data = nullptr;
+      rc = workspace(s, qp.part_bytes, &data);
+      if (rc) return rc;
+      Q.part = (float*)data;
+    }
+    hipError_t e = mi::launch_qmvm(Q, qp, s);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "qmvm launch");
+  }
   if (x_dtype == MI_DTYPE_BFLOAT16 && M > 32 && mi::qmm_supported((int)M, (int)N, (int)K, nb, gs)) {
     mi::QmmParams Q{w, (const uint16_t*)scales, (const uint16_t*)biases, (const uint16_t*)x,
                     (uint16_t*)y, (int)M, (int)N, (int)K, nb, gs, nullptr, 1, 0, 0};
@@ -442,21 +461,6 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
     }
     hipError_t e = mi::launch_qmm(Q, s);
     return e == hipSuccess ? MI_OK : hip_fail(e, "qmm launch");
-  }
-  static const int use_qmvm = env_int("MI_QMM_QMVM", 1);
-  mi::QmvmPlan qp{};
-  if (use_qmvm && x_dtype == MI_DTYPE_BFLOAT16 && M >= 2 && M <= 32 &&
-      mi::qmvm_plan((int)M, (int)N, (int)K, gs, nb, 1, &qp)) {
-    mi::QmvmParams Q{x, w, (const uint16_t*)scales, (const uint16_t*)biases, (uint16_t*)y,
-                     nullptr, (int)M, (int)N, (int)K, gs, qp.kr, qp.wr};
-    if (qp.part_bytes) {
-      void* data = nullptr;
-      rc = workspace(s, qp.part_bytes, &data);
-      if (rc) return rc;
-      Q.part = (float*)data;
-    }
-    hipError_t e = mi::launch_qmvm(Q, qp, s);
-    return e == hipSuccess ? MI_OK : hip_fail(e, "qmvm launch");
   }
   // Dense = gather with a single pair on expert 0; M rows ride in one x batch.
   return mi_gather_qmm(y, x, w, scales, biases, nullptr, nullptr, 1, 1, 1, M, N, K, 1, transpose,

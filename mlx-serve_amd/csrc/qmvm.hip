@@ -27,6 +27,10 @@ extern template void launch_family<8, 16, false, false>(const QmvmParams&, const
                                                      const QmvmPlan&, dim3, hipStream_t);
 extern template void launch_family<8, 32, false, false>(const QmvmParams&, const QmvParams&,
                                                      const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 64, false, false>(const QmvmParams&, const QmvParams&,
+                                                     const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<8, 64, false, false>(const QmvmParams&, const QmvParams&,
+                                                     const QmvmPlan&, dim3, hipStream_t);
 }  // namespace qmvm_detail
 
 namespace {
@@ -62,19 +66,21 @@ void launch_any(QmvmParams P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
     if constexpr (!GATHER) {  // 8-bit instances are dense only
       if (pl.mt == 16 && pl.sbf32) launch_family<8, 16, true, false>(P, G, pl, grid, s);
       else if (pl.mt == 16) launch_family<8, 16, false, false>(P, G, pl, grid, s);
-      else launch_family<8, 32, false, false>(P, G, pl, grid, s);
+      else if (pl.mt == 32) launch_family<8, 32, false, false>(P, G, pl, grid, s);
+      else launch_family<8, 64, false, false>(P, G, pl, grid, s);
     }
     return;
   }
   if (pl.mt == 16 && pl.sbf32) launch_family<4, 16, true, GATHER>(P, G, pl, grid, s);
   else if (pl.mt == 16) launch_family<4, 16, false, GATHER>(P, G, pl, grid, s);
-  else launch_family<4, 32, false, GATHER>(P, G, pl, grid, s);
+  else if (pl.mt == 32) launch_family<4, 32, false, GATHER>(P, G, pl, grid, s);
+  else if constexpr (!GATHER) launch_family<4, 64, false, false>(P, G, pl, grid, s);
 }
 
 }  // namespace
 
 bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan* out) {
-  if ((bits != 4 && bits != 8) || M < 2 || M > 32) return false;
+  if ((bits != 4 && bits != 8) || M < 2 || M > 64) return false;
   const int cv = 512 / bits;  // values per 64-byte chunk of a row
   if (K % cv != 0) return false;
   if (gs != 64) return false;  // the other group sizes take the general decode kernels
@@ -83,7 +89,8 @@ bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan*
   static const int env_wr = env_or("MI_QMVM_WR", 0);
   static const int env_target = env_or("MI_QMVM_TARGET", 0);
   static const int env_depth = env_or("MI_QMVM_DEPTH", 0);
-  const int mt = M <= 16 ? 16 : 32;
+  const int mt = M <= 16 ? 16 : M <= 32 ? 32 : 64;
+  const int mp = M < 32 ? M : 32;  // rows staged at once (64-row plans stage two passes)
   const size_t lds_max = 160 * 1024 - 512;  // the kernel's static row table
   const int nch = K / cv;
   const int target = env_target ? env_target : 8;
@@ -93,7 +100,8 @@ bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan*
   // fewest K ranges (each range beyond one writes fp32 partials and needs the reduce
   // launch); then chunks per wave near `target` and more waves. Scale/bias pairs are
   // staged as fp32 (s, b - 128 s) when LDS allows, else as bf16 pairs.
-  const int wr0 = env_wr ? env_wr : M <= 2 ? 1 : M <= 16 ? 4 : 8;
+  // 64-row plans: 4 tiles, so 8 waves still cover a K range of 2048 in one block
+  const int wr0 = env_wr ? env_wr : M <= 2 ? 1 : M <= 16 ? 4 : M <= 32 ? 8 : 4;
   QmvmPlan best{};
   double best_cost = 1e30;
   for (int wr = wr0; wr >= 1 && !best.nc; wr >>= 1) {
@@ -103,15 +111,16 @@ bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan*
       const int chs = nch / ks;  // chunks per range
       const int nvals = chs * cv;
       if (gs <= 64 && (nvals / gs) % 2) continue;  // scale/bias pairs: an even group count
-      for (int wk = 1; wk * wr <= 16; ++wk) {
+      const int max_waves = mt == 64 ? 8 : 16;  // the 64-row instances' launch bound
+      for (int wk = 1; wk * wr <= max_waves; ++wk) {
         if (chs % wk) continue;
         const int nc = chs / wk;
         if (nc > 8) continue;
         const int waves = wk * wr;
         for (int f32 = mt == 16 ? 1 : 0; f32 >= 0; --f32) {
-          const qmvm_detail::QmvmLds L = qmvm_detail::qmvm_lds(M, nvals, gs, 16 * wr, waves, mt, f32 != 0);
+          const qmvm_detail::QmvmLds L = qmvm_detail::qmvm_lds(mp, nvals, gs, 16 * wr, waves, mt, f32 != 0);
           if ((size_t)L.total() > lds_max) continue;
-          const int units = M * nvals / 8;
+          const int units = mp * nvals / 8;
           const int xu = (units + 64 * waves - 1) / (64 * waves);
           if (xu > 8) continue;
           const int gr = nvals / gs;
@@ -168,6 +177,7 @@ hipError_t launch_qmvm(const QmvmParams& P, const QmvmPlan& pl, hipStream_t s) {
 }
 
 hipError_t launch_qmvm_gather(const QmvParams& G, const QmvmPlan& pl, int grid_z, hipStream_t s) {
+  if (pl.mt > 32) return hipErrorInvalidValue;  // gather items hold at most 32 rows
   QmvmParams P{G.x, G.w, G.scales, G.biases, (uint16_t*)G.y, G.part, pl.rows, G.N, G.K,
                G.group_size, pl.kr, pl.wr, 0, 0};
   launch_any<true>(P, G, pl, dim3((unsigned)pl.tiles, (unsigned)pl.ks, (unsigned)grid_z), s);

@@ -1,6 +1,6 @@
 // Few-row decode GEMM, 4- or 8-bit affine gs 64, bf16 activations, on the 16x16x32 bf16 MFMA:
-// dense quantized_matmul (2 <= M <= 32) and gather_qmm work items of 2..32 rows (sorted
-// expert runs). The weights stream straight into registers the way the one-row kernel
+// dense quantized_matmul (2 <= M <= 64; above 32 rows in two 32-row passes over the
+// weights held in registers) and gather_qmm work items of 2..32 rows (sorted expert runs). The weights stream straight into registers the way the one-row kernel
 // streams them (no LDS copy of the weights).
 //
 // Block = WR weight tiles of 16 rows x one K range (x one work item for gathers); its W
@@ -34,6 +34,7 @@
 #include "qmv_common.h"
 
 #include <cstdint>
+#include <type_traits>
 
 namespace mi {
 namespace qmvm_detail {
@@ -50,7 +51,7 @@ typedef __bf16 bf16x2m __attribute__((ext_vector_type(2)));
 constexpr int kChunkVals = 128;
 constexpr int kBufFlags = 0x00020000;  // raw (untyped) dword buffer access on this target
 constexpr uint32_t kOOB = 0x7FFFFFF0u;  // buffer offset past any resource: the load returns 0
-constexpr int kMaxRows = 32;
+constexpr int kMaxRows = 64;
 
 MI_DEV f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8m, a),
@@ -114,16 +115,24 @@ __host__ __device__ inline QmvmLds qmvm_lds(int M, int nvals, int gs, int rows, 
 // G is read only by gathers (work items, index arrays, expert bank); dense calls pass
 // their shapes in P.
 template <int BITS, int GS, int NC, int XU, int DEPTH, int MT, bool SBF32, bool GATHER>
-__global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) {
+// MT 64 keeps four accumulator tiles and the second pass's activations in registers:
+// blocks of up to 8 waves (256 VGPRs per lane) instead of 16.
+__global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams P, QmvParams Gp) {
   constexpr int CV = 512 / BITS;        // values per 64-byte chunk of a row
   constexpr int NSTEP = CV / 32;        // MFMA steps per chunk
   constexpr float BOFF = BITS == 4 ? -128.f : 0.f;  // 4-bit A holds 128 + q
   constexpr int SPG = GS / 32;  // 32-value MFMA steps per group
-  constexpr int D = DEPTH < NC ? DEPTH : NC;
+  // MT 64 loads every chunk up front: its pass loop then issues no loads
+  constexpr int D = MT == 64 ? NC : DEPTH < NC ? DEPTH : NC;
   constexpr int GPC = CV / GS;  // groups per chunk (GS <= CV)
   constexpr int SBW = SBF32 ? 2 : 1;    // LDS words per (group, row)
   constexpr int SU = 4;                 // scale/bias loads per thread
   constexpr bool PAIRS = GS <= 64;      // scale/bias as dwords (two groups) or halves
+  // MT 64: the activation rows are staged 32 at a time (two passes over the wave's
+  // chunks, weights kept in registers), so LDS holds at most 32 rows.
+  constexpr int MP = MT == 64 ? 32 : MT;  // rows per pass
+  constexpr int NPASS = MT / MP;
+  constexpr int NTP = MP / 16;            // 16-column MFMA tiles per pass
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ int64_t rowtab[kMaxRows];  // gathers: element offset of each item row's x
   const int tid = threadIdx.x, BD = blockDim.x, W = BD >> 6;
@@ -159,7 +168,8 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
       pos0 = it.pos0;
       if (wave == 0 && lane < M) rowtab[lane] = item_x_row(Gp, it, lane);  // -1 skip, -2 NaN
     }
-    const QmvmLds L = qmvm_lds(M, nvals, GS, rows, W, MT, SBF32);
+    const int Mp0 = min(M, MP);  // rows of the first pass
+    const QmvmLds L = qmvm_lds(Mp0, nvals, GS, rows, W, MT, SBF32);
     unsigned char* xs = smem;
     float* sb = reinterpret_cast<float*>(smem + L.xbytes);
     float* red = reinterpret_cast<float*>(smem);  // reused after the dot products
@@ -180,22 +190,23 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
     //    before all are issued). Gather: the chunks and scale/bias first, then (after the
     //    row table is visible) the activations.
     u32x4_t xv[XU];
-    auto load_x = [&]() {
+    auto load_x = [&](int pass) __attribute__((always_inline)) {
+      const int mb = pass * MP, Mp = min(M - mb, MP);
 #pragma unroll
       for (int t = 0; t < XU; ++t) {
         const int u = tid + t * BD;
         const int m = (int)__umulhi((uint32_t)u, P.upr_mr), k8 = u - m * upr;
         uint32_t off = kOOB;
         if constexpr (GATHER) {
-          const int64_t ro = m < M ? rowtab[m] : -1;
+          const int64_t ro = m < Mp ? rowtab[mb + m] : -1;
           if (ro >= 0) off = (uint32_t)(ro + kb0 + 8 * k8) * 2;
         } else {
-          if (m < M) off = (uint32_t)(m * K + kb0 + 8 * k8) * 2;
+          if (m < Mp) off = (uint32_t)((mb + m) * K + kb0 + 8 * k8) * 2;
         }
         xv[t] = __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0);
       }
     };
-    if constexpr (!GATHER) load_x();
+    if constexpr (!GATHER) load_x(0);
     uint32_t sv[SU], bv[SU];
 #pragma unroll
     for (int t = 0; t < SU; ++t) {
@@ -221,16 +232,17 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
       wv[j] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * j, 0, 0);
     if constexpr (GATHER) {
       lds_barrier();  // the row table
-      load_x();
+      load_x(0);
     }
 
     // 2. stage activations (pair order) and scale/bias pairs.
+    auto stage_x = [&](int Mp) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < XU; ++t) {
       const int u = tid + t * BD;
       const int m = (int)__umulhi((uint32_t)u, P.upr_mr), k8 = u - m * upr;
       const u32x4_t X = xv[t];
-      if (m < M) {
+      if (m < Mp) {
         u32x4_t p = X;  // 8-bit: natural order
         if constexpr (BITS == 4) {
           p.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
@@ -241,6 +253,8 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
         *reinterpret_cast<u32x4_t*>(xs + m * L.xstride + k8 * 16) = p;
       }
     }
+    };
+    stage_x(Mp0);
 #pragma unroll
     for (int t = 0; t < SU; ++t) {
       const int v = tid + t * BD;
@@ -269,88 +283,115 @@ __global__ void __launch_bounds__(1024) qmvm_kernel(QmvmParams P, QmvParams Gp) 
     }
     lds_barrier();
 
-    // 3. MFMA over the wave's chunks as they land.
-    const int jj = min(i, M - 1);
-    const int jj2 = min(16 + i, M - 1);
+    // 3. MFMA over the wave's chunks as they land (pass 0); pass 1 of MT 64 reuses the
+    //    weights held in registers against the next 32 staged rows.
     // 4-bit: lane block q of step t is values 32t + 8q.. of the chunk (after the
     // transpose); 8-bit: values 16q + 8t.. (two words of the lane's own 16 bytes)
     constexpr int QB = BITS == 4 ? 16 : 32;  // bytes between the lane blocks of a row
-    const unsigned char* xrow = xs + jj * L.xstride + QB * q;
-    const unsigned char* xrow2 = xs + jj2 * L.xstride + QB * q;
-    // per-group pointer, stepped by one group at a time (no multiplies in the loop)
-    const float* sbp = sb + SBW * ((c0 * GPC) * rows + rt * 16 + 4 * q);
     // A operand of ones (bf16 1.0 = 0x3F80): ones x B puts each column's group sum X in
     // every row of C, i.e. in the accumulator layout of the outputs
     const u32x4_t ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4_t acc[NTP];
+    auto mfma_pass = [&](int Mp) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      if constexpr (D < NC) {
-        if (j + D < NC)
-          wv[j + D] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * (j + D), 0, 0);
-      }
-      const u32x4_t tw = BITS == 4 ? xpose4(wv[j]) : wv[j];
-      const int kc = (c0 + j) * CV;  // chunk start within the range
-      f32x4_t c = zero, c2 = zero, cx = zero, cx2 = zero;
+      for (int tt = 0; tt < NTP; ++tt) acc[tt] = zero;
+      const unsigned char* xrow[NTP];
 #pragma unroll
-      for (int t = 0; t < NSTEP; ++t) {
-        u32x4_t a;
-        if constexpr (BITS == 4) {
-          a = unpack8(t == 0 ? tw.x : t == 1 ? tw.y : t == 2 ? tw.z : tw.w);
-        } else {
-          a = t == 0 ? unpack8b(tw.x, tw.y) : unpack8b(tw.z, tw.w);
+      for (int tt = 0; tt < NTP; ++tt) xrow[tt] = xs + min(16 * tt + i, Mp - 1) * L.xstride + QB * q;
+      // per-group pointer, stepped by one group at a time (no multiplies in the loop)
+      const float* sbp = sb + SBW * ((c0 * GPC) * rows + rt * 16 + 4 * q);
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        if constexpr (D < NC) {
+          if (j + D < NC)
+            wv[j + D] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * (j + D), 0, 0);
         }
-        const int kb = (kc + (BITS == 4 ? 32 : 8) * t) * 2;  // byte offset in a staged row
-        const u32x4_t b = *reinterpret_cast<const u32x4_t*>(xrow + kb);
-        c = mfma16(a, b, t % SPG == 0 ? zero : c);
-        cx = mfma16(ones, b, t % SPG == 0 ? zero : cx);
-        if constexpr (MT == 32) {
-          const u32x4_t b2 = *reinterpret_cast<const u32x4_t*>(xrow2 + kb);
-          c2 = mfma16(a, b2, t % SPG == 0 ? zero : c2);
-          cx2 = mfma16(ones, b2, t % SPG == 0 ? zero : cx2);
-        }
-        if (t % SPG == SPG - 1) {
-          f32x4_t sb01, sb23;  // (s, b - 128 s) of rows 4q, 4q+1 and 4q+2, 4q+3
-          if constexpr (SBF32) {
-            sb01 = *reinterpret_cast<const f32x4_t*>(sbp);
-            sb23 = *reinterpret_cast<const f32x4_t*>(sbp + 4);
+        const u32x4_t tw = BITS == 4 ? xpose4(wv[j]) : wv[j];
+        const int kc = (c0 + j) * CV;  // chunk start within the range
+        f32x4_t c[NTP], cx[NTP];
+#pragma unroll
+        for (int tt = 0; tt < NTP; ++tt) c[tt] = cx[tt] = zero;
+#pragma unroll
+        for (int t = 0; t < NSTEP; ++t) {
+          u32x4_t a;
+          if constexpr (BITS == 4) {
+            a = unpack8(t == 0 ? tw.x : t == 1 ? tw.y : t == 2 ? tw.z : tw.w);
           } else {
-            const u32x4_t ev = *reinterpret_cast<const u32x4_t*>(sbp);
-            sb01.x = lo_bf16(ev.x);
-            sb01.y = fmaf(BOFF, sb01.x, hi_bf16(ev.x));
-            sb01.z = lo_bf16(ev.y);
-            sb01.w = fmaf(BOFF, sb01.z, hi_bf16(ev.y));
-            sb23.x = lo_bf16(ev.z);
-            sb23.y = fmaf(BOFF, sb23.x, hi_bf16(ev.z));
-            sb23.z = lo_bf16(ev.w);
-            sb23.w = fmaf(BOFF, sb23.z, hi_bf16(ev.w));
+            a = t == 0 ? unpack8b(tw.x, tw.y) : unpack8b(tw.z, tw.w);
           }
-          sbp += SBW * rows;
-          const float X = cx[0];
-          acc[0] = fmaf(sb01.x, c[0], fmaf(sb01.y, X, acc[0]));
-          acc[1] = fmaf(sb01.z, c[1], fmaf(sb01.w, X, acc[1]));
-          acc[2] = fmaf(sb23.x, c[2], fmaf(sb23.y, X, acc[2]));
-          acc[3] = fmaf(sb23.z, c[3], fmaf(sb23.w, X, acc[3]));
-          if constexpr (MT == 32) {
-            const float X2 = cx2[0];
-            acc2[0] = fmaf(sb01.x, c2[0], fmaf(sb01.y, X2, acc2[0]));
-            acc2[1] = fmaf(sb01.z, c2[1], fmaf(sb01.w, X2, acc2[1]));
-            acc2[2] = fmaf(sb23.x, c2[2], fmaf(sb23.y, X2, acc2[2]));
-            acc2[3] = fmaf(sb23.z, c2[3], fmaf(sb23.w, X2, acc2[3]));
+          const int kb = (kc + (BITS == 4 ? 32 : 8) * t) * 2;  // byte offset in a staged row
+          // every column tile runs (rows past the pass's end repeat its last row and are
+          // never written): no branches inside the unrolled chunk loop
+#pragma unroll
+          for (int tt = 0; tt < NTP; ++tt) {
+            const u32x4_t b = *reinterpret_cast<const u32x4_t*>(xrow[tt] + kb);
+            c[tt] = mfma16(a, b, t % SPG == 0 ? zero : c[tt]);
+            cx[tt] = mfma16(ones, b, t % SPG == 0 ? zero : cx[tt]);
+          }
+          if (t % SPG == SPG - 1) {
+            f32x4_t sb01, sb23;  // (s, b - 128 s) of rows 4q, 4q+1 and 4q+2, 4q+3
+            if constexpr (SBF32) {
+              sb01 = *reinterpret_cast<const f32x4_t*>(sbp);
+              sb23 = *reinterpret_cast<const f32x4_t*>(sbp + 4);
+            } else {
+              const u32x4_t ev = *reinterpret_cast<const u32x4_t*>(sbp);
+              sb01.x = lo_bf16(ev.x);
+              sb01.y = fmaf(BOFF, sb01.x, hi_bf16(ev.x));
+              sb01.z = lo_bf16(ev.y);
+              sb01.w = fmaf(BOFF, sb01.z, hi_bf16(ev.y));
+              sb23.x = lo_bf16(ev.z);
+              sb23.y = fmaf(BOFF, sb23.x, hi_bf16(ev.z));
+              sb23.z = lo_bf16(ev.w);
+              sb23.w = fmaf(BOFF, sb23.z, hi_bf16(ev.w));
+            }
+            sbp += SBW * rows;
+#pragma unroll
+            for (int tt = 0; tt < NTP; ++tt) {
+              f32x4_t& ac = acc[tt];
+              const float X = cx[tt][0];
+              ac[0] = fmaf(sb01.x, c[tt][0], fmaf(sb01.y, X, ac[0]));
+              ac[1] = fmaf(sb01.z, c[tt][1], fmaf(sb01.w, X, ac[1]));
+              ac[2] = fmaf(sb23.x, c[tt][2], fmaf(sb23.y, X, ac[2]));
+              ac[3] = fmaf(sb23.z, c[tt][3], fmaf(sb23.w, X, ac[3]));
+            }
           }
         }
+        if constexpr (D < NC) __builtin_amdgcn_sched_barrier(0);  // keep the issue order
       }
-      if constexpr (D < NC) __builtin_amdgcn_sched_barrier(0);  // keep the issue order
-    }
-
-    // 4. sum the WK waves of each tile in wave order, write y (or the range's partial).
-    lds_barrier();  // LDS reads of step 3 are done: reuse it
+    };
     // red[kp][rt][col][row16] : lane holds rows 4q..4q+3 of column i
+    auto write_red = [&](const f32x4_t* a, int col0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      red[((kp * WR + rt) * MT + i) * 16 + 4 * q + r] = acc[r];
-      if constexpr (MT == 32) red[((kp * WR + rt) * MT + 16 + i) * 16 + 4 * q + r] = acc2[r];
+      for (int tt = 0; tt < NTP; ++tt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          red[((kp * WR + rt) * MT + col0 + 16 * tt + i) * 16 + 4 * q + r] = a[tt][r];
+    };
+    if constexpr (NPASS == 1) {
+      mfma_pass(Mp0);
+      // 4. sum the WK waves of each tile in wave order, write y (or the range's partial).
+      lds_barrier();  // LDS reads of step 3 are done: reuse it
+      write_red(acc, 0);
+    } else {
+      // Two passes of 32 rows over the weights held in registers (a runtime branch, so
+      // the compiler keeps no per-chunk state of the first pass for the second); the
+      // second pass's activations are in flight while the first computes.
+      const bool two = M > MP;  // block-uniform
+      if (two) load_x(1);
+      mfma_pass(Mp0);
+      f32x4_t first[NTP];
+#pragma unroll
+      for (int tt = 0; tt < NTP; ++tt) first[tt] = acc[tt];
+      if (two) {
+        lds_barrier();  // the first pass's reads of the staged rows are done
+        stage_x(M - MP);
+        lds_barrier();
+        mfma_pass(M - MP);
+      }
+      lds_barrier();  // LDS reads of step 3 are done: reuse it
+      write_red(first, 0);
+      if (two) write_red(acc, MP);
     }
     lds_barrier();
     const int WK = W / WR;

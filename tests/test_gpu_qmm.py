@@ -55,7 +55,8 @@ QMM_CASES = [(1, 4096, 512), (1, 100, 1024), (2, 64, 256), (3, 48, 512), (4, 80,
              (5, 32, 384), (8, 64, 512), (16, 64, 256), (17, 40, 256), (32, 96, 512),
              (33, 64, 256), (64, 48, 256), (1, 1024, 4096), (3, 512, 8192), (16, 256, 4096),
              (1, 320, 14336), (5, 48, 2560), (1, 64, 2176), (1, 200, 3200), (1, 8, 256),
-             (32, 256, 8192), (12, 320, 14336), (7, 4096, 1024)]
+             (32, 256, 8192), (12, 320, 14336), (7, 4096, 1024), (48, 320, 8192),
+             (64, 512, 2048), (40, 200, 3200)]
 
 
 @pytest.mark.parametrize("bits", [4, 8])
