@@ -3,6 +3,7 @@
 #include "mi_qmm.h"
 
 #include <algorithm>
+#include <cmath>
 
 #include <hip/hip_runtime.h>
 
@@ -263,6 +264,15 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
   if (J.use_items) {
     const int64_t runs = n_idx < n_experts ? n_idx : n_experts;
     int64_t avg = (PT + runs - 1) / runs;
+    if (item_rows <= 0 && nb == 4 && !P.x_f32) {
+      // Items for the few-row MFMA kernel: size them for the rows a distinct expert gets
+      // under uniform routing, mu = PT / (E (1 - (1 - 1/E)^PT)), plus 3 standard deviations,
+      // so a run is rarely cut (each extra item re-reads the expert). configs[4] T=64: mu 2.3
+      // -> 8-row items, 2.05 -> 1.67 ms; T=8: mu 1.1 stays at one-row items.
+      const double e = (double)n_experts, distinct = e * (1.0 - std::pow(1.0 - 1.0 / e, (double)PT));
+      const double mu = distinct > 0 ? (double)PT / distinct : 1.0;
+      if (mu > 1.3) avg = std::max<int64_t>(avg, (int64_t)std::ceil(mu + 3.0 * std::sqrt(mu)));
+    }
     if (item_rows > 0) avg = item_rows;
     J.narrow = q16 && avg <= 4;
     // (64-row items on the two-pass few-row kernel measured slower than 32-row items
