@@ -85,32 +85,50 @@ void mo_randn_f32(float* out, int64_t n, uint64_t seed, double mean, double stdd
 }
 
 /* ------------------------------------------------------------- packing --- */
-static int valid_bits(int bits) { return bits == 2 || bits == 4 || bits == 8; }
+/* Affine widths MLX packs: 2, 3, 4, 5, 6 and 8 bits. A row of K codes is one LSB-first
+ * bitstream, code j at bit j*bits of the row's little-endian bytes (uint32 words, K*bits a
+ * multiple of 32). For 2/4/8 bits this is "value j of a word = (word >> (j*bits)) & mask"
+ * (src/transformer.zig:20098-20108); 5 bits puts 8 codes in 5 bytes and 6 bits 4 codes in
+ * 3 bytes (src/transformer.zig:516-578, the byte reads of vqmmColumnLoad / vqmmColumnChain). */
+static int valid_bits(int bits) {
+  return bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 8;
+}
+
+static uint32_t get_code(const uint32_t* row, int64_t j, int bits) {
+  const int64_t o = j * bits;
+  const int64_t w = o >> 5;
+  const int sh = (int)(o & 31);
+  uint64_t v = row[w] >> sh;
+  if (sh + bits > 32) v |= (uint64_t)row[w + 1] << (32 - sh);
+  return (uint32_t)(v & ((1u << bits) - 1u));
+}
+
+/* the row's words must start at zero */
+static void put_code(uint32_t* row, int64_t j, int bits, uint32_t code) {
+  const int64_t o = j * bits;
+  const int64_t w = o >> 5;
+  const int sh = (int)(o & 31);
+  code &= (1u << bits) - 1u;
+  row[w] |= code << sh;
+  if (sh + bits > 32) row[w + 1] |= code >> (32 - sh);
+}
 
 int mo_pack(const uint8_t* q, int64_t rows, int64_t K, int bits, uint32_t* wq) {
   if (!valid_bits(bits) || (K * bits) % 32) return -1;
-  int pf = 32 / bits;
-  int64_t wc = K / pf;
-  for (int64_t r = 0; r < rows; ++r)
-    for (int64_t c = 0; c < wc; ++c) {
-      uint32_t word = 0;
-      for (int j = 0; j < pf; ++j)
-        word |= ((uint32_t)q[r * K + c * pf + j] & ((1u << bits) - 1u)) << (j * bits);
-      wq[r * wc + c] = word;
-    }
+  int64_t wc = K * bits / 32;
+  for (int64_t r = 0; r < rows; ++r) {
+    uint32_t* row = wq + r * wc;
+    for (int64_t c = 0; c < wc; ++c) row[c] = 0;
+    for (int64_t j = 0; j < K; ++j) put_code(row, j, bits, q[r * K + j]);
+  }
   return 0;
 }
 
 int mo_unpack(const uint32_t* wq, int64_t rows, int64_t K, int bits, uint8_t* q) {
   if (!valid_bits(bits) || (K * bits) % 32) return -1;
-  int pf = 32 / bits;
-  int64_t wc = K / pf;
-  uint32_t mask = (1u << bits) - 1u;
+  int64_t wc = K * bits / 32;
   for (int64_t r = 0; r < rows; ++r)
-    for (int64_t c = 0; c < wc; ++c) {
-      uint32_t word = wq[r * wc + c];
-      for (int j = 0; j < pf; ++j) q[r * K + c * pf + j] = (uint8_t)((word >> (j * bits)) & mask);
-    }
+    for (int64_t j = 0; j < K; ++j) q[r * K + j] = (uint8_t)get_code(wq + r * wc, j, bits);
   return 0;
 }
 
@@ -128,8 +146,7 @@ int mo_quantize_bf16(const uint16_t* w, int64_t rows, int64_t K, int gs, int bit
   if (!valid_bits(bits) || gs <= 0 || K % gs || (gs * bits) % 32) return -1;
   const float n_bins = (float)((1 << bits) - 1);
   const float eps = 1e-7f;
-  int pf = 32 / bits;
-  int64_t wc = K / pf, ng = K / gs;
+  int64_t wc = K * bits / 32, ng = K / gs;
 #pragma omp parallel for schedule(static)
   for (int64_t r = 0; r < rows; ++r) {
     for (int64_t g = 0; g < ng; ++g) {
@@ -151,15 +168,13 @@ int mo_quantize_bf16(const uint16_t* w, int64_t rows, int64_t K, int gs, int bit
         scale = edge / q0;
         bias = edge;
       }
-      for (int c = 0; c < gs / pf; ++c) {
-        uint32_t word = 0;
-        for (int j = 0; j < pf; ++j) {
-          volatile float d = mo_bf16_to_f32(src[c * pf + j]) - bias;
-          float qv = rintf(d / scale);
-          qv = fminf(fmaxf(qv, 0.0f), n_bins);
-          word |= (uint32_t)qv << (j * bits);
-        }
-        wq[r * wc + g * (gs / pf) + c] = word;
+      uint32_t* gw = wq + r * wc + g * (gs * bits / 32);  /* the group's whole words */
+      for (int c = 0; c < gs * bits / 32; ++c) gw[c] = 0;
+      for (int j = 0; j < gs; ++j) {
+        volatile float d = mo_bf16_to_f32(src[j]) - bias;
+        float qv = rintf(d / scale);
+        qv = fminf(fmaxf(qv, 0.0f), n_bins);
+        put_code(gw, j, bits, (uint32_t)qv);
       }
       scales[r * ng + g] = mo_f32_to_bf16(scale);
       biases[r * ng + g] = mo_f32_to_bf16(bias);
@@ -178,14 +193,11 @@ int mo_quantize_bf16(const uint16_t* w, int64_t rows, int64_t K, int gs, int bit
 int mo_dequantize(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
                   int64_t rows, int64_t K, int gs, int bits, int kind, void* out) {
   if (!valid_bits(bits) || gs <= 0 || K % gs || (K * bits) % 32) return -1;
-  int pf = 32 / bits;
-  uint32_t mask = (1u << bits) - 1u;
-  int64_t wc = K / pf, ng = K / gs;
+  int64_t wc = K * bits / 32, ng = K / gs;
 #pragma omp parallel for schedule(static)
   for (int64_t r = 0; r < rows; ++r) {
     for (int64_t k = 0; k < K; ++k) {
-      uint32_t word = wq[r * wc + k / pf];
-      float q = (float)((word >> ((k % pf) * bits)) & mask);
+      float q = (float)get_code(wq + r * wc, k, bits);
       float s = mo_bf16_to_f32(scales[r * ng + k / gs]);
       float b = mo_bf16_to_f32(biases[r * ng + k / gs]);
       volatile float sq = s * q; /* exact */
@@ -215,12 +227,9 @@ static double x_at(const void* x, int x_f32, int64_t i) {
 /* Exact dequantized row n (fp64: s*q+b has no rounding in double). */
 static void deq_row_f64(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
                         int64_t n, int64_t K, int gs, int bits, double* row) {
-  int pf = 32 / bits;
-  uint32_t mask = (1u << bits) - 1u;
-  int64_t wc = K / pf, ng = K / gs;
+  int64_t wc = K * bits / 32, ng = K / gs;
   for (int64_t k = 0; k < K; ++k) {
-    uint32_t word = wq[n * wc + k / pf];
-    double q = (double)((word >> ((k % pf) * bits)) & mask);
+    double q = (double)get_code(wq + n * wc, k, bits);
     row[k] = (double)mo_bf16_to_f32(scales[n * ng + k / gs]) * q +
              (double)mo_bf16_to_f32(biases[n * ng + k / gs]);
   }
@@ -256,9 +265,7 @@ int mo_qmm_f32(const uint16_t* x_bf16, const uint32_t* wq, const uint16_t* scale
                const uint16_t* biases, int64_t M, int64_t N, int64_t K, int gs, int bits,
                float* y, int threads) {
   if (!valid_bits(bits) || gs <= 0 || K % gs || (K * bits) % 32) return -1;
-  int pf = 32 / bits;
-  uint32_t mask = (1u << bits) - 1u;
-  int64_t wc = K / pf, ng = K / gs;
+  int64_t wc = K * bits / 32, ng = K / gs;
   float* xf = (float*)malloc(sizeof(float) * (size_t)(M * K));
   float* xs = (float*)malloc(sizeof(float) * (size_t)(M * ng));
   for (int64_t i = 0; i < M * K; ++i) xf[i] = mo_bf16_to_f32(x_bf16[i]);
@@ -278,10 +285,7 @@ int mo_qmm_f32(const uint16_t* x_bf16, const uint32_t* wq, const uint16_t* scale
     float* qrow = (float*)malloc(sizeof(float) * (size_t)K);
 #pragma omp for schedule(static)
     for (int64_t n = 0; n < N; ++n) {
-      for (int64_t c = 0; c < wc; ++c) {
-        uint32_t word = wq[n * wc + c];
-        for (int j = 0; j < pf; ++j) qrow[c * pf + j] = (float)((word >> (j * bits)) & mask);
-      }
+      for (int64_t k = 0; k < K; ++k) qrow[k] = (float)get_code(wq + n * wc, k, bits);
       for (int64_t m = 0; m < M; ++m) {
         float acc = 0.f;
         const float* xr = xf + m * K;
@@ -312,8 +316,7 @@ int mo_gather_qmm_f64(const void* x, int x_f32, const uint32_t* wq, const uint16
                       int64_t n_idx, int64_t lhs_div, int64_t M, int64_t N, int64_t K,
                       int64_t x_batch, int64_t n_experts, int gs, int bits, double* out) {
   if (!valid_bits(bits) || gs <= 0 || K % gs || (K * bits) % 32 || lhs_div <= 0) return -1;
-  int pf = 32 / bits;
-  int64_t wc = K / pf, ng = K / gs;
+  int64_t wc = K * bits / 32, ng = K / gs;
   for (int64_t i = 0; i < n_idx; ++i) {
     int64_t li = lhs ? (int64_t)lhs[i] : i / lhs_div;
     int64_t ri = rhs ? (int64_t)rhs[i] : i;

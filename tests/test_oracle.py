@@ -67,17 +67,58 @@ def test_pack_known_words():
     assert O.pack(q8, 8).tolist() == [[0x04030201, 0x078000FF]]
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+ALL_BITS = [2, 3, 4, 5, 6, 8]
+
+
+def _bitstream_unpack(wq, K, bits):
+    # a row is one LSB-first bitstream over its little-endian bytes: code j = bits
+    # [j*bits, (j+1)*bits)
+    rows = wq.reshape(-1, wq.shape[-1])
+    bitv = np.unpackbits(rows.view(np.uint8), axis=1, bitorder="little")
+    bitv = bitv[:, : K * bits].reshape(rows.shape[0], K, bits).astype(np.uint32)
+    return (bitv << np.arange(bits, dtype=np.uint32)).sum(axis=2).astype(np.uint8)
+
+
+@pytest.mark.parametrize("bits", ALL_BITS)
 def test_pack_round_trip(bits):
     rng = np.random.default_rng(bits)
     q = rng.integers(0, 1 << bits, size=(7, 256)).astype(np.uint8)
     wq = O.pack(q, bits)
     assert wq.shape == (7, 256 * bits // 32)
     assert np.array_equal(O.unpack(wq, 256, bits), q)
-    # independent numpy unpack
-    shifts = np.arange(32 // bits, dtype=np.uint32) * bits
-    nq = ((wq[..., None] >> shifts) & ((1 << bits) - 1)).reshape(7, 256)
-    assert np.array_equal(nq, q)
+    assert np.array_equal(_bitstream_unpack(wq, 256, bits), q)  # independent unpack
+    if 32 % bits == 0:  # whole codes per word: value j of a word at bits j*bits
+        shifts = np.arange(32 // bits, dtype=np.uint32) * bits
+        nq = ((wq[..., None] >> shifts) & ((1 << bits) - 1)).reshape(7, 256)
+        assert np.array_equal(nq, q)
+
+
+def test_pack_5_and_6_bit_follow_the_reference_byte_reads():
+    # src/transformer.zig:516-578: a pack of 8 codes is `bits` bytes at pack*bits. 5-bit:
+    # a 40-bit little-endian r from 5 bytes, code ki = (r >> 5ki) & 31. 6-bit: three
+    # little-endian u16 h0..h2, a0 = h0 | (h1 & 0xFF) << 16, a1 = h1 >> 8 | h2 << 8, codes
+    # (a0 >> 6ki) & 63 then (a1 >> 6ki) & 63.
+    rng = np.random.default_rng(56)
+    q5 = rng.integers(0, 32, size=(3, 64)).astype(np.uint8)
+    b5 = O.pack(q5, 5).view(np.uint8).reshape(3, -1)
+    for r in range(3):
+        for p in range(8):
+            by = b5[r, 5 * p:5 * p + 5].astype(np.uint64)
+            rr = int(sum(int(by[i]) << (8 * i) for i in range(5)))
+            assert [(rr >> (5 * ki)) & 31 for ki in range(8)] == q5[r, 8 * p:8 * p + 8].tolist()
+    q6 = rng.integers(0, 64, size=(3, 64)).astype(np.uint8)
+    b6 = O.pack(q6, 6).view(np.uint8).reshape(3, -1)
+    for r in range(3):
+        for p in range(8):
+            h = [int(b6[r, 6 * p + 2 * i]) | int(b6[r, 6 * p + 2 * i + 1]) << 8 for i in range(3)]
+            a0 = h[0] | (h[1] & 0xFF) << 16
+            a1 = (h[1] >> 8) | (h[2] << 8)
+            got = [(a0 >> (6 * ki)) & 63 for ki in range(4)] + [(a1 >> (6 * ki)) & 63 for ki in range(4)]
+            assert got == q6[r, 8 * p:8 * p + 8].tolist()
+    # 3-bit: 8 codes in 3 bytes, hand-packed: codes 1..7, 0 -> 0b000_111_110_101_100_011_010_001
+    q3 = np.array([[1, 2, 3, 4, 5, 6, 7, 0] * 4], np.uint8)
+    w3 = O.pack(q3, 3).view(np.uint8).reshape(-1)
+    assert w3[:3].tolist() == list((0b000111110101100011010001).to_bytes(3, "little"))
 
 
 # -------------------------------------------------------------- quantize --
@@ -93,7 +134,7 @@ def test_quantize_hand_worked_group():
     assert s[0, 0] == O.f32_to_bf16(np.float32(0.1)) and b[0, 0] == 0xBF80
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", ALL_BITS)
 @pytest.mark.parametrize("gs", [32, 64, 128])
 def test_quantize_invariants(bits, gs):
     w = O.f32_to_bf16(O.randn(32 * 512, 9, 0.0, 0.02).reshape(32, 512))
@@ -127,7 +168,7 @@ def test_quantize_invariants(bits, gs):
 
 
 # ------------------------------------------------------------ dequantize --
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", ALL_BITS)
 def test_dequantize_closed_forms(bits):
     rng = np.random.default_rng(1)
     N, K, gs = 16, 256, 64
@@ -155,7 +196,7 @@ def _dense(wq, s, b, gs, bits):
     return O.dequantize(wq, s, b, gs, bits, O.DQ_F32).astype(np.float64)
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", ALL_BITS)
 def test_qmm_f64_matches_numpy(bits):
     wq, s, b = O.make_weight(48, 512, 5, bits)
     x = O.make_x_bf16(3, 512, 6)
