@@ -45,7 +45,8 @@ int resolve_common(mi_optional_int gs_in, mi_optional_int bits_in, const char* m
   if (mode && std::strcmp(mode, "affine") != 0)
     return fail(MI_ERR_UNSUPPORTED, "mode '%s' not supported (affine only)", mode);
   if (!transpose) return fail(MI_ERR_UNSUPPORTED, "transpose=false not supported");
-  if (*bits != 4 && *bits != 8) return fail(MI_ERR_UNSUPPORTED, "bits=%d not supported", *bits);
+  if (*bits != 2 && *bits != 3 && *bits != 4 && *bits != 5 && *bits != 6 && *bits != 8)
+    return fail(MI_ERR_UNSUPPORTED, "bits=%d not supported", *bits);
   if (*gs != 32 && *gs != 64 && *gs != 128)
     return fail(MI_ERR_UNSUPPORTED, "group_size=%d not supported", *gs);
   if (K <= 0 || K % *gs != 0)
@@ -218,6 +219,8 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
   int gs = 0, nb = 0;
   int rc = resolve_common(group_size, bits, mode, transpose, K, &gs, &nb);
   if (rc) return rc;
+  if (nb != 4 && nb != 8)
+    return fail(MI_ERR_UNSUPPORTED, "gather_qmm: bits=%d not supported (4 and 8)", nb);
   if (!valid_x_dtype(x_dtype)) return fail(MI_ERR_UNSUPPORTED, "x dtype %d not supported", x_dtype);
   if (sb_dtype != MI_DTYPE_BFLOAT16)
     return fail(MI_ERR_UNSUPPORTED, "scales/biases dtype %d not supported", sb_dtype);
@@ -426,9 +429,13 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   // M >= 256: dequantize once into the workspace and run a dense bf16 GEMM (the reference's
   // prefillDqGemm shape, src/transformer.zig:20987-21011); below the threshold the fused
   // dequant-in-register kernel is faster.
+  // 2/3/5/6-bit weights take this path at every M (no fused kernel for those widths).
   static const int dq_min = env_int("MI_QMM_DQGEMM_MIN", 256);
-  if (x_dtype == MI_DTYPE_BFLOAT16 && dq_min > 0 && M >= dq_min && K <= INT32_MAX &&
-      N * K * 2 <= ((int64_t)1 << 34)) {
+  const bool odd_width = nb != 4 && nb != 8;
+  if (odd_width && (x_dtype != MI_DTYPE_BFLOAT16 || N * K * 2 > ((int64_t)1 << 34)))
+    return fail(MI_ERR_UNSUPPORTED, "bits=%d: bf16 activations only", nb);
+  if (x_dtype == MI_DTYPE_BFLOAT16 && (odd_width || (dq_min > 0 && M >= dq_min)) &&
+      K <= INT32_MAX && N * K * 2 <= ((int64_t)1 << 34)) {
     const size_t wbytes = round256((size_t)N * K * 2);
     void* data = nullptr;
     rc = workspace(s, wbytes + mi::kDqGemmBlasWs, &data);

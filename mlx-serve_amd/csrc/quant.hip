@@ -46,6 +46,39 @@ __global__ void dequant_kernel(void* __restrict__ out, const uint32_t* __restric
   }
 }
 
+// Any affine width (2, 3, 5, 6 bits; 4 and 8 take the kernels around this one). A row of
+// K codes is one LSB-first bitstream over its little-endian bytes; a pack of 8 codes is
+// exactly `bits` bytes at byte 8*p*bits/8 of the row (the reference's unit of 8 values,
+// src/transformer.zig:516-578). One thread per pack; gs >= 32, so a pack lies in one group.
+__global__ void dequant_any_kernel(void* __restrict__ out, const uint32_t* __restrict__ w,
+                                   const uint16_t* __restrict__ s, const uint16_t* __restrict__ b,
+                                   int64_t n_packs, int64_t K, int gs, int bits, int out_f32,
+                                   int rounding) {
+  const int64_t ppr = K / 8;                 // packs per row
+  const int64_t row_bytes = K * bits / 8;    // a whole number of words
+  const int64_t G = K / gs;
+  const uint32_t mask = (1u << bits) - 1u;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_packs;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / ppr, p = i - row * ppr;
+    const uint8_t* pb = reinterpret_cast<const uint8_t*>(w) + row * row_bytes + p * bits;
+    uint64_t r = 0;
+    for (int j = 0; j < bits; ++j) r |= (uint64_t)pb[j] << (8 * j);
+    const int64_t k0 = 8 * p;
+    const int64_t gi = row * G + k0 / gs;
+    const float sc = bf16_bits_to_f32(s[gi]);
+    const float bi = bf16_bits_to_f32(b[gi]);
+    const int64_t o = row * K + k0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float sq = sc * (float)((uint32_t)(r >> (j * bits)) & mask);
+      const float v = rounding ? bf16_bits_to_f32(f32_to_bf16_bits(sq)) + bi : sq + bi;
+      if (out_f32) ((float*)out)[o + j] = v;
+      else ((uint16_t*)out)[o + j] = (uint16_t)f32_to_bf16_bits(v);
+    }
+  }
+}
+
 // 4-bit to bf16 with one rounding, gs in {32, 64, 128}. A block expands 1024 consecutive
 // packed words: per step a wave reads 64 consecutive words (256 B) and writes their 512
 // values as 1 KiB of consecutive bf16, so loads and stores are both contiguous per
@@ -100,7 +133,6 @@ __global__ void quant_kernel(uint32_t* __restrict__ wq, uint16_t* __restrict__ s
                              uint16_t* __restrict__ bo, const void* __restrict__ w, int w_f32,
                              int64_t n_groups, int gs, int bits) {
   const float n_bins = (float)((1 << bits) - 1);
-  const int pf = 32 / bits;
   for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < n_groups;
        gi += (int64_t)gridDim.x * blockDim.x) {
     const int64_t base = gi * gs;
@@ -124,15 +156,20 @@ __global__ void quant_kernel(uint32_t* __restrict__ wq, uint16_t* __restrict__ s
       scale = __fdiv_rn(edge, q0);
       bias = edge;
     }
-    uint32_t* out = wq + gi * (gs / pf);
-    for (int c = 0; c < gs / pf; ++c) {
-      uint32_t word = 0;
-      for (int j = 0; j < pf; ++j) {
-        float qv = rintf(__fdiv_rn(__fsub_rn(ld(c * pf + j), bias), scale));
-        qv = fminf(fmaxf(qv, 0.f), n_bins);
-        word |= (uint32_t)qv << (j * bits);
+    // the group's codes as one LSB-first bitstream of gs*bits/32 whole words (any width)
+    uint32_t* out = wq + gi * (gs * bits / 32);
+    uint64_t acc = 0;
+    int nb = 0, wo = 0;
+    for (int j = 0; j < gs; ++j) {
+      float qv = rintf(__fdiv_rn(__fsub_rn(ld(j), bias), scale));
+      qv = fminf(fmaxf(qv, 0.f), n_bins);
+      acc |= (uint64_t)(uint32_t)qv << nb;
+      nb += bits;
+      if (nb >= 32) {
+        out[wo++] = (uint32_t)acc;
+        acc >>= 32;
+        nb -= 32;
       }
-      out[c] = word;
     }
     so[gi] = (uint16_t)f32_to_bf16_bits(scale);
     bo[gi] = (uint16_t)f32_to_bf16_bits(bias);
@@ -308,6 +345,12 @@ hipError_t launch_dequantize(void* out, const uint32_t* w, const uint16_t* s, co
     if (g > (int64_t)1 << 20) g = (int64_t)1 << 20;
     hipLaunchKernelGGL(dequant4_bf16_kernel, dim3((unsigned)g), dim3(bs), 0, st, (u32x4_t*)out,
                        w, s, b, n_words, wshift);
+    return hipGetLastError();
+  }
+  if (bits != 4 && bits != 8) {
+    const int64_t n_packs = rows * (K / 8);
+    hipLaunchKernelGGL(dequant_any_kernel, dim3(grid_for(n_packs, bs)), dim3(bs), 0, st, out, w, s,
+                       b, n_packs, K, gs, bits, out_f32, rounding);
     return hipGetLastError();
   }
   if (bits == 4)

@@ -49,7 +49,8 @@ def _qmm(lib, **kw):
 @pytest.mark.parametrize("kw,code,msg", [
     (dict(mode=b"mxfp4"), L.MI_ERR_UNSUPPORTED, "mode"),
     (dict(transpose=False), L.MI_ERR_UNSUPPORTED, "transpose"),
-    (dict(bits=L.opt(3)), L.MI_ERR_UNSUPPORTED, "bits"),
+    (dict(bits=L.opt(7)), L.MI_ERR_UNSUPPORTED, "bits"),
+    (dict(bits=L.opt(3), xd=L.DT_FLOAT32), L.MI_ERR_UNSUPPORTED, "bf16 activations"),
     (dict(gs=L.opt(16)), L.MI_ERR_UNSUPPORTED, "group_size"),
     (dict(K=100), L.MI_ERR_INVALID, "multiple"),
     (dict(xd=L.DT_FLOAT16), L.MI_ERR_UNSUPPORTED, "dtype"),

@@ -18,7 +18,7 @@ def _print_case(**kw):
     print("CASE", kw, flush=True)
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("gs", [32, 64, 128])
 def test_dequantize_bit_exact(dev, bits, gs):
     _print_case(t="dequant", bits=bits, gs=gs)
@@ -34,7 +34,7 @@ def test_dequantize_bit_exact(dev, bits, gs):
         assert np.array_equal(got, O.dequantize(wq, s, b, gs, bits, kind))
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("gs", [32, 64, 128])
 def test_quantize_bit_exact(dev, bits, gs):
     _print_case(t="quant", bits=bits, gs=gs)
@@ -73,6 +73,31 @@ def test_qmm_bf16(dev, M, N, K, bits, gs):
     truth = O.qmm_f64(x, wq[0], s[0], b[0], gs, bits)
     assert y.shape == (M, N) and y.dtype == torch.bfloat16
     assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+
+
+@pytest.mark.parametrize("bits", [2, 3, 5, 6])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 1024), (7, 96, 512), (300, 64, 384)])
+def test_qmm_other_widths(dev, M, N, K, bits, gs):
+    """2/3/5/6-bit weights: dequantize to bf16, then the bf16 GEMM, at every M."""
+    _print_case(t="qmm_width", M=M, N=N, K=K, bits=bits, gs=gs)
+    wq, s, b = weights(1, N, K, bits, gs, 3000 + bits)
+    x = O.make_x_bf16(M, K, 4000 + M)
+    y = mi_qmm.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(wq[0], dev),
+                                to_dev_bf16(s[0], dev), to_dev_bf16(b[0], dev), True, gs, bits)
+    truth = O.qmm_f64(x, wq[0], s[0], b[0], gs, bits)
+    assert y.shape == (M, N) and y.dtype == torch.bfloat16
+    assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+
+
+def test_gather_other_widths_decline(dev):
+    _print_case(t="gather_width_decline")
+    wq, s, b = weights(2, 32, 256, 3, 64, 5)
+    x = O.make_x_bf16(1, 256, 6).reshape(1, 1, 256)
+    with pytest.raises(Exception, match="bits=3"):
+        mi_qmm.gather_qmm(to_dev_bf16(x, dev), to_dev_u32(wq, dev), to_dev_bf16(s, dev),
+                          to_dev_bf16(b, dev), rhs_indices=to_dev_u32(np.array([1], np.uint32), dev),
+                          group_size=64, bits=3)
 
 
 @pytest.mark.parametrize("bits", [4, 8])
