@@ -282,7 +282,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--decode-only", type=int, default=0, metavar="M",
                     help="only run the configs[1] decode step at this M (for rocprofv3)")
-    ap.add_argument("--bits", type=int, default=4, choices=(4, 8),
+    ap.add_argument("--bits", type=int, default=4, choices=(2, 3, 4, 5, 6, 8),
                     help="weight bits of --decode-only")
     ap.add_argument("--prefill-only", type=int, default=0, metavar="M",
                     help="only run the configs[2] prefill shapes at this M (for rocprofv3)")

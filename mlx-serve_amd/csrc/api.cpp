@@ -434,6 +434,12 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   const bool odd_width = nb != 4 && nb != 8;
   if (odd_width && (x_dtype != MI_DTYPE_BFLOAT16 || N * K * 2 > ((int64_t)1 << 34)))
     return fail(MI_ERR_UNSUPPORTED, "bits=%d: bf16 activations only", nb);
+  static const int any_max = env_int("MI_QMM_ANY_MAX", 8);
+  if (odd_width && M <= any_max) {  // decode rows: straight from the packed bitstream
+    hipError_t e = mi::launch_qmv_any((const uint16_t*)x, w, (const uint16_t*)scales,
+                                      (const uint16_t*)biases, (uint16_t*)y, M, N, K, gs, nb, s);
+    if (e != hipErrorNotSupported) return e == hipSuccess ? MI_OK : hip_fail(e, "qmv_any launch");
+  }
   if (x_dtype == MI_DTYPE_BFLOAT16 && (odd_width || (dq_min > 0 && M >= dq_min)) &&
       K <= INT32_MAX && N * K * 2 <= ((int64_t)1 << 34)) {
     const size_t wbytes = round256((size_t)N * K * 2);

@@ -109,6 +109,11 @@ hipError_t launch_swiglu(uint16_t* y, const uint16_t* g, const uint16_t* u, int6
                          hipStream_t s);
 hipError_t launch_down_reduce(uint16_t* y, const uint16_t* v, const uint16_t* scores, int64_t T,
                               int k, int64_t N, hipStream_t s);
+// Decode GEMV for 2/3/5/6-bit affine weights, 1..8 bf16 activation rows (qmv_any.hip).
+// hipErrorNotSupported when the shape is outside its scope.
+hipError_t launch_qmv_any(const uint16_t* x, const uint32_t* w, const uint16_t* s,
+                          const uint16_t* b, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                          int gs, int bits, hipStream_t st);
 // Decode MoE down projection + score-weighted slot sum in one launch (moe_down.hip).
 bool moe_down_supported(int64_t T, int k, int64_t N, int64_t K, int gs, int bits, int ws, int nc);
 hipError_t launch_moe_down(uint16_t* y, const uint16_t* act, const uint32_t* w,

@@ -77,9 +77,11 @@ def test_qmm_bf16(dev, M, N, K, bits, gs):
 
 @pytest.mark.parametrize("bits", [2, 3, 5, 6])
 @pytest.mark.parametrize("gs", [32, 64, 128])
-@pytest.mark.parametrize("M,N,K", [(1, 256, 1024), (7, 96, 512), (300, 64, 384)])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 1024), (7, 96, 512), (8, 100, 2048), (2, 50, 256),
+                                   (300, 64, 384)])
 def test_qmm_other_widths(dev, M, N, K, bits, gs):
-    """2/3/5/6-bit weights: dequantize to bf16, then the bf16 GEMM, at every M."""
+    """2/3/5/6-bit weights: up to 8 rows read the packed bitstream directly (qmv_any),
+    more rows dequantize to bf16 and run the bf16 GEMM."""
     _print_case(t="qmm_width", M=M, N=N, K=K, bits=bits, gs=gs)
     wq, s, b = weights(1, N, K, bits, gs, 3000 + bits)
     x = O.make_x_bf16(M, K, 4000 + M)
