@@ -55,8 +55,10 @@ typedef struct {
 /* Replaces mlx_quantized_matmul (src/mlx.zig:262), mode "affine", transpose=true:
  *   y[M,N] = x[M,K] @ dequant(w)[N,K]^T, dequant(w) = scale*q + bias per group.
  * x: x_dtype in {bfloat16, float32}; y has x's dtype. scales/biases: sb_dtype
- * bfloat16. bits in {4,8}; group_size in {32,64,128}; K % group_size == 0.
- * transpose=false and other modes return MI_ERR_UNSUPPORTED. */
+ * bfloat16. bits in {2,3,4,5,6,8} (2/3/5/6: bfloat16 x only); group_size in
+ * {32,64,128}; K % group_size == 0. Codes are one LSB-first bitstream per row (for 4
+ * and 8 bits: value j of a word at bits j*bits). transpose=false and other modes return
+ * MI_ERR_UNSUPPORTED. */
 int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
                         const void* biases, int64_t M, int64_t N, int64_t K, bool transpose,
                         mi_optional_int group_size, mi_optional_int bits, const char* mode,
@@ -65,13 +67,14 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
 /* Replaces mlx_gather_qmm (src/mlx.zig:265), transpose=true, mode "affine":
  *   y[i] = x[lhs(i)] @ dequant(w[rhs(i)])^T      for i in [0, n_idx)
  * x: [x_batch, M, K]; w: [n_experts, N, K*bits/32]; scales/biases [n_experts, N, K/gs];
- * y: [n_idx, M, N]. lhs_indices may be NULL: lhs(i) = i / lhs_div (lhs_div=1 is MLX's
+ * y: [n_idx, M, N]. bits 4 or 8 (other widths return MI_ERR_UNSUPPORTED).
+ * lhs_indices may be NULL: lhs(i) = i / lhs_div (lhs_div=1 is MLX's
  * default arange; lhs_div=top_k is one token broadcast over its top-k slots, the
  * reference's decode call). rhs_indices may be NULL: rhs(i) = i.
  * Indices are uint32 device arrays. sorted_indices=true groups consecutive equal
  * rhs values into one weight pass per run (any order stays correct; sorted order
  * is what makes it fast). Out-of-range indices write NaN rows, never read out of
-* bounds. Uses the per-device workspace (mi_workspace_reserve) for sorted work lists
+ * bounds. Uses the per-device workspace (mi_workspace_reserve) for sorted work lists
  * and split-K partials. */
 int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
                   const void* biases, const uint32_t* lhs_indices, const uint32_t* rhs_indices,
