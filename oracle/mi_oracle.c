@@ -462,3 +462,47 @@ int mo_affine_params_from_geometry(int64_t w_cols, int64_t s_cols, int64_t in_di
   *gs = (int)g;
   return 0;
 }
+
+/* ------------------------------------------------ microscaling fp modes --- */
+/* Bias-less modes (mlx_quantized_matmul / mlx_dequantize with mode "nvfp4", "mxfp4",
+ * "mxfp8"; the reference routes them at src/transformer.zig:20905-20921 and names the
+ * (bits, group_size) of each at :16846-16854): w = element(q) * scale(s), with
+ *   nvfp4: 4-bit e2m1 codes, gs 16, e4m3 scale bytes;
+ *   mxfp4: 4-bit e2m1 codes, gs 32, e8m0 scale bytes;
+ *   mxfp8: 8-bit e4m3 codes, gs 32, e8m0 scale bytes.
+ * The element decoders follow the reference's bit constructions (:20126-20142 for e2m1 and
+ * e4m3 with no NaN code, :18918-18924 for e8m0 with byte 0 = 2^-127), restated as the
+ * values they produce. Every product is exact in fp32 and in bf16. */
+float mo_e2m1(uint32_t c) {
+  const uint32_t m = c & 7u, e = m >> 1, f = m & 1u;
+  const float mag = e == 0 ? 0.5f * (float)f : ldexpf(1.0f + 0.5f * (float)f, (int)e - 1);
+  return (c & 8u) ? -mag : mag;
+}
+
+float mo_e4m3(uint32_t b) {
+  const uint32_t m = b & 0x7Fu, e = m >> 3, f = m & 7u;
+  const float mag = e == 0 ? ldexpf((float)f, -9) : ldexpf(1.0f + (float)f / 8.0f, (int)e - 7);
+  return (b & 0x80u) ? -mag : mag;
+}
+
+float mo_e8m0(uint32_t b) { return ldexpf(1.0f, b == 0 ? -127 : (int)b - 127); }
+
+/* mode: 0 nvfp4, 1 mxfp4, 2 mxfp8. out_bf16: 0 fp32, 1 bf16 (exact either way). */
+int mo_dequantize_fp(const uint32_t* wq, const uint8_t* scales, int64_t rows, int64_t K,
+                     int mode, int out_bf16, void* out) {
+  if (mode < 0 || mode > 2) return -1;
+  const int bits = mode == 2 ? 8 : 4, gs = mode == 0 ? 16 : 32;
+  if (K % gs) return -1;
+  const int64_t wc = K * bits / 32, ng = K / gs;
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t k = 0; k < K; ++k) {
+      const uint32_t q = get_code(wq + r * wc, k, bits);
+      const uint32_t sb = scales[r * ng + k / gs];
+      const float el = mode == 2 ? mo_e4m3(q) : mo_e2m1(q);
+      const float sc = mode == 0 ? mo_e4m3(sb) : mo_e8m0(sb);
+      const float v = el * sc;
+      if (out_bf16) ((uint16_t*)out)[r * K + k] = mo_f32_to_bf16(v);
+      else ((float*)out)[r * K + k] = v;
+    }
+  return 0;
+}

@@ -40,6 +40,10 @@ def lib():
         L.mo_unpack.argtypes = [P, i64, i64, i32, P]
         L.mo_quantize_bf16.argtypes = [P, i64, i64, i32, i32, P, P, P]
         L.mo_dequantize.argtypes = [P, P, P, i64, i64, i32, i32, i32, P]
+        L.mo_dequantize_fp.argtypes = [P, P, i64, i64, i32, i32, P]
+        for f in (L.mo_e2m1, L.mo_e4m3, L.mo_e8m0):
+            f.argtypes = [ctypes.c_uint32]
+            f.restype = ctypes.c_float
         L.mo_qmm_f64.argtypes = [P, i32, P, P, P, i64, i64, i64, i32, i32, P]
         L.mo_qmm_f32.argtypes = [P, P, P, P, i64, i64, i64, i32, i32, P, i32]
         L.mo_gather_qmm_f64.argtypes = [P, i32, P, P, P, P, P, i64, i64, i64, i64, i64,
@@ -122,6 +126,27 @@ def quantize(w_bf16, group_size=64, bits=4):
     _check(lib().mo_quantize_bf16(_p(w), rows, K, group_size, bits, _p(wq), _p(s), _p(b)),
            "quantize")
     return wq, s, b
+
+
+FP_MODES = {"nvfp4": (0, 4, 16), "mxfp4": (1, 4, 32), "mxfp8": (2, 8, 32)}
+
+
+def fp_element(code, fmt):
+    """One decoded e2m1 / e4m3 / e8m0 value (float)."""
+    return float({"e2m1": lib().mo_e2m1, "e4m3": lib().mo_e4m3, "e8m0": lib().mo_e8m0}[fmt](code))
+
+
+def dequantize_fp(wq, scales_u8, mode, out_bf16=False):
+    """Bias-less microscaling modes: wq [..., K*bits/32] u32, scales [..., K/gs] uint8."""
+    m, bits, gs = FP_MODES[mode]
+    wq = np.ascontiguousarray(wq, dtype=np.uint32)
+    sc = np.ascontiguousarray(scales_u8, dtype=np.uint8)
+    K = wq.shape[-1] * 32 // bits
+    rows = wq.size // wq.shape[-1]
+    out = np.empty(tuple(wq.shape[:-1]) + (K,), dtype=np.uint16 if out_bf16 else np.float32)
+    _check(lib().mo_dequantize_fp(_p(wq), _p(sc), rows, K, m, int(out_bf16), _p(out)),
+           "dequantize_fp")
+    return out
 
 
 def dequantize(wq, scales, biases, group_size=64, bits=4, kind=DQ_F32):

@@ -316,3 +316,46 @@ def test_geometry_cases_from_reference_tests():
         assert got == want, c["name"]
     assert O.affine_params_from_geometry(512, 64, 4096) == (4, 64)
     assert O.affine_params_from_geometry(1024, 64, 4096) == (8, 64)
+
+
+# --------------------------------------------------- microscaling fp modes --
+def test_fp_element_decoders_match_the_format_tables():
+    # OCP MX v1.0 element tables: e2m1 magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6 (sign bit 3);
+    # e4m3 1.0 = 0x38, max normal 0x7E = 448, min subnormal 0x01 = 2^-9, and 0x7F decodes
+    # to 480 (no NaN code, as the reference's bit construction); e8m0 2^(b-127), b=0 2^-127.
+    assert [O.fp_element(c, "e2m1") for c in range(8)] == [0, .5, 1, 1.5, 2, 3, 4, 6]
+    assert [O.fp_element(c | 8, "e2m1") for c in range(1, 8)] == [-.5, -1, -1.5, -2, -3, -4, -6]
+    assert O.fp_element(0x38, "e4m3") == 1.0 and O.fp_element(0xB8, "e4m3") == -1.0
+    assert O.fp_element(0x7E, "e4m3") == 448.0 and O.fp_element(0x7F, "e4m3") == 480.0
+    assert O.fp_element(0x01, "e4m3") == 2.0 ** -9 and O.fp_element(0x08, "e4m3") == 2.0 ** -6
+    assert O.fp_element(0x80, "e4m3") == 0.0
+    assert O.fp_element(127, "e8m0") == 1.0 and O.fp_element(130, "e8m0") == 8.0
+    assert O.fp_element(0, "e8m0") == 2.0 ** -127 and O.fp_element(254, "e8m0") == 2.0 ** 127
+    # every e4m3 byte against the bit-level definition via a float16 view: the byte's low
+    # 7 bits shifted left by 7 are a float16 of value/256 (the reference's construction)
+    for b in range(256):
+        h = np.array([((b & 0x7F) << 7) | ((b & 0x80) << 8)], np.uint16).view(np.float16)
+        assert O.fp_element(b, "e4m3") == float(h[0]) * 256.0
+    for c in range(16):
+        h = np.array([((c & 7) << 9) | ((c & 8) << 12)], np.uint16).view(np.float16)
+        assert O.fp_element(c, "e2m1") == float(h[0]) * 2.0 ** 14
+
+
+@pytest.mark.parametrize("mode", ["nvfp4", "mxfp4", "mxfp8"])
+def test_dequantize_fp_closed_form(mode):
+    m, bits, gs = O.FP_MODES[mode]
+    rng = np.random.default_rng(m)
+    N, K = 8, 128
+    q = rng.integers(0, 1 << bits, size=(N, K)).astype(np.uint8)
+    sc = rng.integers(100, 140, size=(N, K // gs)).astype(np.uint8)
+    wq = O.pack(q, bits)
+    el = "e4m3" if mode == "mxfp8" else "e2m1"
+    sf = "e4m3" if mode == "nvfp4" else "e8m0"
+    tab_el = np.array([O.fp_element(c, el) for c in range(1 << bits)], np.float64)
+    tab_sc = np.array([O.fp_element(c, sf) for c in range(256)], np.float64)
+    exact = tab_el[q] * np.repeat(tab_sc[sc], gs, axis=1)
+    f32 = O.dequantize_fp(wq, sc, mode)
+    assert np.array_equal(f32.astype(np.float64), exact)  # exact in fp32
+    assert np.array_equal(O.dequantize_fp(wq, sc, mode, out_bf16=True),
+                          O.f32_to_bf16(exact.astype(np.float32)))
+    assert np.array_equal(O.bf16_to_f32(O.dequantize_fp(wq, sc, mode, out_bf16=True)), f32)
