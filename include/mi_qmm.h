@@ -39,6 +39,7 @@ enum {
 
 /* Values match mlx_dtype (src/mlx.zig:20-35). */
 enum {
+  MI_DTYPE_UINT8 = 1,
   MI_DTYPE_UINT32 = 3,
   MI_DTYPE_FLOAT16 = 9,
   MI_DTYPE_FLOAT32 = 10,
@@ -57,8 +58,11 @@ typedef struct {
  * x: x_dtype in {bfloat16, float32}; y has x's dtype. scales/biases: sb_dtype
  * bfloat16. bits in {2,3,4,5,6,8} (2/3/5/6: bfloat16 x only); group_size in
  * {32,64,128}; K % group_size == 0. Codes are one LSB-first bitstream per row (for 4
- * and 8 bits: value j of a word at bits j*bits). transpose=false and other modes return
- * MI_ERR_UNSUPPORTED. */
+ * and 8 bits: value j of a word at bits j*bits).
+ * mode "nvfp4" (4-bit e2m1, gs 16, e4m3 scales), "mxfp4" (4-bit e2m1, gs 32, e8m0
+ * scales), "mxfp8" (8-bit e4m3, gs 32, e8m0 scales): bias-less (biases may be NULL),
+ * scales MI_DTYPE_UINT8, x bfloat16; group_size/bits default to the mode's and must
+ * match it. transpose=false and other modes return MI_ERR_UNSUPPORTED. */
 int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
                         const void* biases, int64_t M, int64_t N, int64_t K, bool transpose,
                         mi_optional_int group_size, mi_optional_int bits, const char* mode,
@@ -85,6 +89,8 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
 
 /* Replaces mlx_dequantize (src/mlx.zig:271), mode "affine", no global scale:
  *   out[r,k] = scale[r,k/gs] * q[r,k] + bias[r,k/gs]
+ * Modes "nvfp4" / "mxfp4" / "mxfp8" (uint8 scales, no biases): out = element(q) *
+ * scale, exact in float32 and bfloat16.
  * out_dtype float32: exact fp32 result. out_dtype bfloat16: rounded like MLX's
  * composed dequantize (a bf16 multiply then a bf16 add). */
 int mi_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,

@@ -56,6 +56,32 @@ int resolve_common(mi_optional_int gs_in, mi_optional_int bits_in, const char* m
   return MI_OK;
 }
 
+// Microscaling modes: 0 nvfp4, 1 mxfp4, 2 mxfp8; -1 for affine (or no mode given).
+int fp_mode_of(const char* mode) {
+  if (!mode || std::strcmp(mode, "affine") == 0) return -1;
+  if (std::strcmp(mode, "nvfp4") == 0) return 0;
+  if (std::strcmp(mode, "mxfp4") == 0) return 1;
+  if (std::strcmp(mode, "mxfp8") == 0) return 2;
+  return -2;
+}
+
+// Each fp mode defines its (bits, group_size) (src/transformer.zig:16846-16854); given
+// values must agree.
+int resolve_fp(int fm, mi_optional_int gs_in, mi_optional_int bits_in, bool transpose, int64_t K,
+               int sb_dtype, int* gs, int* bits) {
+  *bits = fm == 2 ? 8 : 4;
+  *gs = fm == 0 ? 16 : 32;
+  if (!transpose) return fail(MI_ERR_UNSUPPORTED, "transpose=false not supported");
+  if ((gs_in.has_value && gs_in.value != *gs) || (bits_in.has_value && bits_in.value != *bits))
+    return fail(MI_ERR_INVALID, "this mode takes group_size=%d bits=%d", *gs, *bits);
+  if (K <= 0 || K % *gs) return fail(MI_ERR_INVALID, "K=%lld must be a positive multiple of %d",
+                                     (long long)K, *gs);
+  if (K > (int64_t)1 << 30) return fail(MI_ERR_INVALID, "K too large");
+  if (sb_dtype != MI_DTYPE_UINT8)
+    return fail(MI_ERR_UNSUPPORTED, "scales dtype %d not supported (uint8 for this mode)", sb_dtype);
+  return MI_OK;
+}
+
 // Per-device scratch for sorted work lists and K-split partials. Calls on one
 // stream are ordered, so reuse by later calls is safe; calls that overlap on
 // different streams of one device must not both use it. It only grows outside
@@ -416,6 +442,33 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
                         mi_optional_int group_size, mi_optional_int bits, const char* mode,
                         int x_dtype, int sb_dtype, void* stream) {
   int gs = 0, nb = 0;
+  const int fm = fp_mode_of(mode);
+  if (fm >= 0) {
+    // nvfp4 / mxfp4 / mxfp8: the dequantized weight is exact in bf16; dequantize it into the
+    // workspace and run the bf16 GEMM (the reference sends these modes to MLX's own
+    // quantized_matmul, src/transformer.zig:20905-20921)
+    int rc = resolve_fp(fm, group_size, bits, transpose, K, sb_dtype, &gs, &nb);
+    if (rc) return rc;
+    if (x_dtype != MI_DTYPE_BFLOAT16)
+      return fail(MI_ERR_UNSUPPORTED, "mode %s: bf16 activations only", mode);
+    if (M < 0 || N < 0) return fail(MI_ERR_INVALID, "negative size");
+    if (M == 0 || N == 0) return MI_OK;
+    if (!y || !x || !w || !scales) return fail(MI_ERR_INVALID, "null tensor pointer");
+    if (N > (int64_t)1 << 30 || M > (int64_t)1 << 30 || N * K * 2 > ((int64_t)1 << 34))
+      return fail(MI_ERR_INVALID, "N, M or N*K too large");
+    hipStream_t s = (hipStream_t)stream;
+    const size_t wbytes = round256((size_t)N * K * 2);
+    void* data = nullptr;
+    rc = workspace(s, wbytes + mi::kDqGemmBlasWs, &data);
+    if (rc) return rc;
+    hipError_t e = mi::launch_dequantize_fp(data, w, (const uint8_t*)scales, N, K, fm, 0, s);
+    if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+    const char* err = nullptr;
+    if (mi::dq_gemm((const uint16_t*)x, (const uint16_t*)data, (uint16_t*)y, (int)M, (int)N,
+                    (int)K, (int)N, (char*)data + wbytes, mi::kDqGemmBlasWs, s, &err) != 0)
+      return fail(MI_ERR_HIP, "hipBLASLt GEMM: %s", err ? err : "error");
+    return MI_OK;
+  }
   int rc = resolve_common(group_size, bits, mode, transpose, K, &gs, &nb);
   if (rc) return rc;
   if (!valid_x_dtype(x_dtype)) return fail(MI_ERR_UNSUPPORTED, "x dtype %d not supported", x_dtype);
@@ -495,6 +548,19 @@ int mi_dequantize_rounding(void* out, const uint32_t* w, const void* scales, con
                            mi_optional_int bits, const char* mode, int sb_dtype, int out_dtype,
                            int rounding, void* stream) {
   int gs = 0, nb = 0;
+  const int fm = fp_mode_of(mode);
+  if (fm >= 0) {  // exact in either output dtype: rounding does not apply
+    int rc = resolve_fp(fm, group_size, bits, true, K, sb_dtype, &gs, &nb);
+    if (rc) return rc;
+    if (out_dtype != MI_DTYPE_BFLOAT16 && out_dtype != MI_DTYPE_FLOAT32)
+      return fail(MI_ERR_UNSUPPORTED, "output dtype %d not supported", out_dtype);
+    if (rows < 0) return fail(MI_ERR_INVALID, "negative rows");
+    if (rows == 0) return MI_OK;
+    if (!out || !w || !scales) return fail(MI_ERR_INVALID, "null tensor pointer");
+    hipError_t e = mi::launch_dequantize_fp(out, w, (const uint8_t*)scales, rows, K, fm,
+                                            out_dtype == MI_DTYPE_FLOAT32, (hipStream_t)stream);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "dequantize launch");
+  }
   int rc = resolve_common(group_size, bits, mode, true, K, &gs, &nb);
   if (rc) return rc;
   if (sb_dtype != MI_DTYPE_BFLOAT16)

@@ -109,6 +109,9 @@ hipError_t launch_swiglu(uint16_t* y, const uint16_t* g, const uint16_t* u, int6
                          hipStream_t s);
 hipError_t launch_down_reduce(uint16_t* y, const uint16_t* v, const uint16_t* scores, int64_t T,
                               int k, int64_t N, hipStream_t s);
+// nvfp4 (mode 0) / mxfp4 (1) / mxfp8 (2) dequantize, uint8 scales, no biases (quant.hip).
+hipError_t launch_dequantize_fp(void* out, const uint32_t* w, const uint8_t* s, int64_t rows,
+                                int64_t K, int mode, int out_f32, hipStream_t st);
 // Decode GEMV for 2/3/5/6-bit affine weights, 1..8 bf16 activation rows (qmv_any.hip).
 // hipErrorNotSupported when the shape is outside its scope.
 hipError_t launch_qmv_any(const uint16_t* x, const uint32_t* w, const uint16_t* s,

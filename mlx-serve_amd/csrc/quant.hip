@@ -79,6 +79,44 @@ __global__ void dequant_any_kernel(void* __restrict__ out, const uint32_t* __res
   }
 }
 
+// Bias-less microscaling modes: w = element(q) * scale(s), exact in fp32 and in bf16.
+// mode 0 nvfp4 (e2m1 codes, gs 16, e4m3 scales), 1 mxfp4 (e2m1, gs 32, e8m0), 2 mxfp8
+// (e4m3 codes, gs 32, e8m0). Element decoders as the reference builds them from bits
+// (src/transformer.zig:20126-20142 e2m1/e4m3 without a NaN code, :18918-18924 e8m0 with
+// byte 0 = 2^-127), written as the values they produce. One thread per packed word.
+MI_DEV float fp_e2m1(uint32_t c) {
+  const uint32_t m = c & 7u, e = m >> 1, f = m & 1u;
+  const float mag = e == 0 ? 0.5f * (float)f : __builtin_ldexpf(1.0f + 0.5f * (float)f, (int)e - 1);
+  return (c & 8u) ? -mag : mag;
+}
+MI_DEV float fp_e4m3(uint32_t b) {
+  const uint32_t m = b & 0x7Fu, e = m >> 3, f = m & 7u;
+  const float mag =
+      e == 0 ? __builtin_ldexpf((float)f, -9) : __builtin_ldexpf(1.0f + 0.125f * (float)f, (int)e - 7);
+  return (b & 0x80u) ? -mag : mag;
+}
+MI_DEV float fp_e8m0(uint32_t b) { return __builtin_ldexpf(1.0f, b == 0 ? -127 : (int)b - 127); }
+
+__global__ void dequant_fp_kernel(void* __restrict__ out, const uint32_t* __restrict__ w,
+                                  const uint8_t* __restrict__ s, int64_t n_words, int64_t K,
+                                  int mode, int out_f32) {
+  const int bits = mode == 2 ? 8 : 4, gs = mode == 0 ? 16 : 32, pf = 32 / bits;
+  const int64_t wpr = K / pf, G = K / gs;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_words;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / wpr, k0 = (i - row * wpr) * pf;
+    const uint32_t word = w[i];
+    for (int j = 0; j < pf; ++j) {
+      const int64_t k = k0 + j;
+      const uint32_t q = (word >> (j * bits)) & ((1u << bits) - 1u);
+      const uint32_t sb = s[row * G + k / gs];
+      const float v = (mode == 2 ? fp_e4m3(q) : fp_e2m1(q)) * (mode == 0 ? fp_e4m3(sb) : fp_e8m0(sb));
+      if (out_f32) ((float*)out)[row * K + k] = v;
+      else ((uint16_t*)out)[row * K + k] = (uint16_t)f32_to_bf16_bits(v);
+    }
+  }
+}
+
 // 4-bit to bf16 with one rounding, gs in {32, 64, 128}. A block expands 1024 consecutive
 // packed words: per step a wave reads 64 consecutive words (256 B) and writes their 512
 // values as 1 KiB of consecutive bf16, so loads and stores are both contiguous per
@@ -359,6 +397,15 @@ hipError_t launch_dequantize(void* out, const uint32_t* w, const uint16_t* s, co
   else
     hipLaunchKernelGGL(dequant_kernel<8>, dim3(grid_for(n_words, bs)), dim3(bs), 0, st, out, w, s,
                        b, n_words, K, gs, out_f32, rounding);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequantize_fp(void* out, const uint32_t* w, const uint8_t* s, int64_t rows,
+                                int64_t K, int mode, int out_f32, hipStream_t st) {
+  const int64_t n_words = rows * (K * (mode == 2 ? 8 : 4) / 32);
+  if (n_words == 0) return hipSuccess;
+  hipLaunchKernelGGL(dequant_fp_kernel, dim3(grid_for(n_words, 256)), dim3(256), 0, st, out, w, s,
+                     n_words, K, mode, out_f32);
   return hipGetLastError();
 }
 

@@ -6,7 +6,7 @@ import os
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmi_qmm.so")
 
 MI_OK, MI_ERR_UNSUPPORTED, MI_ERR_INVALID, MI_ERR_HIP = 0, 1, 2, 3
-DT_UINT32, DT_FLOAT16, DT_FLOAT32, DT_BFLOAT16 = 3, 9, 10, 12
+DT_UINT8, DT_UINT32, DT_FLOAT16, DT_FLOAT32, DT_BFLOAT16 = 1, 3, 9, 10, 12
 
 
 class MiError(RuntimeError):

@@ -10,9 +10,11 @@ import math
 
 import torch
 
-from ._lib import (DT_BFLOAT16, DT_FLOAT32, MI_ERR_INVALID, MiError, check, lib, opt)
+from ._lib import (DT_BFLOAT16, DT_FLOAT32, DT_UINT8, MI_ERR_INVALID, MiError, check, lib, opt)
 
-_DT = {torch.bfloat16: DT_BFLOAT16, torch.float32: DT_FLOAT32}
+_DT = {torch.bfloat16: DT_BFLOAT16, torch.float32: DT_FLOAT32, torch.uint8: DT_UINT8}
+# bias-less microscaling modes: (group_size, bits) each one defines
+_FP_MODES = {"nvfp4": (16, 4), "mxfp4": (32, 4), "mxfp8": (32, 8)}
 
 
 def _stream(t):
@@ -40,10 +42,16 @@ def _require(cond, msg):
         raise MiError(MI_ERR_INVALID, msg)
 
 
-def _resolve(w, scales, group_size, bits, K):
-    """MLX defaults (64, 4); validate against the packed geometry."""
-    gs = 64 if group_size is None else int(group_size)
-    nb = 4 if bits is None else int(bits)
+def _defaults(mode):
+    return _FP_MODES.get(mode, (64, 4))
+
+
+def _resolve(w, scales, group_size, bits, K, mode="affine"):
+    """MLX defaults ((64, 4) for affine, the mode's own otherwise); validate against the
+    packed geometry."""
+    dgs, dnb = _defaults(mode)
+    gs = dgs if group_size is None else int(group_size)
+    nb = dnb if bits is None else int(bits)
     _require(w.shape[-1] * 32 == K * nb,
              f"packed width {w.shape[-1]} does not match K={K} at bits={nb}")
     _require(scales.shape[-1] * gs == K,
@@ -63,7 +71,7 @@ def quantized_matmul(x, w, scales, biases, transpose=True, group_size=None, bits
     """y = x @ dequantize(w).T (mlx_quantized_matmul, src/mlx.zig:262). x [..., K]."""
     _contig(x, w, scales, biases)
     K = x.shape[-1]
-    gs, nb = _resolve(_packed(w), scales, group_size, bits, K)
+    gs, nb = _resolve(_packed(w), scales, group_size, bits, K, mode)
     _require(w.dim() == 2, "w must be [N, K*bits/32]")
     N = w.shape[0]
     M = x.numel() // K if K else 0
@@ -145,9 +153,9 @@ def dequantize(w, scales, biases, group_size=None, bits=None, mode="affine", dty
     """mlx_dequantize (src/mlx.zig:271). dtype defaults to the scales dtype.
     rounding (bf16 output only): None/1 = op-by-op bf16, 0 = single rounding."""
     _contig(w, scales, biases)
-    K = w.shape[-1] * 32 // (4 if bits is None else int(bits))
-    gs, nb = _resolve(_packed(w), scales, group_size, bits, K)
-    dtype = scales.dtype if dtype is None else dtype
+    K = w.shape[-1] * 32 // (_defaults(mode)[1] if bits is None else int(bits))
+    gs, nb = _resolve(_packed(w), scales, group_size, bits, K, mode)
+    dtype = (torch.bfloat16 if scales.dtype == torch.uint8 else scales.dtype) if dtype is None else dtype
     rows = w.numel() // w.shape[-1] if w.shape[-1] else 0
     out = torch.empty(tuple(w.shape[:-1]) + (K,), dtype=dtype, device=w.device)
     check(lib().mi_dequantize_rounding(_ptr(out), _ptr(w), _ptr(scales), _ptr(biases), rows, K,

@@ -47,7 +47,9 @@ def _qmm(lib, **kw):
 
 
 @pytest.mark.parametrize("kw,code,msg", [
-    (dict(mode=b"mxfp4"), L.MI_ERR_UNSUPPORTED, "mode"),
+    (dict(mode=b"nf4"), L.MI_ERR_UNSUPPORTED, "mode"),
+    (dict(mode=b"mxfp4", gs=L.opt(32)), L.MI_ERR_UNSUPPORTED, "uint8"),
+    (dict(mode=b"mxfp4", gs=L.opt(64)), L.MI_ERR_INVALID, "group_size=32"),
     (dict(transpose=False), L.MI_ERR_UNSUPPORTED, "transpose"),
     (dict(bits=L.opt(7)), L.MI_ERR_UNSUPPORTED, "bits"),
     (dict(bits=L.opt(3), xd=L.DT_FLOAT32), L.MI_ERR_UNSUPPORTED, "bf16 activations"),

@@ -283,3 +283,42 @@ def test_prefill_full_size_sampled_rows(dev, N, K):
     ref = xd.float() @ wf.t()
     err = (y.float() - ref).abs().max().item() / ref.abs().max().item()
     assert err <= BF16_TOL
+
+
+def _fp_weight(mode, N, K, seed):
+    m, bits, gs = O.FP_MODES[mode]
+    rng = np.random.default_rng(seed)
+    q = rng.integers(0, 1 << bits, size=(N, K)).astype(np.uint8)
+    if mode == "mxfp8":
+        q[(q & 0x7F) == 0x7F] = 0x3F  # keep codes in the finite e4m3 range
+    # e8m0 scales near 1; nvfp4's e4m3 scales positive, 2^-3 .. 2^1
+    lo, hi = (0x20, 0x48) if mode == "nvfp4" else (118, 126)
+    sc = rng.integers(lo, hi, size=(N, K // gs)).astype(np.uint8)
+    return O.pack(q, bits), sc
+
+
+@pytest.mark.parametrize("mode", ["nvfp4", "mxfp4", "mxfp8"])
+def test_dequantize_fp_modes_bit_exact(dev, mode):
+    _print_case(t="dequant_fp", mode=mode)
+    wq, sc = _fp_weight(mode, 96, 512, 7)
+    W, S = to_dev_u32(wq, dev), torch.from_numpy(sc).to(dev)
+    f32 = mi_qmm.dequantize(W, S, None, mode=mode, dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(f32.view(np.uint32), O.dequantize_fp(wq, sc, mode).view(np.uint32))
+    bf = bf16_bits(mi_qmm.dequantize(W, S, None, mode=mode))
+    assert np.array_equal(bf, O.dequantize_fp(wq, sc, mode, out_bf16=True))
+
+
+@pytest.mark.parametrize("mode", ["nvfp4", "mxfp4", "mxfp8"])
+@pytest.mark.parametrize("M,N,K", [(1, 256, 1024), (5, 96, 512), (300, 64, 384)])
+def test_qmm_fp_modes(dev, mode, M, N, K):
+    """Bias-less modes: dequantize (exact in bf16) + bf16 GEMM; truth is fp64 over the
+    oracle's exactly dequantized weight."""
+    _print_case(t="qmm_fp", mode=mode, M=M, N=N, K=K)
+    wq, sc = _fp_weight(mode, N, K, 11 + M)
+    x = O.make_x_bf16(M, K, 12 + N)
+    y = mi_qmm.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(wq, dev),
+                                torch.from_numpy(sc).to(dev), None, True, mode=mode)
+    wd = O.dequantize_fp(wq, sc, mode).astype(np.float64)
+    truth = O.bf16_to_f32(x).astype(np.float64) @ wd.T
+    assert y.shape == (M, N) and y.dtype == torch.bfloat16
+    assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
