@@ -27,9 +27,33 @@ def seed(cfg, stream, extra=0):
     return (SEED_BASE + 16 * cfg + stream + (extra << 20)) & ((1 << 64) - 1)
 
 
-def qbytes(N, K, bits, gs, M):
-    """Algorithmic bytes of one qmm call: packed W + bf16 scales/biases + x + y."""
-    return N * K * bits // 8 + 2 * (N * K // gs) * 2 + M * K * 2 + M * N * 2
+FP_MODES = {"nvfp4": (16, 4), "mxfp4": (32, 4), "mxfp8": (32, 8)}  # (group_size, bits)
+
+
+def qbytes(N, K, bits, gs, M, mode="affine"):
+    """Algorithmic bytes of one qmm call: packed W + scales (+ biases) + x + y. Affine
+    scales/biases are bf16; the fp modes have one uint8 scale per group and no biases."""
+    sb = N * K // gs if mode in FP_MODES else 2 * (N * K // gs) * 2
+    return N * K * bits // 8 + sb + M * K * 2 + M * N * 2
+
+
+def build_fp_layers(torch, n_layers, mode, dev, hidden=4096, inter=14336):
+    """Random codes and scales for a bias-less fp mode (near-unit scales; every code)."""
+    gs, bits = FP_MODES[mode]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed(2, 1))
+    lo, hi = (0x20, 0x48) if mode == "nvfp4" else (118, 126)
+
+    def one(N, K):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K * bits // 32), generator=gen,
+                          device=dev, dtype=torch.int32)
+        sc = torch.randint(lo, hi, (N, K // gs), generator=gen, device=dev, dtype=torch.uint8)
+        return (w, sc, None)
+
+    layers = [(one(inter, hidden), one(inter, hidden), one(hidden, inter))
+              for _ in range(n_layers)]
+    torch.cuda.synchronize()
+    return layers
 
 
 def make_layer_weights(torch, mi, N, K, bits, gs, sd, tmp):
@@ -64,7 +88,8 @@ def time_region(torch, fn, steps, warmup):
     return s.elapsed_time(e) / 1000.0
 
 
-def decode_mlp(torch, mi, layers, M, bits, gs, dev, steps, warmup, hidden=4096, inter=14336):
+def decode_mlp(torch, mi, layers, M, bits, gs, dev, steps, warmup, hidden=4096, inter=14336,
+               mode="affine"):
     x = torch.empty(M, hidden, dtype=torch.bfloat16, device=dev)
     h = torch.empty(M, inter, dtype=torch.bfloat16, device=dev)
     mi.fill_randn(x, seed(2, 0), 0.0, 1.0)
@@ -72,9 +97,9 @@ def decode_mlp(torch, mi, layers, M, bits, gs, dev, steps, warmup, hidden=4096, 
 
     def step():
         for (g, u, d) in layers:
-            mi.quantized_matmul(x, *g, True, gs, bits)
-            mi.quantized_matmul(x, *u, True, gs, bits)
-            mi.quantized_matmul(h, *d, True, gs, bits)
+            mi.quantized_matmul(x, *g, True, gs, bits, mode)
+            mi.quantized_matmul(x, *u, True, gs, bits, mode)
+            mi.quantized_matmul(h, *d, True, gs, bits, mode)
 
     # The 96 launches of one token are captured once in a HIP graph and replayed, so
     # the timed region measures the GPU, not Python's per-call launch overhead.
@@ -88,7 +113,7 @@ def decode_mlp(torch, mi, layers, M, bits, gs, dev, steps, warmup, hidden=4096, 
         step()
     t = time_region(torch, graph.replay, steps, warmup)
     launches = 3 * len(layers) * steps
-    per_launch = qbytes(inter, hidden, bits, gs, M)  # gate/up/down move the same bytes
+    per_launch = qbytes(inter, hidden, bits, gs, M, mode)  # gate/up/down move the same bytes
     return {"seconds": t, "launches": launches, "bytes_per_launch": per_launch,
             "avg_launch_us": t / launches * 1e6,
             "GBs": per_launch * launches / t / 1e9,
@@ -284,6 +309,8 @@ def main():
                     help="only run the configs[1] decode step at this M (for rocprofv3)")
     ap.add_argument("--bits", type=int, default=4, choices=(2, 3, 4, 5, 6, 8),
                     help="weight bits of --decode-only")
+    ap.add_argument("--mode", default="affine", choices=("affine",) + tuple(FP_MODES),
+                    help="weight format of --decode-only (fp modes: random codes and scales)")
     ap.add_argument("--prefill-only", type=int, default=0, metavar="M",
                     help="only run the configs[2] prefill shapes at this M (for rocprofv3)")
     ap.add_argument("--moe-only", type=int, default=0, choices=(0, 3, 4), metavar="CFG",
@@ -311,10 +338,15 @@ def main():
         return
     import mi_qmm as mi
     if args.decode_only:
-        layers = build_mlp_layers(torch, mi, args.layers, args.bits, 64, dev)
-        r = decode_mlp(torch, mi, layers, args.decode_only, args.bits, 64, dev, args.steps,
-                       args.warmup)
-        print(json.dumps({"M": args.decode_only, "bits": args.bits,
+        if args.mode in FP_MODES:
+            gs, bits = FP_MODES[args.mode]
+            layers = build_fp_layers(torch, args.layers, args.mode, dev)
+        else:
+            gs, bits = 64, args.bits
+            layers = build_mlp_layers(torch, mi, args.layers, bits, gs, dev)
+        r = decode_mlp(torch, mi, layers, args.decode_only, bits, gs, dev, args.steps,
+                       args.warmup, mode=args.mode)
+        print(json.dumps({"M": args.decode_only, "bits": bits, "mode": args.mode,
                           "GBs": round(r["GBs"], 1), "avg_launch_us": round(r["avg_launch_us"], 3),
                           "bytes_per_launch": r["bytes_per_launch"]}))
         return

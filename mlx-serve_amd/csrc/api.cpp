@@ -457,6 +457,12 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
     if (N > (int64_t)1 << 30 || M > (int64_t)1 << 30 || N * K * 2 > ((int64_t)1 << 34))
       return fail(MI_ERR_INVALID, "N, M or N*K too large");
     hipStream_t s = (hipStream_t)stream;
+    static const int fp_any_max = env_int("MI_QMM_ANY_MAX", 8);
+    if (M <= fp_any_max) {  // decode rows: straight from the packed codes
+      hipError_t e = mi::launch_qmv_any((const uint16_t*)x, w, scales, nullptr, (uint16_t*)y, M,
+                                        N, K, gs, nb, fm, s);
+      if (e != hipErrorNotSupported) return e == hipSuccess ? MI_OK : hip_fail(e, "qmv_any launch");
+    }
     const size_t wbytes = round256((size_t)N * K * 2);
     void* data = nullptr;
     rc = workspace(s, wbytes + mi::kDqGemmBlasWs, &data);
@@ -489,8 +495,8 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
     return fail(MI_ERR_UNSUPPORTED, "bits=%d: bf16 activations only", nb);
   static const int any_max = env_int("MI_QMM_ANY_MAX", 8);
   if (odd_width && M <= any_max) {  // decode rows: straight from the packed bitstream
-    hipError_t e = mi::launch_qmv_any((const uint16_t*)x, w, (const uint16_t*)scales,
-                                      (const uint16_t*)biases, (uint16_t*)y, M, N, K, gs, nb, s);
+    hipError_t e = mi::launch_qmv_any((const uint16_t*)x, w, scales, (const uint16_t*)biases,
+                                      (uint16_t*)y, M, N, K, gs, nb, -1, s);
     if (e != hipErrorNotSupported) return e == hipSuccess ? MI_OK : hip_fail(e, "qmv_any launch");
   }
   if (x_dtype == MI_DTYPE_BFLOAT16 && (odd_width || (dq_min > 0 && M >= dq_min)) &&

@@ -112,11 +112,12 @@ hipError_t launch_down_reduce(uint16_t* y, const uint16_t* v, const uint16_t* sc
 // nvfp4 (mode 0) / mxfp4 (1) / mxfp8 (2) dequantize, uint8 scales, no biases (quant.hip).
 hipError_t launch_dequantize_fp(void* out, const uint32_t* w, const uint8_t* s, int64_t rows,
                                 int64_t K, int mode, int out_f32, hipStream_t st);
-// Decode GEMV for 2/3/5/6-bit affine weights, 1..8 bf16 activation rows (qmv_any.hip).
-// hipErrorNotSupported when the shape is outside its scope.
-hipError_t launch_qmv_any(const uint16_t* x, const uint32_t* w, const uint16_t* s,
+// Decode GEMV for 2/3/5/6-bit affine weights (fp_mode -1, bf16 scales/biases) and the
+// nvfp4 / mxfp4 / mxfp8 modes (fp_mode 0/1/2, uint8 scales), 1..8 bf16 activation rows
+// (qmv_any.hip). hipErrorNotSupported when the shape is outside its scope.
+hipError_t launch_qmv_any(const uint16_t* x, const uint32_t* w, const void* s,
                           const uint16_t* b, uint16_t* y, int64_t M, int64_t N, int64_t K,
-                          int gs, int bits, hipStream_t st);
+                          int gs, int bits, int fp_mode, hipStream_t st);
 // Decode MoE down projection + score-weighted slot sum in one launch (moe_down.hip).
 bool moe_down_supported(int64_t T, int k, int64_t N, int64_t K, int gs, int bits, int ws, int nc);
 hipError_t launch_moe_down(uint16_t* y, const uint16_t* act, const uint32_t* w,

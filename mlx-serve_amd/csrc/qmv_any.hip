@@ -1,5 +1,7 @@
-// Decode GEMV for the affine widths without a fused matmul kernel (2, 3, 5, 6 bits), up to
-// 8 activation rows, bf16 activations and outputs, fp32 accumulation.
+// Decode GEMV for the weight formats without a fused matmul kernel, up to 8 activation rows,
+// bf16 activations and outputs, fp32 accumulation: affine 2, 3, 5 and 6 bits, and the
+// bias-less microscaling modes nvfp4 (e2m1 codes, 16-value groups, e4m3 scales), mxfp4
+// (e2m1, 32, e8m0) and mxfp8 (e4m3, 32, e8m0).
 //
 // A row of K codes is one LSB-first bitstream over little-endian words: 32 codes are
 // exactly BITS whole dwords, at dword c*BITS of the row for chunk c (the same stream as the
@@ -8,8 +10,12 @@
 // Each wave streams its 4 weight rows together: lane l takes chunks l, l+64, ... and loads
 // the chunk's BITS dwords of all 4 rows before using any, so 4*BITS loads are in flight per
 // lane. Per chunk (inside one group, gs >= 32), row and activation row:
-// acc += s * sum(x*q) + b * sum(x). The wave's lanes are summed with shuffles in a fixed
-// order.
+// acc += s * sum(x*q) + b * sum(x) (affine), acc += s * sum(x*element(q)) (fp modes; an
+// nvfp4 chunk holds two groups). The wave's lanes are summed with shuffles in a fixed
+// order. Element decoders build the fp32 bits directly (exact for every code): e2m1
+// exponent e, mantissa f -> 2^(e-1) (1 + f/2), e = 0 -> f/2; e4m3 -> 2^(e-7) (1 + f/8),
+// e = 0 -> f 2^-9, no NaN code; e8m0 -> 2^(b-127), b = 0 -> 2^-127 (the reference's
+// constructions, src/transformer.zig:20126-20142, :18918-18924).
 #include "mi_common.h"
 #include "mi_internal.h"
 
@@ -18,13 +24,26 @@ namespace {
 
 constexpr int kAnyRowsPerBlock = 16;
 
+MI_DEV float el_e2m1(uint32_t c) {
+  const uint32_t m = c & 7u, e = m >> 1, f = m & 1u;
+  const float mag = e ? __uint_as_float(((e + 126u) << 23) | (f << 22)) : 0.5f * (float)f;
+  return (c & 8u) ? -mag : mag;
+}
+MI_DEV float el_e4m3(uint32_t b) {
+  const uint32_t m = b & 0x7Fu, e = m >> 3, f = m & 7u;
+  const float mag = e ? __uint_as_float(((e + 120u) << 23) | (f << 20)) : (float)f * 0.001953125f;
+  return (b & 0x80u) ? -mag : mag;
+}
+MI_DEV float sc_e8m0(uint32_t b) { return b ? __uint_as_float(b << 23) : __uint_as_float(0x00400000u); }
+
 MI_DEV float bf_lo(uint32_t v) { return __uint_as_float(v << 16); }
 MI_DEV float bf_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
 
-template <int BITS, int MR>
+// FPM: -1 affine (bf16 scales and biases), 0 nvfp4, 1 mxfp4, 2 mxfp8 (uint8 scales).
+template <int BITS, int MR, int FPM = -1>
 __global__ void __launch_bounds__(256) qmv_any_kernel(const uint16_t* __restrict__ x,
                                                       const uint32_t* __restrict__ w,
-                                                      const uint16_t* __restrict__ s,
+                                                      const void* __restrict__ s,
                                                       const uint16_t* __restrict__ b,
                                                       uint16_t* __restrict__ y, int M, int N,
                                                       int K, int gs) {
@@ -55,11 +74,18 @@ __global__ void __launch_bounds__(256) qmv_any_kernel(const uint16_t* __restrict
 #pragma unroll
       for (int j = 0; j < BITS; ++j) wd[rr][j] = w[nr[rr] * wpr + (int64_t)c * BITS + j];
     const int g = (32 * c) / gs;
-    float sc[4], bi[4];
+    float sc[4], sc2[4], bi[4];
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      sc[rr] = bf16_bits_to_f32(s[(int64_t)nr[rr] * G + g]);
-      bi[rr] = bf16_bits_to_f32(b[(int64_t)nr[rr] * G + g]);
+      if constexpr (FPM < 0) {
+        sc[rr] = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(s)[(int64_t)nr[rr] * G + g]);
+        bi[rr] = bf16_bits_to_f32(b[(int64_t)nr[rr] * G + g]);
+      } else {
+        const uint8_t* s8 = reinterpret_cast<const uint8_t*>(s) + (int64_t)nr[rr] * G + g;
+        sc[rr] = FPM == 0 ? el_e4m3(s8[0]) : sc_e8m0(s8[0]);
+        sc2[rr] = FPM == 0 ? el_e4m3(s8[1]) : sc[rr];  // nvfp4: codes 16..31 are the next group
+        bi[rr] = 0.f;
+      }
     }
     float sx[MR];
 #pragma unroll
@@ -82,14 +108,20 @@ __global__ void __launch_bounds__(256) qmv_any_kernel(const uint16_t* __restrict
         const int o = j * BITS, wi = o >> 5, sh = o & 31;
         uint32_t v = wd[rr][wi] >> sh;
         if (sh + BITS > 32) v |= wd[rr][wi + 1] << (32 - sh);
-        q[j] = (float)(v & MASK);
+        if constexpr (FPM == 2) q[j] = el_e4m3(v & MASK);
+        else if constexpr (FPM >= 0) q[j] = el_e2m1(v & MASK);
+        else q[j] = (float)(v & MASK);
       }
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
         if (m < M) {
-          float d = 0.f;
+          float d = 0.f, dh = 0.f;  // dh: codes 16..31 of an nvfp4 chunk
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
+            if (FPM == 0 && t == 2) {
+              dh = d;
+              d = 0.f;
+            }
             const u32x4_t xv = xs[m * np + 4 * c + t];
             d = fmaf(bf_lo(xv.x), q[8 * t + 0], d);
             d = fmaf(bf_hi(xv.x), q[8 * t + 1], d);
@@ -100,7 +132,9 @@ __global__ void __launch_bounds__(256) qmv_any_kernel(const uint16_t* __restrict
             d = fmaf(bf_lo(xv.w), q[8 * t + 6], d);
             d = fmaf(bf_hi(xv.w), q[8 * t + 7], d);
           }
-          acc[rr][m] = fmaf(sc[rr], d, fmaf(bi[rr], sx[m], acc[rr][m]));
+          if constexpr (FPM == 0) acc[rr][m] = fmaf(sc2[rr], d, fmaf(sc[rr], dh, acc[rr][m]));
+          else if constexpr (FPM > 0) acc[rr][m] = fmaf(sc[rr], d, acc[rr][m]);
+          else acc[rr][m] = fmaf(sc[rr], d, fmaf(bi[rr], sx[m], acc[rr][m]));
         }
       }
     }
@@ -116,17 +150,17 @@ __global__ void __launch_bounds__(256) qmv_any_kernel(const uint16_t* __restrict
     }
 }
 
-template <int BITS>
-void launch_mr(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+template <int BITS, int FPM = -1>
+void launch_mr(const uint16_t* x, const uint32_t* w, const void* s, const uint16_t* b,
                uint16_t* y, int M, int N, int K, int gs, size_t lds, hipStream_t st) {
   const dim3 grid((unsigned)((N + kAnyRowsPerBlock - 1) / kAnyRowsPerBlock)), block(256);
 #define MI_ANY(MRV)                                                                             \
   do {                                                                                          \
     static const bool attr = hipFuncSetAttribute(                                               \
-        reinterpret_cast<const void*>(&qmv_any_kernel<BITS, MRV>),                              \
+        reinterpret_cast<const void*>(&qmv_any_kernel<BITS, MRV, FPM>),                              \
         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;                  \
     (void)attr; /* a failure shows as a launch error above 64 KiB */                           \
-    hipLaunchKernelGGL((qmv_any_kernel<BITS, MRV>), grid, block, lds, st, x, w, s, b, y, M, N, \
+    hipLaunchKernelGGL((qmv_any_kernel<BITS, MRV, FPM>), grid, block, lds, st, x, w, s, b, y, M, N, \
                        K, gs);                                                                  \
   } while (0)
   if (M <= 1) MI_ANY(1);
@@ -138,13 +172,22 @@ void launch_mr(const uint16_t* x, const uint32_t* w, const uint16_t* s, const ui
 
 }  // namespace
 
-hipError_t launch_qmv_any(const uint16_t* x, const uint32_t* w, const uint16_t* s,
+hipError_t launch_qmv_any(const uint16_t* x, const uint32_t* w, const void* s,
                           const uint16_t* b, uint16_t* y, int64_t M, int64_t N, int64_t K,
-                          int gs, int bits, hipStream_t st) {
+                          int gs, int bits, int fp_mode, hipStream_t st) {
   const size_t lds = (size_t)M * K * 2;
-  if (M < 1 || M > 8 || K % 32 || gs < 32 || lds > 160 * 1024 || N >= ((int64_t)1 << 31) ||
-      (uintptr_t)x % 16)
+  if (M < 1 || M > 8 || K % 32 || (fp_mode < 0 && gs < 32) || lds > 160 * 1024 ||
+      N >= ((int64_t)1 << 31) || (uintptr_t)x % 16)
     return hipErrorNotSupported;
+  if (fp_mode >= 0) {
+    switch (fp_mode) {
+      case 0: launch_mr<4, 0>(x, w, s, b, y, (int)M, (int)N, (int)K, 16, lds, st); break;
+      case 1: launch_mr<4, 1>(x, w, s, b, y, (int)M, (int)N, (int)K, 32, lds, st); break;
+      case 2: launch_mr<8, 2>(x, w, s, b, y, (int)M, (int)N, (int)K, 32, lds, st); break;
+      default: return hipErrorNotSupported;
+    }
+    return hipGetLastError();
+  }
   switch (bits) {
     case 2: launch_mr<2>(x, w, s, b, y, (int)M, (int)N, (int)K, gs, lds, st); break;
     case 3: launch_mr<3>(x, w, s, b, y, (int)M, (int)N, (int)K, gs, lds, st); break;
