@@ -36,6 +36,23 @@ MI_DEV float el_e4m3(uint32_t b) {
 }
 MI_DEV float sc_e8m0(uint32_t b) { return b ? __uint_as_float(b << 23) : __uint_as_float(0x00400000u); }
 
+// e2m1 codes to bf16 by byte tables: for 4 codes held one per byte (magnitude bits 0-2,
+// sign bit 3), v_perm_b32 picks each magnitude's bf16 high byte (00 3F 3F 3F 40 40 40 40)
+// and low byte (00 00 80 C0 00 40 80 C0) at once; the sign goes to bit 7 of the high byte.
+// Two more permutes interleave them into bf16 pairs (bytes 0,1) and (bytes 2,3).
+typedef __bf16 bf16x2a __attribute__((ext_vector_type(2)));
+MI_DEV float dot2a(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2a, a),
+                                         __builtin_bit_cast(bf16x2a, b), c, false);
+}
+MI_DEV void e2m1_pairs(uint32_t codes4, uint32_t& p01, uint32_t& p23) {
+  const uint32_t m = codes4 & 0x07070707u;
+  const uint32_t hb = perm_b32(0x40404040u, 0x3F3F3F00u, m) | ((codes4 & 0x08080808u) << 4);
+  const uint32_t lb = perm_b32(0xC0804000u, 0xC0800000u, m);
+  p01 = perm_b32(hb, lb, 0x05010400u);
+  p23 = perm_b32(hb, lb, 0x07030602u);
+}
+
 MI_DEV float bf_lo(uint32_t v) { return __uint_as_float(v << 16); }
 MI_DEV float bf_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
 
@@ -51,7 +68,16 @@ __global__ void __launch_bounds__(256) qmv_any_kernel(const uint16_t* __restrict
   u32x4_t* xs = reinterpret_cast<u32x4_t*>(smem);  // [M][K/8] units of 8 bf16
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int np = K / 8;
-  for (int i = tid; i < M * np; i += blockDim.x) xs[i] = reinterpret_cast<const u32x4_t*>(x)[i];
+  constexpr bool FP4 = FPM == 0 || FPM == 1;  // e2m1 codes: byte-table decode, dot2
+  for (int i = tid; i < M * np; i += blockDim.x) {
+    const u32x4_t X = reinterpret_cast<const u32x4_t*>(x)[i];
+    if constexpr (FP4) {  // pair order (x0,x2) (x4,x6) (x1,x3) (x5,x7): even / odd nibbles
+      xs[i] = u32x4_t{perm_b32(X.y, X.x, 0x05040100u), perm_b32(X.w, X.z, 0x05040100u),
+                      perm_b32(X.y, X.x, 0x07060302u), perm_b32(X.w, X.z, 0x07060302u)};
+    } else {
+      xs[i] = X;
+    }
+  }
   __syncthreads();
   constexpr uint32_t MASK = (1u << BITS) - 1u;
   const int nch = K / 32;                   // 32-code chunks per row
@@ -91,7 +117,7 @@ __global__ void __launch_bounds__(256) qmv_any_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       sx[m] = 0.f;
-      if (m < M) {
+      if (FPM < 0 && m < M) {  // the bias term: affine only
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const u32x4_t xv = xs[m * np + 4 * c + t];
@@ -99,6 +125,39 @@ __global__ void __launch_bounds__(256) qmv_any_kernel(const uint16_t* __restrict
                    ((bf_lo(xv.z) + bf_hi(xv.z)) + (bf_lo(xv.w) + bf_hi(xv.w)));
         }
       }
+    }
+    if constexpr (FP4) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        uint32_t a[4][4];  // per dword t of the chunk: (x0,x2) (x4,x6) (x1,x3) (x5,x7) weights
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t wv = wd[rr][t];
+          e2m1_pairs(wv & 0x0F0F0F0Fu, a[t][0], a[t][1]);
+          e2m1_pairs((wv >> 4) & 0x0F0F0F0Fu, a[t][2], a[t][3]);
+        }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          if (m < M) {
+            float d = 0.f, dh = 0.f;  // dh: the chunk's first 16 codes (nvfp4's first group)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              if (FPM == 0 && t == 2) {
+                dh = d;
+                d = 0.f;
+              }
+              const u32x4_t xv = xs[m * np + 4 * c + t];
+              d = dot2a(a[t][0], xv.x, d);
+              d = dot2a(a[t][1], xv.y, d);
+              d = dot2a(a[t][2], xv.z, d);
+              d = dot2a(a[t][3], xv.w, d);
+            }
+            if constexpr (FPM == 0) acc[rr][m] = fmaf(sc2[rr], d, fmaf(sc[rr], dh, acc[rr][m]));
+            else acc[rr][m] = fmaf(sc[rr], d, acc[rr][m]);
+          }
+        }
+      }
+      continue;
     }
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
