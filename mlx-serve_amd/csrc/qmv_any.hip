@@ -127,33 +127,42 @@ __global__ void __launch_bounds__(256) qmv_any_kernel(const uint16_t* __restrict
       }
     }
     if constexpr (FP4) {
+      // all 4 rows' decoded weights first, so each staged activation read serves 4 rows
+      uint32_t a[4][4][4];  // [row][dword t][(x0,x2) (x4,x6) (x1,x3) (x5,x7)]
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        uint32_t a[4][4];  // per dword t of the chunk: (x0,x2) (x4,x6) (x1,x3) (x5,x7) weights
+      for (int rr = 0; rr < 4; ++rr)
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const uint32_t wv = wd[rr][t];
-          e2m1_pairs(wv & 0x0F0F0F0Fu, a[t][0], a[t][1]);
-          e2m1_pairs((wv >> 4) & 0x0F0F0F0Fu, a[t][2], a[t][3]);
+          e2m1_pairs(wv & 0x0F0F0F0Fu, a[rr][t][0], a[rr][t][1]);
+          e2m1_pairs((wv >> 4) & 0x0F0F0F0Fu, a[rr][t][2], a[rr][t][3]);
         }
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-          if (m < M) {
-            float d = 0.f, dh = 0.f;  // dh: the chunk's first 16 codes (nvfp4's first group)
+      for (int m = 0; m < MR; ++m) {
+        if (m < M) {
+          float d[4] = {0.f, 0.f, 0.f, 0.f}, dh[4];  // dh: nvfp4's first group of the chunk
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              if (FPM == 0 && t == 2) {
-                dh = d;
-                d = 0.f;
+          for (int t = 0; t < 4; ++t) {
+            if (FPM == 0 && t == 2) {
+#pragma unroll
+              for (int rr = 0; rr < 4; ++rr) {
+                dh[rr] = d[rr];
+                d[rr] = 0.f;
               }
-              const u32x4_t xv = xs[m * np + 4 * c + t];
-              d = dot2a(a[t][0], xv.x, d);
-              d = dot2a(a[t][1], xv.y, d);
-              d = dot2a(a[t][2], xv.z, d);
-              d = dot2a(a[t][3], xv.w, d);
             }
-            if constexpr (FPM == 0) acc[rr][m] = fmaf(sc2[rr], d, fmaf(sc[rr], dh, acc[rr][m]));
-            else acc[rr][m] = fmaf(sc[rr], d, acc[rr][m]);
+            const u32x4_t xv = xs[m * np + 4 * c + t];
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+              d[rr] = dot2a(a[rr][t][0], xv.x, d[rr]);
+              d[rr] = dot2a(a[rr][t][1], xv.y, d[rr]);
+              d[rr] = dot2a(a[rr][t][2], xv.z, d[rr]);
+              d[rr] = dot2a(a[rr][t][3], xv.w, d[rr]);
+            }
+          }
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            if constexpr (FPM == 0) acc[rr][m] = fmaf(sc2[rr], d[rr], fmaf(sc[rr], dh[rr], acc[rr][m]));
+            else acc[rr][m] = fmaf(sc[rr], d[rr], acc[rr][m]);
           }
         }
       }
