@@ -289,8 +289,9 @@ def _fp_weight(mode, N, K, seed):
     m, bits, gs = O.FP_MODES[mode]
     rng = np.random.default_rng(seed)
     q = rng.integers(0, 1 << bits, size=(N, K)).astype(np.uint8)
-    if mode == "mxfp8":
-        q[(q & 0x7F) == 0x7F] = 0x3F  # keep codes in the finite e4m3 range
+    if mode == "mxfp8":  # a few 0x7F / 0xFF codes: +-480 in the reference's decoder
+        q[(q & 0x7F) == 0x7F] = 0x3F
+        q[0, 3], q[1, 40], q[N - 1, K - 1] = 0x7F, 0xFF, 0x7F
     # e8m0 scales near 1; nvfp4's e4m3 scales positive, 2^-3 .. 2^1
     lo, hi = (0x20, 0x48) if mode == "nvfp4" else (118, 126)
     sc = rng.integers(lo, hi, size=(N, K // gs)).astype(np.uint8)
