@@ -423,6 +423,32 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
                   int64_t n_experts, bool transpose, mi_optional_int group_size,
                   mi_optional_int bits, const char* mode, bool sorted_indices, int x_dtype,
                   int sb_dtype, void* stream) {
+  const int fm = fp_mode_of(mode);
+  if (fm >= 0 || (bits.has_value && bits.value != 4 && bits.value != 8 && fm == -1)) {
+    // nvfp4 / mxfp4 / mxfp8 and affine 2/3/5/6 bits: one block column per pair of the
+    // few-row decode kernel, up to 8 rows per pair
+    int gs = 0, nb = 0;
+    int rc = fm >= 0 ? resolve_fp(fm, group_size, bits, transpose, K, sb_dtype, &gs, &nb)
+                     : resolve_common(group_size, bits, mode, transpose, K, &gs, &nb);
+    if (rc) return rc;
+    if (fm < 0 && sb_dtype != MI_DTYPE_BFLOAT16)
+      return fail(MI_ERR_UNSUPPORTED, "scales/biases dtype %d not supported", sb_dtype);
+    if (x_dtype != MI_DTYPE_BFLOAT16)
+      return fail(MI_ERR_UNSUPPORTED, "gather_qmm at this format: bf16 activations only");
+    if (n_idx < 0 || M < 0 || N < 0 || x_batch < 0 || n_experts < 0 || lhs_div <= 0)
+      return fail(MI_ERR_INVALID, "negative size or lhs_div <= 0");
+    if (n_idx == 0 || M == 0 || N == 0) return MI_OK;
+    if (!y || !x || !w || !scales || (fm < 0 && !biases))
+      return fail(MI_ERR_INVALID, "null tensor pointer");
+    hipError_t e = mi::launch_qmv_any_gather(
+        (const uint16_t*)x, w, scales, fm < 0 ? (const uint16_t*)biases : nullptr, (uint16_t*)y,
+        M, N, K, gs, nb, fm, lhs_indices, rhs_indices, n_idx, lhs_div, x_batch, n_experts,
+        (hipStream_t)stream);
+    if (e == hipErrorNotSupported)
+      return fail(MI_ERR_UNSUPPORTED, "gather_qmm at this format: up to 8 rows per pair, "
+                  "65535 pairs and K*rows*2 <= 160 KiB");
+    return e == hipSuccess ? MI_OK : hip_fail(e, "qmv_any gather launch");
+  }
   GatherJob J;
   int rc = gather_prepare(J, y, x, w, scales, biases, lhs_indices, rhs_indices, n_idx, lhs_div,
                           x_batch, M, N, K, n_experts, transpose, group_size, bits, mode,

@@ -118,6 +118,14 @@ hipError_t launch_dequantize_fp(void* out, const uint32_t* w, const uint8_t* s, 
 hipError_t launch_qmv_any(const uint16_t* x, const uint32_t* w, const void* s,
                           const uint16_t* b, uint16_t* y, int64_t M, int64_t N, int64_t K,
                           int gs, int bits, int fp_mode, hipStream_t st);
+// The same kernel over gather pairs: block column i computes x[lhs(i)] @ W[rhs(i)]^T into
+// y[i] (lhs(i) = lhs ? lhs[i] : i / lhs_div, rhs(i) = rhs ? rhs[i] : i; out-of-range ids
+// give NaN rows).
+hipError_t launch_qmv_any_gather(const uint16_t* x, const uint32_t* w, const void* s,
+                                 const uint16_t* b, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                                 int gs, int bits, int fp_mode, const uint32_t* lhs,
+                                 const uint32_t* rhs, int64_t n_pairs, int64_t lhs_div,
+                                 int64_t x_batch, int64_t n_experts, hipStream_t st);
 // Decode MoE down projection + score-weighted slot sum in one launch (moe_down.hip).
 bool moe_down_supported(int64_t T, int k, int64_t N, int64_t K, int gs, int bits, int ws, int nc);
 hipError_t launch_moe_down(uint16_t* y, const uint16_t* act, const uint32_t* w,

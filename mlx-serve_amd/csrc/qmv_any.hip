@@ -24,6 +24,15 @@ namespace {
 
 constexpr int kAnyRowsPerBlock = 16;
 
+// Gathers: block column y is pair i, lhs(i) = lhs ? lhs[i] : i / lhs_div, expert
+// rhs(i) = rhs ? rhs[i] : i; an lhs >= x_batch or an expert >= n_experts gives NaN rows.
+// Dense calls are the single pair (0, 0).
+struct AnyGather {
+  const uint32_t* lhs;
+  const uint32_t* rhs;
+  int64_t lhs_div, x_batch, n_experts;
+};
+
 MI_DEV float el_e2m1(uint32_t c) {
   const uint32_t m = c & 7u, e = m >> 1, f = m & 1u;
   const float mag = e ? __uint_as_float(((e + 126u) << 23) | (f << 22)) : 0.5f * (float)f;
@@ -63,11 +72,29 @@ __global__ void __launch_bounds__(256) qmv_any_kernel(const uint16_t* __restrict
                                                       const void* __restrict__ s,
                                                       const uint16_t* __restrict__ b,
                                                       uint16_t* __restrict__ y, int M, int N,
-                                                      int K, int gs) {
+                                                      int K, int gs, AnyGather A) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   u32x4_t* xs = reinterpret_cast<u32x4_t*>(smem);  // [M][K/8] units of 8 bf16
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int np = K / 8;
+  {
+    const int64_t i = blockIdx.y;
+    const int64_t li = A.lhs ? (int64_t)A.lhs[i] : i / A.lhs_div;
+    const int64_t e = A.rhs ? (int64_t)A.rhs[i] : i;
+    y += i * M * N;
+    if (li >= A.x_batch || e >= A.n_experts) {  // block-uniform
+      for (int o = tid; o < M * kAnyRowsPerBlock; o += blockDim.x) {
+        const int m = o / kAnyRowsPerBlock, n = blockIdx.x * kAnyRowsPerBlock + o % kAnyRowsPerBlock;
+        if (n < N) y[(int64_t)m * N + n] = 0x7FC0u;  // bf16 NaN
+      }
+      return;
+    }
+    const int64_t G0 = (int64_t)N * (K / gs);  // scale entries per expert
+    x += li * M * K;
+    w += e * N * ((int64_t)K * BITS / 32);
+    s = reinterpret_cast<const uint8_t*>(s) + e * G0 * (FPM < 0 ? 2 : 1);
+    if (b) b += e * G0;
+  }
   constexpr bool FP4 = FPM == 0 || FPM == 1;  // e2m1 codes: byte-table decode, dot2
   for (int i = tid; i < M * np; i += blockDim.x) {
     const u32x4_t X = reinterpret_cast<const u32x4_t*>(x)[i];
@@ -220,8 +247,9 @@ __global__ void __launch_bounds__(256) qmv_any_kernel(const uint16_t* __restrict
 
 template <int BITS, int FPM = -1>
 void launch_mr(const uint16_t* x, const uint32_t* w, const void* s, const uint16_t* b,
-               uint16_t* y, int M, int N, int K, int gs, size_t lds, hipStream_t st) {
-  const dim3 grid((unsigned)((N + kAnyRowsPerBlock - 1) / kAnyRowsPerBlock)), block(256);
+               uint16_t* y, int M, int N, int K, int gs, size_t lds, const AnyGather& A,
+               unsigned n_pairs, hipStream_t st) {
+  const dim3 grid((unsigned)((N + kAnyRowsPerBlock - 1) / kAnyRowsPerBlock), n_pairs), block(256);
 #define MI_ANY(MRV)                                                                             \
   do {                                                                                          \
     static const bool attr = hipFuncSetAttribute(                                               \
@@ -229,7 +257,7 @@ void launch_mr(const uint16_t* x, const uint32_t* w, const void* s, const uint16
         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;                  \
     (void)attr; /* a failure shows as a launch error above 64 KiB */                           \
     hipLaunchKernelGGL((qmv_any_kernel<BITS, MRV, FPM>), grid, block, lds, st, x, w, s, b, y, M, N, \
-                       K, gs);                                                                  \
+                       K, gs, A);                                                               \
   } while (0)
   if (M <= 1) MI_ANY(1);
   else if (M <= 2) MI_ANY(2);
@@ -240,30 +268,42 @@ void launch_mr(const uint16_t* x, const uint32_t* w, const void* s, const uint16
 
 }  // namespace
 
-hipError_t launch_qmv_any(const uint16_t* x, const uint32_t* w, const void* s,
-                          const uint16_t* b, uint16_t* y, int64_t M, int64_t N, int64_t K,
-                          int gs, int bits, int fp_mode, hipStream_t st) {
+hipError_t launch_qmv_any_gather(const uint16_t* x, const uint32_t* w, const void* s,
+                                 const uint16_t* b, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                                 int gs, int bits, int fp_mode, const uint32_t* lhs,
+                                 const uint32_t* rhs, int64_t n_pairs, int64_t lhs_div,
+                                 int64_t x_batch, int64_t n_experts, hipStream_t st) {
   const size_t lds = (size_t)M * K * 2;
   if (M < 1 || M > 8 || K % 32 || (fp_mode < 0 && gs < 32) || lds > 160 * 1024 ||
-      N >= ((int64_t)1 << 31) || (uintptr_t)x % 16)
+      N >= ((int64_t)1 << 31) || (uintptr_t)x % 16 || n_pairs < 1 || n_pairs > 65535 ||
+      lhs_div < 1)
     return hipErrorNotSupported;
+  const AnyGather A{lhs, rhs, lhs_div, x_batch, n_experts};
+  const unsigned np = (unsigned)n_pairs;
   if (fp_mode >= 0) {
     switch (fp_mode) {
-      case 0: launch_mr<4, 0>(x, w, s, b, y, (int)M, (int)N, (int)K, 16, lds, st); break;
-      case 1: launch_mr<4, 1>(x, w, s, b, y, (int)M, (int)N, (int)K, 32, lds, st); break;
-      case 2: launch_mr<8, 2>(x, w, s, b, y, (int)M, (int)N, (int)K, 32, lds, st); break;
+      case 0: launch_mr<4, 0>(x, w, s, b, y, (int)M, (int)N, (int)K, 16, lds, A, np, st); break;
+      case 1: launch_mr<4, 1>(x, w, s, b, y, (int)M, (int)N, (int)K, 32, lds, A, np, st); break;
+      case 2: launch_mr<8, 2>(x, w, s, b, y, (int)M, (int)N, (int)K, 32, lds, A, np, st); break;
       default: return hipErrorNotSupported;
     }
     return hipGetLastError();
   }
   switch (bits) {
-    case 2: launch_mr<2>(x, w, s, b, y, (int)M, (int)N, (int)K, gs, lds, st); break;
-    case 3: launch_mr<3>(x, w, s, b, y, (int)M, (int)N, (int)K, gs, lds, st); break;
-    case 5: launch_mr<5>(x, w, s, b, y, (int)M, (int)N, (int)K, gs, lds, st); break;
-    case 6: launch_mr<6>(x, w, s, b, y, (int)M, (int)N, (int)K, gs, lds, st); break;
+    case 2: launch_mr<2>(x, w, s, b, y, (int)M, (int)N, (int)K, gs, lds, A, np, st); break;
+    case 3: launch_mr<3>(x, w, s, b, y, (int)M, (int)N, (int)K, gs, lds, A, np, st); break;
+    case 5: launch_mr<5>(x, w, s, b, y, (int)M, (int)N, (int)K, gs, lds, A, np, st); break;
+    case 6: launch_mr<6>(x, w, s, b, y, (int)M, (int)N, (int)K, gs, lds, A, np, st); break;
     default: return hipErrorNotSupported;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_qmv_any(const uint16_t* x, const uint32_t* w, const void* s,
+                          const uint16_t* b, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                          int gs, int bits, int fp_mode, hipStream_t st) {
+  return launch_qmv_any_gather(x, w, s, b, y, M, N, K, gs, bits, fp_mode, nullptr, nullptr, 1, 1,
+                               1, 1, st);
 }
 
 }  // namespace mi

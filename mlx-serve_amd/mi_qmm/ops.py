@@ -133,7 +133,7 @@ def gather_qmm(x, w, scales, biases, lhs_indices=None, rhs_indices=None, transpo
     _require(x.dim() >= 2 and w.dim() >= 2, "x and w need at least 2 dims")
     K = x.shape[-1]
     M = x.shape[-2]
-    gs, nb = _resolve(_packed(w), scales, group_size, bits, K)
+    gs, nb = _resolve(_packed(w), scales, group_size, bits, K, mode)
     N = w.shape[-2]
     lhs, lhs_div, rhs, shape = _broadcast_indices(x, w, lhs_indices, rhs_indices)
     n_idx = math.prod(shape)

@@ -92,14 +92,44 @@ def test_qmm_other_widths(dev, M, N, K, bits, gs):
     assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
 
 
-def test_gather_other_widths_decline(dev):
-    _print_case(t="gather_width_decline")
-    wq, s, b = weights(2, 32, 256, 3, 64, 5)
-    x = O.make_x_bf16(1, 256, 6).reshape(1, 1, 256)
-    with pytest.raises(Exception, match="bits=3"):
-        mi_qmm.gather_qmm(to_dev_bf16(x, dev), to_dev_u32(wq, dev), to_dev_bf16(s, dev),
-                          to_dev_bf16(b, dev), rhs_indices=to_dev_u32(np.array([1], np.uint32), dev),
-                          group_size=64, bits=3)
+@pytest.mark.parametrize("bits", [3, 5, 6])
+def test_gather_other_widths(dev, bits):
+    """2/3/5/6-bit gathers: one token broadcast over its slots, one slot out of range
+    (NaN row); truth is the oracle's fp64 gather."""
+    _print_case(t="gather_width", bits=bits)
+    E, N, K, T, k = 4, 48, 256, 3, 2
+    wq, s, b = weights(E, N, K, bits, 64, 5 + bits)
+    x = O.make_x_bf16(T, K, 6)
+    inds = np.array([[1, 3], [0, E + 2], [2, 2]], np.uint32)
+    y = mi_qmm.gather_qmm(to_dev_bf16(x, dev).reshape(T, 1, 1, K), to_dev_u32(wq, dev),
+                          to_dev_bf16(s, dev), to_dev_bf16(b, dev),
+                          rhs_indices=to_dev_u32(inds, dev), group_size=64, bits=bits)
+    yf = to_f64(y).reshape(T * k, 1, N)
+    assert np.isnan(yf[3]).all()
+    ok = inds.reshape(-1).copy()
+    ok[3] = 0
+    truth = O.gather_qmm_f64(x.reshape(T, 1, K), wq, s, b, None, ok, T * k, lhs_div=k,
+                             group_size=64, bits=bits)
+    keep = [0, 1, 2, 4, 5]
+    assert max_err_ratio(yf[keep], truth[keep]) <= BF16_TOL
+
+
+@pytest.mark.parametrize("mode", ["nvfp4", "mxfp4", "mxfp8"])
+def test_gather_fp_modes(dev, mode):
+    _print_case(t="gather_fp", mode=mode)
+    E, N, K, T = 3, 40, 512, 4
+    banks = [_fp_weight(mode, N, K, 30 + e) for e in range(E)]
+    wq = np.stack([bk[0] for bk in banks])
+    sc = np.stack([bk[1] for bk in banks])
+    x = O.make_x_bf16(T * 2, K, 31).reshape(T, 2, K)  # 2 rows per pair
+    rhs = np.array([2, 0, 1, 2], np.uint32)
+    y = mi_qmm.gather_qmm(to_dev_bf16(x, dev), to_dev_u32(wq, dev), torch.from_numpy(sc).to(dev),
+                          None, lhs_indices=to_dev_u32(np.arange(T, dtype=np.uint32), dev),
+                          rhs_indices=to_dev_u32(rhs, dev), mode=mode)
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    truth = np.stack([xf[i] @ O.dequantize_fp(wq[rhs[i]], sc[rhs[i]], mode).astype(np.float64).T
+                      for i in range(T)])
+    assert max_err_ratio(to_f64(y).reshape(T, 2, N), truth) <= BF16_TOL
 
 
 @pytest.mark.parametrize("bits", [4, 8])
