@@ -24,8 +24,22 @@ TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_host.cpp")
 TEST_BIN = os.path.join(ROOT, "tests", "cpp", "_build", "test_host")
 
 
-def _compile(src):
+def _stale(src, obj):
+    """True when obj is older than src or than any header under csrc/, host/, include/."""
+    if not os.path.exists(obj):
+        return True
+    newest = os.path.getmtime(os.path.join(HERE, src))
+    for d in (os.path.join(HERE, "csrc"), HOST, os.path.join(ROOT, "include")):
+        for f in os.listdir(d):
+            if f.endswith((".h", ".hpp")):
+                newest = max(newest, os.path.getmtime(os.path.join(d, f)))
+    return newest > os.path.getmtime(obj)
+
+
+def _compile(src, incremental=False):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    if incremental and not _stale(src, obj):
+        return obj
     cmd = [HIPCC] + FLAGS + ["-c", os.path.join(HERE, src), "-o", obj]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
@@ -37,11 +51,12 @@ def _compile(src):
     return obj
 
 
-def build(verbose=True):
+def build(verbose=True, incremental=False):
+    """Compile every source (incremental=True skips objects newer than their inputs)."""
     os.makedirs(BUILD, exist_ok=True)
     srcs = [s for s in SOURCES if os.path.exists(os.path.join(HERE, s))]
     with cf.ThreadPoolExecutor(max_workers=min(os.cpu_count() or 8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda s: _compile(s, incremental), srcs))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs + [
         "-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
@@ -72,5 +87,5 @@ def build_host_tests(verbose=True):
 
 
 if __name__ == "__main__":
-    build()
+    build(incremental="-i" in sys.argv[1:])
     sys.exit(0)

@@ -134,6 +134,7 @@ int env_int(const char* name, int dflt) {
 struct QmvPlan {
   mi::QmvConfig cfg;
   int row_blocks, ks, gps;
+  bool ok = true;  // false: no (waves, K range) split fits the LDS budget
 };
 
 size_t lds_per_block() {
@@ -170,14 +171,24 @@ QmvPlan qmv_plan(int N, int K, int gs, int bits, int rows, int64_t n_items, int 
   if (ks > nch) ks = nch;
   if (ks < 1) ks = 1;
   if (env_ks > 0) ks = env_ks < nch ? env_ks : nch;
+  // Whole chunks per range keep every wave's DMA aligned to 256-byte rows; the LDS check
+  // uses that rounded range. When even one-chunk ranges do not fit, fewer waves share
+  // the block's LDS.
+  const int ks0 = ks;
   for (;;) {
-    const int gps = ceil_div(G, ks);
-    if (mi::qmv_lds_bytes(gps, gs, mr, x_f32, w) <= lds_max || ks >= G) break;
-    ++ks;
+    p.gps = std::min(G, ceil_div(ceil_div(G, ks), ug) * ug);
+    if (mi::qmv_lds_bytes(p.gps, gs, mr, x_f32, w) <= lds_max) break;
+    if (p.gps > ug) {
+      ++ks;
+      continue;
+    }
+    if (w == 1) {
+      p.ok = false;
+      break;
+    }
+    w >>= 1;
+    ks = ks0;
   }
-  // Whole chunks per range keep every wave's DMA aligned to 256-byte rows.
-  p.gps = ceil_div(ceil_div(G, ks), ug) * ug;
-  if (p.gps > G) p.gps = G;
   p.ks = ceil_div(G, p.gps);
   p.cfg.waves = w;
   p.row_blocks = ceil_div(tiles, w);
@@ -202,18 +213,21 @@ QmvPlan qmv16_plan(int N, int K, int gs, int bits, int rows, int64_t n_items, in
   if (env_w >= 1 && env_w <= 8) w = env_w;
   if (w > nch) w = nch;
   int ks = 1;
+  // K ranges start on 8-group boundaries (aligned scale runs); the LDS check uses that
+  // rounded range.
   for (;;) {
-    const int gps = ceil_div(G, ks);
-    if (mi::qmv16_lds_bytes(gps, gs, bits, mp, x_f32, w) <= lds_max) break;
+    p.gps = ks == 1 ? G : std::min(G, ceil_div(ceil_div(G, ks), 8) * 8);
+    if (mi::qmv16_lds_bytes(p.gps, gs, bits, mp, x_f32, w) <= lds_max) break;
     if (w > 1) {
       w >>= 1;
       continue;
     }
-    if (ks >= G) break;
+    if (p.gps <= 8) {
+      p.ok = false;
+      break;
+    }
     ++ks;
   }
-  // K ranges start on 8-group boundaries (aligned scale runs).
-  p.gps = ks == 1 ? G : ceil_div(ceil_div(G, ks), 8) * 8;
   p.ks = ceil_div(G, p.gps);
   p.cfg.waves = w;
   p.row_blocks = tiles;
@@ -353,10 +367,17 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
                   mi::qmvm_plan(item_rows, P.N, P.K, gs, nb, n_items, &J.planm);
     J.plan = J.narrow ? qmv16_plan(P.N, P.K, gs, nb, item_rows, n_items, P.x_f32)
                       : qmv_plan(P.N, P.K, gs, nb, item_rows, n_items, P.x_f32);
+    if (!J.multi_row && !J.plan.ok)
+      return fail(MI_ERR_UNSUPPORTED, "gather_qmm: %d rows per item of K=%d do not fit LDS",
+                  item_rows, P.K);
     P.ks = J.multi_row ? J.planm.ks : J.plan.ks;
     P.gps = J.plan.gps;
     P.row_blocks = J.plan.row_blocks;
   }
+  // The split reduce indexes outputs with 32-bit math.
+  if (P.ks > 1 && PT * N >= ((int64_t)1 << 32))
+    return fail(MI_ERR_UNSUPPORTED, "gather_qmm: K-split output of %lld elements exceeds 2^32",
+                (long long)(PT * N));
   J.items_bytes = J.use_items ? (size_t)J.max_items * 16 + 256 : 0;
   J.part_bytes = P.ks > 1 ? (size_t)P.ks * PT * N * 4 : 0;
   return MI_OK;

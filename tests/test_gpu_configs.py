@@ -1,0 +1,288 @@
+"""GPU parity at the exact workloads BASELINE.json names (configs[0..4]): the same
+shapes, bit widths and kernel plans the benchmark times, checked through the C ABI
+against the CPU oracle.
+
+Weights are generated on the device (mi_fill_randn + mi_quantize, both bit-exact
+against the oracle in test_gpu_qmm.py) and the packed triples are copied back to the
+host, so the oracle computes truth from exactly the bytes the kernels read.
+Tolerances: bf16 output max-abs-err <= 1e-2*||y||inf, fp32 output <= 1e-3*||y||inf,
+against fp64 truth; index work is bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import BF16_TOL, F32_TOL, bf16_bits, max_err_ratio, to_dev_bf16, to_f64
+import mi_qmm
+
+pytestmark = pytest.mark.gpu
+
+SEED_BASE = 0x4D49333500000000
+
+
+def seed(cfg, stream, extra=0):
+    return (SEED_BASE + 16 * cfg + stream + (extra << 20)) & ((1 << 64) - 1)
+
+
+def _case(**kw):
+    print("CASE", kw, flush=True)
+
+
+def dev_weight(dev, rows, K, bits, sd, gs=64):
+    """W ~ N(0, 0.02) as bf16 on the device, quantized there: (wq, s, b) device tensors."""
+    tmp = torch.empty(rows, K, dtype=torch.bfloat16, device=dev)
+    mi_qmm.fill_randn(tmp, sd, 0.0, 0.02)
+    out = mi_qmm.quantize(tmp, gs, bits)
+    del tmp
+    return out
+
+
+def host(wq, s, b):
+    """Device triple -> numpy (uint32 codes, bf16-bits scales, bf16-bits biases)."""
+    return (wq.cpu().numpy().view(np.uint32), bf16_bits(s), bf16_bits(b))
+
+
+def dev_x(dev, M, K, sd, dtype=torch.bfloat16):
+    x = torch.empty(M, K, dtype=dtype, device=dev)
+    mi_qmm.fill_randn(x, sd, 0.0, 1.0)
+    return x
+
+
+def host_x(x):
+    return bf16_bits(x) if x.dtype == torch.bfloat16 else x.cpu().numpy()
+
+
+# ------------------------------------------------------------------ configs[0] --
+def test_config0_single_qmv(dev):
+    """x [1,4096] bf16 against 4-bit g64 W [4096,4096]; whole output."""
+    _case(t="cfg0")
+    W = dev_weight(dev, 4096, 4096, 4, seed(1, 1))
+    x = dev_x(dev, 1, 4096, seed(1, 0))
+    y = mi_qmm.quantized_matmul(x, *W, True, 64, 4)
+    truth = O.qmm_f64(host_x(x), *host(*W), 64, 4)
+    assert y.shape == (1, 4096) and y.dtype == torch.bfloat16
+    assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+
+
+# ------------------------------------------------------------------ configs[1] --
+DECODE_MS = (1, 2, 4, 8, 16, 32)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("N,K,name", [(14336, 4096, "gate_up"), (4096, 14336, "down")])
+def test_config1_decode_sweep(dev, N, K, name, bits):
+    """the Llama-3-8B MLP shapes at every decode M, whole output against the
+    oracle. Rows are independent, so the truth of the first M rows is a prefix of the
+    32-row truth; each M runs the kernel plan the benchmark times at that M."""
+    _case(t="cfg1", name=name, bits=bits)
+    W = dev_weight(dev, N, K, bits, seed(2, 1, 7 + bits))
+    x = dev_x(dev, 32, K, seed(2, 0, bits))
+    truth = O.qmm_f64(host_x(x), *host(*W), 64, bits)
+    for M in DECODE_MS:
+        _case(t="cfg1", name=name, bits=bits, M=M)
+        y = mi_qmm.quantized_matmul(x[:M].contiguous(), *W, True, 64, bits)
+        assert y.shape == (M, N)
+        err = max_err_ratio(to_f64(y), truth[:M])
+        assert err <= BF16_TOL, (M, err)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_config1_fp32_activations_long_k(dev, bits):
+    """fp32 activations at K = 14336 (the down projection), where the affine
+    refactoring sum(x*(128+q)) - 128*s*sum(x) cancels the most: 1e-3 relative."""
+    _case(t="cfg1_f32", bits=bits)
+    N, K = 4096, 14336
+    W = dev_weight(dev, N, K, bits, seed(2, 1, 20 + bits))
+    x = dev_x(dev, 32, K, seed(2, 0, 30 + bits), torch.float32)
+    truth = O.qmm_f64(host_x(x), *host(*W), 64, bits)
+    for M in (1, 4, 32):
+        _case(t="cfg1_f32", bits=bits, M=M)
+        y = mi_qmm.quantized_matmul(x[:M].contiguous(), *W, True, 64, bits)
+        assert y.dtype == torch.float32
+        err = max_err_ratio(y.cpu().numpy().astype(np.float64), truth[:M])
+        assert err <= F32_TOL, (M, err)
+
+
+# ------------------------------------------------------------------ configs[2] --
+def _stratified_rows(M, per_tile=2, tile=256, seed_=0):
+    """Rows covering every 256-row tile: its first and last row, plus random ones."""
+    rng = np.random.default_rng(seed_)
+    rows = set()
+    for t0 in range(0, M, tile):
+        t1 = min(M, t0 + tile)
+        rows.update((t0, t1 - 1))
+        rows.update(int(r) for r in rng.integers(t0, t1, size=per_tile))
+    return np.array(sorted(rows))
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
+def test_config2_prefill(dev, N, K):
+    """M = 512 / 2048 / 8192 at full size. Every output column and every
+    256-row tile is checked against the oracle on stratified rows."""
+    W = dev_weight(dev, N, K, 4, seed(3, 1, N))
+    Wh = host(*W)
+    for M in (512, 2048, 8192):
+        _case(t="cfg2", N=N, K=K, M=M)
+        x = dev_x(dev, M, K, seed(3, 0, M))
+        y = mi_qmm.quantized_matmul(x, *W, True, 64, 4)
+        assert y.shape == (M, N)
+        rows = _stratified_rows(M, per_tile=1 if M > 2048 else 2, seed_=M)
+        truth = O.qmm_f64(bf16_bits(x[torch.from_numpy(rows).to(dev)]), *Wh, 64, 4)
+        err = max_err_ratio(to_f64(y)[rows], truth)
+        assert err <= BF16_TOL, (M, err)
+        del x, y
+
+
+# --------------------------------------------------------------- MoE helpers --
+def route(dev, T, E, k, sd, skew_seed=None):
+    logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+    mi_qmm.fill_randn(logits, sd, 0.0, 1.0)
+    if skew_seed is not None:  # 10% of tokens pushed onto 8 fixed hot experts
+        g = torch.Generator().manual_seed(skew_seed & 0x7FFFFFFF)
+        hot = torch.randperm(E, generator=g)[:8]
+        pick = torch.rand(T, generator=g) < 0.1
+        bump = torch.zeros(T, E)
+        bump[:, hot] = 8.0
+        logits += (bump * pick[:, None]).to(dev)
+    inds, sc = mi_qmm.moe_route_topk(logits, k, torch.bfloat16)
+    ri, _ = O.route_softmax_topk(logits.cpu().numpy(), k)
+    assert np.array_equal(inds.cpu().numpy().view(np.uint32), ri)
+    return inds, sc
+
+
+def bank_host_experts(bank, experts):
+    """Copy only the listed experts of a device bank to the host (dict by expert)."""
+    wq, s, b = bank
+    return {int(e): host(wq[int(e)], s[int(e)], b[int(e)]) for e in set(experts)}
+
+
+def sampled_gather_check(y_pairs, x_h, lhs, srt, bank, picks):
+    """y_pairs[p] vs truth for the pairs p in picks: x_h[lhs[p]] @ W[srt[p]]^T."""
+    hb = bank_host_experts(bank, srt[picks])
+    for p in picks:
+        e = int(srt[p])
+        t = O.qmm_f64(x_h[lhs[p]:lhs[p] + 1], *hb[e], 64, 4)[0]
+        err = max_err_ratio(y_pairs[p], t)
+        assert err <= BF16_TOL, (int(p), e, err)
+
+
+def moe_bank(dev, E, N, K, bits, sd):
+    wq, s, b = dev_weight(dev, E * N, K, bits, sd)
+    return wq.view(E, N, -1), s.view(E, N, -1), b.view(E, N, -1)
+
+
+def check_decode_moe(dev, G, U, D, x, inds, sc, k):
+    """T=1 fused entry points: gate+up+SwiGLU and down+score-reduce against the split
+    calls (bit-equal) and each gather against the oracle."""
+    T, hidden = x.shape
+    act = mi_qmm.gather_qmv_gate_up_swiglu(x, *G, *U, inds, 64, 4)
+    y = mi_qmm.gather_qmv_down_reduce(act, *D, inds, sc, 64, 4)
+    xs = x.view(T, 1, 1, hidden)  # one token broadcast over its k slots
+    g = mi_qmm.gather_qmm(xs, *G, rhs_indices=inds.view(T, k), group_size=64, bits=4)
+    u = mi_qmm.gather_qmm(xs, *U, rhs_indices=inds.view(T, k), group_size=64, bits=4)
+    a = mi_qmm.swiglu(g, u)
+    assert np.array_equal(bf16_bits(a).reshape(-1), bf16_bits(act).reshape(-1))
+    v = mi_qmm.gather_qmm(act.view(T * k, 1, -1), *D, rhs_indices=inds.view(-1),
+                          group_size=64, bits=4)
+    y2 = mi_qmm.moe_down_reduce(v.view(T, k, -1), sc)
+    assert np.array_equal(bf16_bits(y), bf16_bits(y2))
+    e = inds.cpu().numpy().view(np.uint32).reshape(-1)
+    xh = bf16_bits(x)
+    lhs = np.repeat(np.arange(T), k)
+    for bank, out, xin in ((G, g, xh), (U, u, xh), (D, v, bf16_bits(act).reshape(T * k, -1))):
+        src = lhs if xin is xh else np.arange(T * k)
+        sampled_gather_check(to_f64(out).reshape(T * k, -1), xin, src, e, bank,
+                             np.arange(T * k))
+
+
+def check_sorted_moe(dev, G, U, D, x, inds, sc, k, E, n_pick, seed_):
+    """Sorted prefill pipeline (sort dispatch -> 3 sorted gathers -> take -> reduce):
+    dispatch bit-exact against the oracle, sampled pairs of every gather against the
+    oracle, and the sorted results equal the unsorted path's after the inverse take."""
+    T, hidden = x.shape
+    flat = inds.reshape(-1)
+    order, inv, srt, lhs, seg = mi_qmm.moe_sort_dispatch(flat, k, E)
+    fh = flat.cpu().numpy().view(np.uint32)
+    ro, ri, rs, rl = O.sort_dispatch(fh, k)
+    for a, r in ((order, ro), (inv, ri), (srt, rs), (lhs, rl)):
+        assert np.array_equal(a.cpu().numpy().view(np.uint32), r)
+    xs = x.view(T, 1, hidden)
+    kw = dict(group_size=64, bits=4, sorted_indices=True)
+    g = mi_qmm.gather_qmm(xs, *G, lhs_indices=lhs, rhs_indices=srt, **kw)
+    u = mi_qmm.gather_qmm(xs, *U, lhs_indices=lhs, rhs_indices=srt, **kw)
+    a = mi_qmm.swiglu(g, u)
+    v = mi_qmm.gather_qmm(a, *D, rhs_indices=srt, **kw)
+    picks = np.random.default_rng(seed_).choice(T * k, size=min(n_pick, T * k), replace=False)
+    xh = bf16_bits(x)
+    sampled_gather_check(to_f64(g).reshape(T * k, -1), xh, rl, rs, G, picks)
+    sampled_gather_check(to_f64(u).reshape(T * k, -1), xh, rl, rs, U, picks)
+    sampled_gather_check(to_f64(v).reshape(T * k, -1), bf16_bits(a).reshape(T * k, -1),
+                         np.arange(T * k), rs, D, picks)
+    vb = mi_qmm.take_rows(v.view(T * k, hidden), inv)
+    y = mi_qmm.moe_down_reduce(vb.view(T, k, hidden), sc)
+    # same products through the unsorted path, in (token, slot) order
+    gu = mi_qmm.gather_qmm(x.view(T, 1, 1, hidden), *G, rhs_indices=inds.view(T, k),
+                           group_size=64, bits=4)
+    assert max_err_ratio(to_f64(gu).reshape(T * k, -1)[ro],
+                         to_f64(g).reshape(T * k, -1)) <= BF16_TOL
+    assert torch.isfinite(y.float()).all()
+
+
+# ------------------------------------------------------------------ configs[3] --
+@pytest.fixture(scope="module")
+def qwen_banks(dev):
+    E, hidden, inter = 128, 2048, 768
+    return (moe_bank(dev, E, inter, hidden, 4, seed(4, 1, 1)),
+            moe_bank(dev, E, inter, hidden, 4, seed(4, 1, 2)),
+            moe_bank(dev, E, hidden, inter, 4, seed(4, 1, 3)))
+
+
+def test_config3_moe_decode(dev, qwen_banks):
+    _case(t="cfg3", T=1)
+    G, U, D = qwen_banks
+    x = dev_x(dev, 1, 2048, seed(4, 0, 1))
+    inds, sc = route(dev, 1, 128, 8, seed(4, 2, 1))
+    check_decode_moe(dev, G, U, D, x, inds, sc, 8)
+
+
+def test_config3_moe_prefill(dev, qwen_banks):
+    _case(t="cfg3", T=512)
+    G, U, D = qwen_banks
+    x = dev_x(dev, 512, 2048, seed(4, 0, 512))
+    inds, sc = route(dev, 512, 128, 8, seed(4, 2, 512))
+    check_sorted_moe(dev, G, U, D, x, inds, sc, 8, 128, 96, 3)
+
+
+# ------------------------------------------------------------------ configs[4] --
+@pytest.fixture(scope="module")
+def dsv3_banks(dev):
+    E, hidden, inter = 256, 7168, 2048
+    return (moe_bank(dev, E, inter, hidden, 4, seed(5, 1, 1)),
+            moe_bank(dev, E, inter, hidden, 4, seed(5, 1, 2)),
+            moe_bank(dev, E, hidden, inter, 4, seed(5, 1, 3)))
+
+
+@pytest.mark.parametrize("T", [1, 8, 64])
+def test_config4_moe(dev, dsv3_banks, T):
+    _case(t="cfg4", T=T)
+    G, U, D = dsv3_banks
+    x = dev_x(dev, T, 7168, seed(5, 0, T))
+    inds, sc = route(dev, T, 256, 8, seed(5, 2, T), skew_seed=seed(5, 3))
+    if T == 1:
+        check_decode_moe(dev, G, U, D, x, inds, sc, 8)
+    else:
+        check_sorted_moe(dev, G, U, D, x, inds, sc, 8, 256, 40, T)
+
+
+@pytest.mark.parametrize("T", [1, 8, 64])
+def test_config4_shared_expert_8bit(dev, T):
+    """configs[4]'s shared expert: 8-bit g64 dense (2048,7168) x2 and (7168,2048)."""
+    _case(t="cfg4_shared", T=T)
+    for (N, K, st) in ((2048, 7168, 4), (7168, 2048, 6)):
+        W = dev_weight(dev, N, K, 8, seed(5, 1, st))
+        x = dev_x(dev, T, K, seed(5, 0, 100 + T + st))
+        y = mi_qmm.quantized_matmul(x, *W, True, 64, 8)
+        truth = O.qmm_f64(bf16_bits(x), *host(*W), 64, 8)
+        err = max_err_ratio(to_f64(y), truth)
+        assert err <= BF16_TOL, (N, K, err)
