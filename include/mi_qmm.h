@@ -88,6 +88,23 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
                   mi_optional_int bits, const char* mode, bool sorted_indices, int x_dtype,
                   int sb_dtype, void* stream);
 
+/* mi_gather_qmm without any device allocation. No counterpart in the reference: it is
+ * for callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, results and kernels as
+ * mi_gather_qmm; its work items and K-split partials live in a fixed per-device scratch
+ * array of MI_GATHER_NOALLOC_SCRATCH_BYTES (64 MiB) inside the library, held until the
+ * process ends. A call that would need more returns MI_ERR_WORKSPACE. Every call on a
+ * device shares that device's scratch: calls that overlap on one device (different
+ * streams, or concurrent host threads) race and must not be issued. */
+#define MI_GATHER_NOALLOC_SCRATCH_BYTES ((int64_t)64 << 20)
+int mi_gather_qmm_noalloc(void* y, const void* x, const uint32_t* w, const void* scales,
+                          const void* biases, const uint32_t* lhs_indices,
+                          const uint32_t* rhs_indices, int64_t n_idx, int64_t lhs_div,
+                          int64_t x_batch, int64_t M, int64_t N, int64_t K, int64_t n_experts,
+                          bool transpose, mi_optional_int group_size, mi_optional_int bits,
+                          const char* mode, bool sorted_indices, int x_dtype, int sb_dtype,
+                          void* stream);
+
 /* Replaces mlx_dequantize (src/mlx.zig:271), mode "affine", no global scale:
  *   out[r,k] = scale[r,k/gs] * q[r,k] + bias[r,k/gs]
  * Modes "nvfp4" / "mxfp4" / "mxfp8" (uint8 scales, no biases): out = element(q) *

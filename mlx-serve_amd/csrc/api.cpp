@@ -18,6 +18,13 @@
 
 #include "mi_internal.h"
 
+// Fixed scratch of mi_gather_qmm_noalloc: work items and K-split partials of one call.
+// Each device holds its own copy for the life of the process; host code reaches it only
+// through the address hipGetSymbolAddress returns for the current device (the name
+// itself is a host-side stand-in, never a device address).
+static constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 namespace {
 
 thread_local std::string g_err;
@@ -117,6 +124,25 @@ int workspace(hipStream_t s, size_t bytes, void** data) {
     w.size = want;
   }
   *data = w.data;
+  return MI_OK;
+}
+
+std::mutex g_scratch_mu;
+std::map<int, void*> g_scratch;  // device -> device address of `scratch`
+
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch.find(dev);
+  if (it == g_scratch.end()) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    it = g_scratch.emplace(dev, ptr).first;
+  }
+  *out = it->second;
   return MI_OK;
 }
 
@@ -482,6 +508,36 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
     if (rc) return rc;
   }
   return gather_launch(J, data, s);
+}
+
+int mi_gather_qmm_noalloc(void* y, const void* x, const uint32_t* w, const void* scales,
+                          const void* biases, const uint32_t* lhs_indices,
+                          const uint32_t* rhs_indices, int64_t n_idx, int64_t lhs_div,
+                          int64_t x_batch, int64_t M, int64_t N, int64_t K, int64_t n_experts,
+                          bool transpose, mi_optional_int group_size, mi_optional_int bits,
+                          const char* mode, bool sorted_indices, int x_dtype, int sb_dtype,
+                          void* stream) {
+  // The scratch address is resolved (once per device) before anything else, so a first
+  // call made under stream capture still finds it.
+  void* data = nullptr;
+  int rc = scratch_address(&data);
+  if (rc) return rc;
+  const int fm = fp_mode_of(mode);
+  if (fm >= 0 || (bits.has_value && bits.value != 4 && bits.value != 8 && fm == -1))
+    // the odd-width and fp-mode gathers use no scratch: the allocating entry point
+    // allocates nothing on that path
+    return mi_gather_qmm(y, x, w, scales, biases, lhs_indices, rhs_indices, n_idx, lhs_div,
+                         x_batch, M, N, K, n_experts, transpose, group_size, bits, mode,
+                         sorted_indices, x_dtype, sb_dtype, stream);
+  GatherJob J;
+  rc = gather_prepare(J, y, x, w, scales, biases, lhs_indices, rhs_indices, n_idx, lhs_div,
+                      x_batch, M, N, K, n_experts, transpose, group_size, bits, mode,
+                      sorted_indices, x_dtype, sb_dtype);
+  if (rc || J.empty) return rc;
+  if (J.ws_bytes() > kNoAllocScratchBytes)
+    return fail(MI_ERR_WORKSPACE, "gather_qmm_noalloc: the call needs %zu bytes of scratch, "
+                "the fixed maximum is %zu", J.ws_bytes(), kNoAllocScratchBytes);
+  return gather_launch(J, data, (hipStream_t)stream);
 }
 
 int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,

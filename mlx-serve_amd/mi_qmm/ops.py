@@ -126,9 +126,12 @@ def _broadcast_indices(x, w, lhs_indices, rhs_indices):
 
 
 def gather_qmm(x, w, scales, biases, lhs_indices=None, rhs_indices=None, transpose=True,
-               group_size=None, bits=None, mode="affine", sorted_indices=False):
+               group_size=None, bits=None, mode="affine", sorted_indices=False, out=None,
+               noalloc=False):
     """out[i] = x[lhs[i]] @ dequantize(w[rhs[i]]).T (mlx_gather_qmm, src/mlx.zig:265).
-    x [..., M, K], w [..., N, K*bits/32]; out shape = broadcast(lhs, rhs) + [M, N]."""
+    x [..., M, K], w [..., N, K*bits/32]; out shape = broadcast(lhs, rhs) + [M, N].
+    noalloc=True calls mi_gather_qmm_noalloc (fixed library scratch, no device
+    allocation inside the library); `out` may supply the result tensor."""
     _contig(x, w, scales, biases)
     _require(x.dim() >= 2 and w.dim() >= 2, "x and w need at least 2 dims")
     K = x.shape[-1]
@@ -139,12 +142,14 @@ def gather_qmm(x, w, scales, biases, lhs_indices=None, rhs_indices=None, transpo
     n_idx = math.prod(shape)
     x_batch = x.numel() // (M * K) if M * K else 0
     n_exp = w.numel() // (N * w.shape[-1]) if N * w.shape[-1] else 0
-    y = torch.empty(tuple(shape) + (M, N), dtype=x.dtype, device=x.device)
-    check(lib().mi_gather_qmm(_ptr(y), _ptr(x), _ptr(w), _ptr(scales), _ptr(biases), _ptr(lhs),
-                              _ptr(rhs), n_idx, lhs_div, x_batch, M, N, K, n_exp,
-                              bool(transpose), opt(gs), opt(nb),
-                              mode.encode() if mode else None, bool(sorted_indices),
-                              _dtype_code(x, "x"), _dtype_code(scales, "scales"), _stream(x)))
+    y = torch.empty(tuple(shape) + (M, N), dtype=x.dtype, device=x.device) if out is None else out
+    _require(tuple(y.shape) == tuple(shape) + (M, N) and y.dtype == x.dtype and y.is_contiguous(),
+             "out has the wrong shape, dtype or layout")
+    fn = lib().mi_gather_qmm_noalloc if noalloc else lib().mi_gather_qmm
+    check(fn(_ptr(y), _ptr(x), _ptr(w), _ptr(scales), _ptr(biases), _ptr(lhs), _ptr(rhs), n_idx,
+             lhs_div, x_batch, M, N, K, n_exp, bool(transpose), opt(gs), opt(nb),
+             mode.encode() if mode else None, bool(sorted_indices), _dtype_code(x, "x"),
+             _dtype_code(scales, "scales"), _stream(x)))
     return y
 
 
