@@ -204,8 +204,16 @@ int mi_gather_qmv_down_reduce(void* y, const void* act, const uint32_t* w_down,
 
 /* Grow the per-device workspace (sorted work lists, K-split partials) to at least
  * `bytes` ahead of HIP graph capture; calls that fit never allocate. No mlx-c
- * counterpart (MLX owns its allocator). Synchronizes the device when it grows. */
+ * counterpart (MLX owns its allocator). Growing allocates a new buffer and keeps the
+ * outgrown one allocated (graphs captured earlier still use it) until
+ * mi_workspace_release. */
 int mi_workspace_reserve(int64_t bytes, void* stream);
+
+/* Free the workspace generations this device has outgrown. Growing never frees the
+ * previous buffer, because a HIP graph captured while it was current keeps its address;
+ * call this only when no such graph will be replayed again. Synchronizes the device when
+ * there is something to free. No mlx-c counterpart (MLX owns its allocator). */
+int mi_workspace_release(void* stream);
 
 /* Thread-local text of the last non-zero return on this thread ("" if none). */
 const char* mi_last_error(void);

@@ -17,6 +17,7 @@
 #include <utility>
 
 #include "mi_internal.h"
+#include "workspace_pool.h"
 
 // Fixed scratch of mi_gather_qmm_noalloc: work items and K-split partials of one call.
 // Each device holds its own copy for the life of the process; host code reaches it only
@@ -92,38 +93,30 @@ int resolve_fp(int fm, mi_optional_int gs_in, mi_optional_int bits_in, bool tran
 // Per-device scratch for sorted work lists and K-split partials. Calls on one
 // stream are ordered, so reuse by later calls is safe; calls that overlap on
 // different streams of one device must not both use it. It only grows outside
-// stream capture (mi_workspace_reserve sizes it up front).
-struct Workspace {
-  void* data = nullptr;
-  size_t size = 0;
-};
+// stream capture (mi_workspace_reserve sizes it up front), and an outgrown generation
+// stays allocated until mi_workspace_release: graphs captured earlier keep its address.
 std::mutex g_ws_mu;
-std::map<int, Workspace> g_ws;
+std::map<int, mi::GrowOnlyBuffer> g_ws;
 
 int workspace(hipStream_t s, size_t bytes, void** data) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   std::lock_guard<std::mutex> lk(g_ws_mu);
-  Workspace& w = g_ws[dev];
-  if (w.size < bytes) {
+  mi::GrowOnlyBuffer& w = g_ws[dev];
+  if (w.size() < bytes || !w.data()) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
       return fail(MI_ERR_WORKSPACE, "workspace too small during stream capture "
                   "(call mi_workspace_reserve before capturing)");
-    if (w.data) {
-      e = hipDeviceSynchronize();  // queued work may still use the old buffer
-      if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
-      (void)hipFree(w.data);
-      w.data = nullptr;
-      w.size = 0;
-    }
-    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes + bytes / 4;
-    e = hipMalloc(&w.data, want);
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
-    w.size = want;
+    hipError_t ae = hipSuccess;
+    const int rc = w.grow(bytes, [&](void** p, size_t n) {
+      ae = hipMalloc(p, n);
+      return ae == hipSuccess ? 0 : 1;
+    });
+    if (rc) return hip_fail(ae, "hipMalloc(workspace)");
   }
-  *data = w.data;
+  *data = w.data();
   return MI_OK;
 }
 
@@ -443,6 +436,20 @@ int mi_workspace_reserve(int64_t bytes, void* stream) {
   if (bytes < 0) return fail(MI_ERR_INVALID, "negative size");
   void* d = nullptr;
   return workspace((hipStream_t)stream, (size_t)bytes, &d);
+}
+
+int mi_workspace_release(void* stream) {
+  (void)stream;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  auto it = g_ws.find(dev);
+  if (it == g_ws.end() || it->second.retired_count() == 0) return MI_OK;
+  e = hipDeviceSynchronize();  // queued work may still use a retired generation
+  if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+  it->second.release_retired([](void* p) { (void)hipFree(p); });
+  return MI_OK;
 }
 
 const char* mi_version(void) { return "mi_qmm 0.1 gfx950"; }

@@ -62,6 +62,7 @@ def lib():
                                             OptInt, s, P]
     L.mi_gather_qmm_noalloc.argtypes = L.mi_gather_qmm.argtypes
     L.mi_workspace_reserve.argtypes = [i64, P]
+    L.mi_workspace_release.argtypes = [P]
     L.mi_last_error.restype = ctypes.c_char_p
     L.mi_version.restype = ctypes.c_char_p
     for name in EXTRA_SIGNATURES:

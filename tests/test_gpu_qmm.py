@@ -353,3 +353,40 @@ def test_qmm_fp_modes(dev, mode, M, N, K):
     truth = O.bf16_to_f32(x).astype(np.float64) @ wd.T
     assert y.shape == (M, N) and y.dtype == torch.bfloat16
     assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+
+
+def test_graph_replay_after_workspace_growth(dev):
+    """A sorted gather captured in a HIP graph keeps its workspace address; a later,
+    larger uncaptured call grows the workspace, and every replay of the old graph must
+    still match the eager result (the outgrown buffer stays allocated until
+    mi_workspace_release)."""
+    _print_case(t="ws_growth")
+    E, N, K, T, topk = 8, 64, 8192, 64, 4
+    wq, s, b = weights(E, N, K, 4, 64, 401)
+    flat = np.random.default_rng(402).integers(0, E, size=T * topk).astype(np.uint32)
+    _, _, srt, lhs = O.sort_dispatch(flat, topk)
+    x = to_dev_bf16(O.make_x_bf16(T, K, 403).reshape(T, 1, K), dev)
+    args = (to_dev_u32(wq, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev))
+    kw = dict(lhs_indices=to_dev_u32(lhs, dev), rhs_indices=to_dev_u32(srt, dev), group_size=64,
+              bits=4, sorted_indices=True)
+    eager = bf16_bits(mi_qmm.gather_qmm(x, *args, **kw))
+    out = torch.empty(T * topk, 1, N, dtype=torch.bfloat16, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mi_qmm.gather_qmm(x, *args, out=out, **kw)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        mi_qmm.gather_qmm(x, *args, out=out, **kw)
+    # grow the workspace past anything earlier tests needed
+    mi_qmm.workspace_reserve(1 << 30)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(out), eager)
+    del g
+    torch.cuda.synchronize()
+    mi_qmm._lib.check(mi_qmm._lib.lib().mi_workspace_release(None))
+    assert np.array_equal(bf16_bits(mi_qmm.gather_qmm(x, *args, **kw)), eager)
