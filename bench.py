@@ -120,14 +120,89 @@ def decode_mlp(torch, mi, layers, M, bits, gs, dev, steps, warmup, hidden=4096, 
             "tokens_per_s": M * steps / t}
 
 
+def single_qmv(torch, mi, dev, reps=50, warmup=5):
+    """one 4-bit g64 qmv x [1,4096] @ W [4096,4096]^T. Reports the eager
+    single-call latency (event-timed call on an idle GPU, median) and the rate over
+    rotated copies (>= 512 MB in one graph, so each call streams its weight from HBM)."""
+    N = K = 4096
+    bits, gs = 4, 64
+    per = qbytes(N, K, bits, gs, 1)
+    copies = -(-512 * 10 ** 6 // per)
+    tmp = torch.empty(N, K, dtype=torch.bfloat16, device=dev)
+    Ws = []
+    for c in range(copies):
+        mi.fill_randn(tmp, seed(1, 1, c), 0.0, 0.02)
+        Ws.append(mi.quantize(tmp, gs, bits))
+    del tmp
+    x = torch.empty(1, K, dtype=torch.bfloat16, device=dev)
+    mi.fill_randn(x, seed(1, 0), 0.0, 1.0)
+    for _ in range(warmup):
+        mi.quantized_matmul(x, *Ws[0], True, gs, bits)
+    torch.cuda.synchronize()
+    lat = []
+    for r in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        mi.quantized_matmul(x, *Ws[r % copies], True, gs, bits)
+        b.record()
+        torch.cuda.synchronize()
+        lat.append(a.elapsed_time(b) * 1e3)
+    lat.sort()
+
+    def all_copies():
+        for W in Ws:
+            mi.quantized_matmul(x, *W, True, gs, bits)
+    t = graph_time(torch, all_copies, 10, 2) / copies
+    return {"cfg0_single_call_latency_us": round(lat[len(lat) // 2], 2),
+            "cfg0_rotated_us_per_call": round(t * 1e6, 3),
+            "cfg0_rotated_GBs": round(per / t / 1e9, 1),
+            "cfg0_rotated_copies": copies}
+
+
+def cpu_info():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return model, os.cpu_count() or 1, avail
+
+
+def check_sample(torch, layers, x, y_fn, bits, gs, hidden=4096):
+    """Bench-time correctness gate: the first layer's gate output for the benchmark's own
+    x against the C oracle (fp64), before any number is reported."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as O
+    g = layers[0][0]
+    y = y_fn(x, g)
+    wq = g[0].cpu().numpy().view(np.uint32)
+    s = g[1].cpu().view(torch.int16).numpy().view(np.uint16)
+    b = g[2].cpu().view(torch.int16).numpy().view(np.uint16)
+    xh = x.cpu().view(torch.int16).numpy().view(np.uint16)
+    truth = O.qmm_f64(xh, wq, s, b, gs, bits)
+    err = float(np.max(np.abs(y.float().cpu().numpy() - truth)) / np.max(np.abs(truth)))
+    if not err <= 1e-2:
+        raise SystemExit(f"bench correctness gate failed: rel-err {err:.3e}")
+    return err
+
+
 def cpu_baseline(torch, layers, bits, gs, hidden=4096, inter=14336, budget_s=10.0):
     """Time the C oracle's fp32 qmv (a C restatement of MLX CPU semantics, not MLX)
     on host cores over a bounded sample: the first layers' weights copied to host."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle as O
-    threads = min(16, os.cpu_count() or 1)
-    n_l = min(2, len(layers))
+    model, ncpu, avail = cpu_info()
+    threads = min(16, avail)  # the GPU box's CPU share is 16 threads
+    n_l = min(4, len(layers))
     host = []
     for (g, u, d) in layers[:n_l]:
         host.append([tuple(t.cpu().view(torch.int16 if t.element_size() == 2 else torch.int32)
@@ -147,8 +222,10 @@ def cpu_baseline(torch, layers, bits, gs, hidden=4096, inter=14336, budget_s=10.
     t = time.perf_counter() - t0
     per = qbytes(inter, hidden, bits, gs, 1)
     return {"value": per * done / t / 1e12, "unit": "TB/s", "cores": threads, "kind": "port",
+            "cpu_model": model, "nproc": ncpu, "affinity_cpus": avail, "threads": threads,
             "sample": f"{done} qmv calls (M=1, 4-bit g64, Llama-3-8B MLP shapes) over the first "
-                      f"{n_l} layers' weights, {t:.1f} s, C oracle mo_qmm_f32 with OpenMP"}
+                      f"{n_l} layers' weights, {t:.1f} s, C oracle mo_qmm_f32 (fp32, C "
+                      f"restatement of MLX CPU semantics, not MLX) with {threads} OpenMP threads"}
 
 
 def graph_time(torch, fn, replays, warmup=2):
@@ -304,7 +381,7 @@ def main():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--decode-only", type=int, default=0, metavar="M",
                     help="only run the configs[1] decode step at this M (for rocprofv3)")
     ap.add_argument("--bits", type=int, default=4, choices=(2, 3, 4, 5, 6, 8),
@@ -367,6 +444,10 @@ def main():
     bits, gs = 4, 64
     layers = build_mlp_layers(torch, mi, args.layers, bits, gs, dev)
     head = decode_mlp(torch, mi, layers, 1, bits, gs, dev, args.steps, args.warmup)
+    xg = torch.empty(1, 4096, dtype=torch.bfloat16, device=dev)
+    mi.fill_randn(xg, seed(2, 0), 0.0, 1.0)
+    gate_err = check_sample(torch, layers, xg,
+                            lambda x, g: mi.quantized_matmul(x, *g, True, gs, bits), bits, gs)
 
     extra = {}
     if not args.no_extra:
@@ -383,6 +464,7 @@ def main():
             extra[f"q8_M{M}_tok_s"] = round(r["tokens_per_s"], 1)
         del layers8
         torch.cuda.empty_cache()
+        extra.update(single_qmv(torch, mi, dev))
         extra.update(prefill(torch, mi, dev, (512, 2048, 8192)))
         extra.update(moe_layer(torch, mi, dev, 3, 128, 2048, 768, 8, (1, 512)))
         extra.update(moe_layer(torch, mi, dev, 4, 256, 7168, 2048, 8, (1, 8, 64), skew=True))
@@ -392,7 +474,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         if layers is None:
-            layers = build_mlp_layers(torch, mi, 2, bits, gs, dev)
+            layers = build_mlp_layers(torch, mi, 4, bits, gs, dev)
         cpu = cpu_baseline(torch, layers, bits, gs, budget_s=args.cpu_seconds)
 
     ms_per_step = head["seconds"] / args.steps * 1e3
@@ -414,7 +496,8 @@ def main():
                                "(gate/up [14336,4096], down [4096,14336]), 4-bit g64, M=1",
                    "global_batch": 1, "layers": args.layers, "pct_of_hbm_peak":
                    round(100.0 * head["GBs"] / HBM_PEAK_GBS, 2),
-                   "tokens_per_s": round(head["tokens_per_s"], 1)},
+                   "tokens_per_s": round(head["tokens_per_s"], 1),
+                   "gate_rel_err_vs_oracle": float(f"{gate_err:.3e}")},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": pmc_traffic(), "kernel": "mi::qmv1_kernel<64, NC, XU, true> (dense M=1 instances)",
