@@ -599,7 +599,25 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   // prefillDqGemm shape, src/transformer.zig:20987-21011); below the threshold the fused
   // dequant-in-register kernel is faster.
   // 2/3/5/6-bit weights take this path at every M (no fused kernel for those widths).
+  // 4-bit weights at M >= MI_QMM_PREFILL_MIN (default 128): the fused prefill kernel
+  // (prefill.hip). Dequantize + hipBLASLt is opt-in (MI_QMM_DQGEMM=1) for 4/8 bits.
   static const int dq_min = env_int("MI_QMM_DQGEMM_MIN", 256);
+  static const int use_dqgemm = env_int("MI_QMM_DQGEMM", 0);
+  static const int prefill_min = env_int("MI_QMM_PREFILL_MIN", 128);
+  if (x_dtype == MI_DTYPE_BFLOAT16 && !use_dqgemm && M >= prefill_min &&
+      mi::prefill_supported(M, N, K, nb, gs)) {
+    mi::PrefillParams Q{w, (const uint16_t*)scales, (const uint16_t*)biases, (const uint16_t*)x,
+                        (uint16_t*)y, (int)M, (int)N, (int)K, gs, nullptr, 1, 0};
+    const size_t ws = mi::prefill_plan(Q);
+    if (ws) {
+      void* data = nullptr;
+      rc = workspace(s, ws, &data);
+      if (rc) return rc;
+      Q.part = (float*)data;
+    }
+    hipError_t e = mi::launch_prefill(Q, s);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "prefill launch");
+  }
   const bool odd_width = nb != 4 && nb != 8;
   if (odd_width && (x_dtype != MI_DTYPE_BFLOAT16 || N * K * 2 > ((int64_t)1 << 34)))
     return fail(MI_ERR_UNSUPPORTED, "bits=%d: bf16 activations only", nb);
@@ -609,7 +627,7 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
                                       (uint16_t*)y, M, N, K, gs, nb, -1, s);
     if (e != hipErrorNotSupported) return e == hipSuccess ? MI_OK : hip_fail(e, "qmv_any launch");
   }
-  if (x_dtype == MI_DTYPE_BFLOAT16 && (odd_width || (dq_min > 0 && M >= dq_min)) &&
+  if (x_dtype == MI_DTYPE_BFLOAT16 && (odd_width || (use_dqgemm && dq_min > 0 && M >= dq_min)) &&
       K <= INT32_MAX && N * K * 2 <= ((int64_t)1 << 34)) {
     const size_t wbytes = round256((size_t)N * K * 2);
     void* data = nullptr;

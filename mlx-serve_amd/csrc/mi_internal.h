@@ -152,6 +152,24 @@ size_t qmm_plan(QmmParams& P);
 hipError_t launch_qmm(const QmmParams& P, hipStream_t s);
 bool qmm_supported(int M, int N, int K, int bits, int gs);
 
+// Prefill GEMM for 4-bit weights (prefill.hip): 256x256 tiles, weights dequantized in
+// registers, x through an LDS ring; ks > 1 splits K (fp32 partials [ks][M][N] in `part`,
+// summed in split order by a second kernel).
+struct PrefillParams {
+  const uint32_t* w;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  const uint16_t* x;  // bf16 [M, K]
+  uint16_t* y;        // bf16 [M, N]
+  int M, N, K;
+  int group_size;
+  float* part;
+  int ks, sps;  // K splits and 64-wide steps per split
+};
+bool prefill_supported(int64_t M, int64_t N, int64_t K, int bits, int gs);
+size_t prefill_plan(PrefillParams& P);  // fills ks / sps; returns workspace bytes
+hipError_t launch_prefill(const PrefillParams& P, hipStream_t s);
+
 // Dequantize + hipBLASLt bf16 GEMM for large M (blas.cpp): y = x @ wd^T with wd the
 // dequantized bf16 [N, K] weight; blas_ws is the library's scratch. 0 or -1 (err set).
 constexpr size_t kDqGemmBlasWs = (size_t)32 << 20;
