@@ -8,8 +8,12 @@
  *   mo_pack/mo_unpack        known bit patterns + round trip; reference restatement
  *                            src/transformer.zig:20098-20108 (nibble order), :522-525 (bytes).
  *   mo_quantize_bf16         invariants (code range, exact edge, |w-deq| <= |s|/2, exact zero)
- *                            and hand-computed groups. Bit-parity with real mx.quantize is
- *                            PARITY UNPINNED (MLX is an un-vendored submodule, no MLX here).
+ *                            and hand-computed groups: exact .5 ties of the codes and of
+ *                            edge/scale (rint, ties to even), the edge refit, negative-edge
+ *                            groups, the q0 == 0 branch under the 1e-7 scale floor, codes
+ *                            straddling words at 2/3/5/6 bits. Bit-parity with real
+ *                            mx.quantize is PARITY UNPINNED (MLX is an un-vendored submodule,
+ *                            no MLX here): these checks fix this restatement, not MLX.
  *   mo_dequantize            closed forms (s*q exact in fp32), hand-computed values; which
  *                            bf16 rounding mx.dequantize applies is PARITY UNPINNED, both kept.
  *   mo_qmm_f64 / gather      numpy float64 matmul on independently dequantized weights,
@@ -17,6 +21,9 @@
  *   mo_route_softmax_topk    numpy softmax + lexsort top-k.
  *   mo_sort_dispatch         numpy stable argsort; inverse-permutation identity.
  *   mo_swiglu / down_reduce  exhaustive sigmoid table vs fp64 sigmoid; composition checks.
+ *                            The table is the correctly rounded sigmoid; the reference builds
+ *                            it with mlx_sigmoid on bf16 values (src/transformer.zig:19876-
+ *                            19880), whose rounding is PARITY UNPINNED (no MLX here).
  *   mo_affine_params...      the reference's own test cases for the geometry solve.
  */
 #include "mi_oracle.h"

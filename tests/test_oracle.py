@@ -134,6 +134,82 @@ def test_quantize_hand_worked_group():
     assert s[0, 0] == O.f32_to_bf16(np.float32(0.1)) and b[0, 0] == 0xBF80
 
 
+def _bits_le(wq_row, K, bits):
+    """Independent bitstream unpack: code j = bits [j*bits, (j+1)*bits) of the row's
+    little-endian byte string (numpy bit operations, no oracle code)."""
+    by = np.ascontiguousarray(wq_row, dtype=np.uint32).view(np.uint8)
+    bitv = np.unpackbits(by, bitorder="little")
+    return np.array([int("".join(str(b) for b in bitv[j * bits:(j + 1) * bits][::-1]), 2)
+                     for j in range(K)])
+
+
+def test_quantize_code_ties_round_to_even():
+    """(w - bias)/scale landing exactly on k + 0.5 rounds to the even code (rint), not
+    away from zero. Group {15/16, 6.5/16, 0}: span 15/16, scale -1/16 (|min| <= |max|),
+    edge = max, q0 = -15, scale stays -1/16, bias 15/16; code(w) = 15 - 16 w, so
+    w = 6.5/16 gives 8.5 -> 8 (half-away-from-zero would give 9), and 0 gives 15."""
+    g = np.zeros(64, np.float32)
+    g[0], g[1] = 15 / 16, 6.5 / 16
+    wq, s, b = O.quantize(O.f32_to_bf16(g[None, :]), 64, 4)
+    q = _bits_le(wq[0], 64, 4)
+    assert q[0] == 0 and q[1] == 8 and (q[2:] == 15).all()
+    assert O.bf16_to_f32(s)[0, 0] == -1 / 16 and O.bf16_to_f32(b)[0, 0] == 15 / 16
+
+
+def test_quantize_edge_tie_rounds_to_even_then_refits():
+    """edge/scale exactly -12.5 (max 12.5/8, min -2.5/8, span 15/8 so scale -1/8): q0 =
+    rint(-12.5) = -12 (not -13), the scale is refit to edge/q0 = -0.13020833 and the
+    bias is the edge, 1.5625. The max then decodes exactly and the min to code
+    rint((-0.3125 - 1.5625)/s) = rint(14.4) = 14."""
+    g = np.zeros(32, np.float32)
+    g[0], g[1] = 12.5 / 8, -2.5 / 8
+    wq, s, b = O.quantize(O.f32_to_bf16(g[None, :]), 32, 4)
+    scale = np.float32(np.float32(1.5625) / np.float32(-12.0))
+    assert s[0, 0] == O.f32_to_bf16(np.array([scale], np.float32))[0]
+    assert O.bf16_to_f32(b)[0, 0] == 1.5625
+    q = _bits_le(wq[0], 32, 4)
+    assert q[0] == 0 and q[1] == 14
+    assert (q[2:] == 12).all()  # 0.0 -> rint(-1.5625 / -0.1302) = rint(12.0) = 12
+
+
+def test_quantize_negative_edge_group():
+    """|min| > |max|: the scale is positive and the bias is the (negative) minimum.
+    Values in [-15/8, 0]: scale 1/8, q0 = -15, bias -1.875, code = 15 + 8 w."""
+    g = np.array([-1.875, 0.0, -1.0, -0.5, -1.125] + [-0.25] * 27, np.float32)
+    wq, s, b = O.quantize(O.f32_to_bf16(g[None, :]), 32, 4)
+    assert O.bf16_to_f32(s)[0, 0] == 0.125 and O.bf16_to_f32(b)[0, 0] == -1.875
+    q = _bits_le(wq[0], 32, 4)
+    assert list(q[:5]) == [0, 15, 7, 11, 6] and (q[5:] == 13).all()
+
+
+def test_quantize_zero_q0_branch_keeps_eps_scale():
+    """A group far below the 1e-7 scale floor: (max-min)/15 < eps so the scale is -1e-7
+    (|min| <= |max|), q0 = rint(max/-1e-7) = 0, so the refit is skipped: bias 0, scale
+    stays -1e-7 and every code clamps to 0."""
+    g = np.full(64, 2.0 ** -26, np.float32)
+    g[3] = 2.0 ** -25
+    wq, s, b = O.quantize(O.f32_to_bf16(g[None, :]), 64, 4)
+    assert b[0, 0] == 0
+    assert s[0, 0] == O.f32_to_bf16(np.array([-1e-7], np.float32))[0]
+    assert (_bits_le(wq[0], 64, 4) == 0).all()
+
+
+@pytest.mark.parametrize("bits", [2, 3, 5, 6])
+def test_quantize_codes_straddle_words(bits):
+    """Grid-exact groups at the odd widths: codes c_j = j mod 2^bits on value
+    bias + scale*c (scale 1/4, positive-edge groups); the codes crossing 32-bit word
+    boundaries come back exact from an independent bitstream read."""
+    gs = 32
+    nb = (1 << bits) - 1
+    c = np.arange(2 * gs) % (nb + 1)
+    c[0], c[gs] = 0, 0
+    c[1], c[gs + 1] = nb, nb
+    vals = (nb - c).astype(np.float32) * 0.25  # max nb/4 = edge (code 0), min 0 (code nb)
+    wq, s, b = O.quantize(O.f32_to_bf16(vals[None, :]), gs, bits)
+    assert (O.bf16_to_f32(s) == -0.25).all() and (O.bf16_to_f32(b) == nb * 0.25).all()
+    assert np.array_equal(_bits_le(wq[0], 2 * gs, bits), c)
+
+
 @pytest.mark.parametrize("bits", ALL_BITS)
 @pytest.mark.parametrize("gs", [32, 64, 128])
 def test_quantize_invariants(bits, gs):
