@@ -301,10 +301,11 @@ def moe_layer(torch, mi, dev, cfg, E, hidden, inter, k, Ts, n_routes=16, steps=1
         distinct = [torch.unique(r[0]).numel() for r in routes]
 
         def layer(r):
-            inds, sc = mi.moe_route_topk(logits[r], k, torch.bfloat16)
             if T == 1:
-                act = mi.gather_qmv_gate_up_swiglu(x, *G, *U, inds, gs, bits)
+                # routing runs inside the gate + up launch (2 launches per layer)
+                act, inds, sc = mi.moe_route_gate_up_swiglu(logits[r], x, *G, *U, k, gs, bits)
                 return mi.gather_qmv_down_reduce(act, *D, inds, sc, gs, bits)
+            inds, sc = mi.moe_route_topk(logits[r], k, torch.bfloat16)
             order, inv, srt, lhs, seg = mi.moe_sort_dispatch(inds.reshape(-1), k, E)
             xs = x.view(T, 1, hidden)
             g = mi.gather_qmm(xs, *G, lhs_indices=lhs, rhs_indices=srt, group_size=gs,

@@ -192,6 +192,20 @@ int mi_gather_qmv_gate_up_swiglu(void* y, const void* x, const uint32_t* w_gate,
                                  mi_optional_int group_size, mi_optional_int bits,
                                  const char* mode, void* stream);
 
+/* Routing fused into the gate + up launch, as the reference's fused router feeds the
+ * decode MoE (src/transformer.zig:17748; routing moeRoutingChain :17022-17072, then
+ * gatherQmvGateUp :20303-20396): inds/scores [T, k] receive mi_moe_route_topk's result
+ * for logits [T, E] fp32 (bit-equal), and y [T, k, N] the result of
+ * mi_gather_qmv_gate_up_swiglu on those indices (bit-equal). One launch when the weights
+ * are 4-bit gs 64 with K in one range, E <= 256 and scores_dtype bfloat16; otherwise the
+ * two calls run in turn. */
+int mi_moe_route_gate_up_swiglu(void* y, uint32_t* inds, void* scores, const float* logits,
+                                const void* x, const uint32_t* w_gate, const void* s_gate,
+                                const void* b_gate, const uint32_t* w_up, const void* s_up,
+                                const void* b_up, int64_t T, int64_t E, int k, int64_t N,
+                                int64_t K, mi_optional_int group_size, mi_optional_int bits,
+                                const char* mode, int scores_dtype, void* stream);
+
 /* Replaces gatherQmvDownReduce (src/transformer.zig:20675-20761): v[t*k+s] =
  * act[t*k+s] @ dequant(w_down[inds[t*k+s]])^T rounded to bf16, then y[t] as
  * mi_moe_down_reduce. act [T*k, K] bf16, scores [T*k] bf16, y [T, N] bf16. Bit-equal to

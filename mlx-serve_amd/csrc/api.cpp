@@ -861,6 +861,45 @@ int mi_gather_qmv_gate_up_swiglu(void* y, const void* x, const uint32_t* w_gate,
   return e == hipSuccess ? MI_OK : hip_fail(e, "swiglu launch");
 }
 
+int mi_moe_route_gate_up_swiglu(void* y, uint32_t* inds, void* scores, const float* logits,
+                                const void* x, const uint32_t* w_gate, const void* s_gate,
+                                const void* b_gate, const uint32_t* w_up, const void* s_up,
+                                const void* b_up, int64_t T, int64_t E, int k, int64_t N,
+                                int64_t K, mi_optional_int group_size, mi_optional_int bits,
+                                const char* mode, int scores_dtype, void* stream) {
+  if (T < 0 || k <= 0 || E <= 0) return fail(MI_ERR_INVALID, "bad T/E/k");
+  if (T == 0) return MI_OK;
+  if (!inds || !scores || !logits) return fail(MI_ERR_INVALID, "null routing pointer");
+  if (k > E || k > 64) return fail(MI_ERR_INVALID, "k must be <= min(64, E)");
+  const int64_t n_idx = T * k;
+  GatherJob G;
+  int rc = gather_prepare(G, y, x, w_gate, s_gate, b_gate, nullptr, inds, n_idx, k, T, 1, N, K, E,
+                          true, group_size, bits, mode, false, MI_DTYPE_BFLOAT16,
+                          MI_DTYPE_BFLOAT16);
+  if (rc || G.empty) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  // Routing inside the gate + up launch: the dual one-row kernel at gs 64 with one K range,
+  // up to 256 experts, bf16 scores. Otherwise route, then the fused gate + up call.
+  if (scores_dtype == MI_DTYPE_BFLOAT16 && E <= 256 && G.one_row && G.P.group_size == 64 &&
+      G.P.ks == 1 && !G.P.x_f32 && !G.ws_bytes()) {
+    G.P.w2 = w_up;
+    G.P.scales2 = (const uint16_t*)s_up;
+    G.P.biases2 = (const uint16_t*)b_up;
+    G.P.dual = 1;
+    G.P.rhs = nullptr;  // each block finds its pair's expert itself
+    G.P.route_logits = logits;
+    G.P.route_inds = inds;
+    G.P.route_scores = (uint16_t*)scores;
+    G.P.route_E = (int)E;
+    G.P.route_k = k;
+    return gather_launch(G, nullptr, s);
+  }
+  rc = mi_moe_route_topk(inds, scores, logits, T, E, k, scores_dtype, stream);
+  if (rc) return rc;
+  return mi_gather_qmv_gate_up_swiglu(y, x, w_gate, s_gate, b_gate, w_up, s_up, b_up, inds, T, k,
+                                      N, K, E, group_size, bits, mode, stream);
+}
+
 int mi_gather_qmv_down_reduce(void* y, const void* act, const uint32_t* w_down,
                               const void* s_down, const void* b_down, const uint32_t* inds,
                               const void* scores, int64_t T, int k, int64_t N, int64_t K,

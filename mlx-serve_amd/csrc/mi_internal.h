@@ -27,6 +27,14 @@ struct QmvParams {
   const uint16_t* scales2;
   const uint16_t* biases2;
   int dual;
+  // dual only, nullable: route inside the launch. Pairs are (token, slot) with
+  // lhs = pair / route_k; each block runs the softmax top-k of its token's route_E logits
+  // (route_E <= 256) to find its expert, and the blocks of row tile 0 write route_inds /
+  // route_scores (bf16) of their pair.
+  const float* route_logits;
+  uint32_t* route_inds;
+  uint16_t* route_scores;
+  int route_E, route_k;
   int64_t n_pairs, lhs_div, x_batch, n_experts;
   int M, N, K;
   int bits, group_size, x_f32;

@@ -19,6 +19,7 @@
 #include "mi_common.h"
 #include "mi_internal.h"
 #include "qmv_common.h"
+#include "moe_route.h"
 
 #include <type_traits>
 
@@ -115,67 +116,71 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
   const uint32_t nn = (uint32_t)min(n, N - 1);
   const int64_t PT = P.n_pairs * P.M;
 
-  // DUAL: gate (bank 0) then up (bank 1) for the same item; the gate sums wait in gsave and
-  // the up pass writes swiglu(gate, up) with the reference's rounding points.
+  // DUAL: gate (bank 0) and up (bank 1) for the same item. Both banks' loads go out
+  // before either is consumed (one memory round trip per item, not two); the gate sums
+  // wait in gsave and the up pass writes swiglu(gate, up) with the reference's rounding
+  // points.
   __shared__ float gsave[16];
-  auto process = [&](const Item& it, int64_t xr, auto bank_c) {
+  constexpr int ND = GPC >= 2 ? NC * GPC / 2 : 1;
+  constexpr int NSL = (ND + 3) / 4;
+  constexpr int D = DEPTH < NC ? DEPTH : NC;
+  struct BankLoads {
+    __amdgpu_buffer_rsrc_t wres;
+    uint32_t wo;
+    uint32_t sd[GPC >= 2 ? NSL : NC], bd[GPC >= 2 ? NSL : NC];
+    u32x4_t wv[NC];
+  };
+  // 1. every global load of this item, before anything waits, as buffer loads from
+  //    per-matrix resources: 32-bit lane offsets, chunk / slot strides folded into the
+  //    instructions' immediate offsets. Reads past a wave's range only feed chunks that
+  //    weigh 0, and reads past a resource's end return 0.
+  auto issue_x = [&](int64_t xr, u32x4_t (&xv)[XU]) {
+    const uint16_t* xb = reinterpret_cast<const uint16_t*>(P.x) + (xr < 0 ? 0 : xr) + kb0;
+    const __amdgpu_buffer_rsrc_t xres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, nvals * 2, kBufFlags);
+#pragma unroll
+    for (int i = 0; i < XU; ++i)
+      xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xres, (tid + i * BD) * 16, 0, 0);
+  };
+  auto issue_bank = [&](const Item& it, auto bank_c, BankLoads& L) {
     constexpr int BANK = decltype(bank_c)::value;
     const uint32_t* Pw = BANK ? P.w2 : P.w;
     const uint16_t* Ps = BANK ? P.scales2 : P.scales;
     const uint16_t* Pb = BANK ? P.biases2 : P.biases;
     const uint32_t e = __builtin_amdgcn_readfirstlane(it.expert_ok ? it.expert : 0u);
-    const bool ok = it.expert_ok && xr >= 0;
-
-    // 1. every global load of this item, before anything waits, as buffer loads from
-    //    per-matrix resources: 32-bit lane offsets, chunk / slot strides folded into the
-    //    instructions' immediate offsets. Reads past a wave's range only feed chunks that
-    //    weigh 0, and reads past a resource's end return 0.
-    const uint16_t* xb = reinterpret_cast<const uint16_t*>(P.x) + (xr < 0 ? 0 : xr) + kb0;
-    const __amdgpu_buffer_rsrc_t xres =
-        __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, nvals * 2, kBufFlags);
     const size_t mat = (size_t)e * (uint32_t)N;
-    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(Pw + mat * (uint32_t)(K / 8)), (short)0, N * (K / 2), kBufFlags);
+    L.wres = __builtin_amdgcn_make_buffer_rsrc((void*)(Pw + mat * (uint32_t)(K / 8)), (short)0,
+                                               N * (K / 2), kBufFlags);
     const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(Ps + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
     const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(Pb + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
-    constexpr bool STAGE = BANK == 0;  // the up pass reuses the staged activations
-    u32x4_t xv[XU];
-    if constexpr (STAGE) {
-#pragma unroll
-      for (int i = 0; i < XU; ++i)
-        xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xres, (tid + i * BD) * 16, 0, 0);
-    }
-    const uint32_t wo = nn * (uint32_t)(K / 2) + (uint32_t)(kb0 + c0 * kChunkVals) / 2 + 16 * g;
+    L.wo = nn * (uint32_t)(K / 2) + (uint32_t)(kb0 + c0 * kChunkVals) / 2 + 16 * g;
     // Scales/biases. gs 64/32: the wave's groups of a row are contiguous dwords; lane g
     // of the row's quad loads dwords g, g+4, ... and chunks take theirs by a quad
     // broadcast. gs 128: one bf16 per chunk.
-    constexpr int ND = GPC >= 2 ? NC * GPC / 2 : 1;
-    constexpr int NSL = (ND + 3) / 4;
     const uint32_t so = nn * (uint32_t)(G * 2) + (uint32_t)((kb0 + c0 * kChunkVals) / GS) * 2;
-    uint32_t sd[GPC >= 2 ? NSL : NC], bd[GPC >= 2 ? NSL : NC];
     if constexpr (GPC >= 2) {
 #pragma unroll
       for (int i = 0; i < NSL; ++i) {
-        sd[i] = __builtin_amdgcn_raw_buffer_load_b32(sres, so + 4 * g + 16 * i, 0, 0);
-        bd[i] = __builtin_amdgcn_raw_buffer_load_b32(bres, so + 4 * g + 16 * i, 0, 0);
+        L.sd[i] = __builtin_amdgcn_raw_buffer_load_b32(sres, so + 4 * g + 16 * i, 0, 0);
+        L.bd[i] = __builtin_amdgcn_raw_buffer_load_b32(bres, so + 4 * g + 16 * i, 0, 0);
       }
     } else {
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
-        sd[j] = __builtin_amdgcn_raw_buffer_load_b16(sres, so + 2 * j, 0, 0);
-        bd[j] = __builtin_amdgcn_raw_buffer_load_b16(bres, so + 2 * j, 0, 0);
+        L.sd[j] = __builtin_amdgcn_raw_buffer_load_b16(sres, so + 2 * j, 0, 0);
+        L.bd[j] = __builtin_amdgcn_raw_buffer_load_b16(bres, so + 2 * j, 0, 0);
       }
     }
     // Weights: the first D chunks now, then one more as each chunk is consumed, so a
     // wave's data arrives in the order it is used.
-    constexpr int D = DEPTH < NC ? DEPTH : NC;
-    u32x4_t wv[NC];
 #pragma unroll
-    for (int j = 0; j < D; ++j) wv[j] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * j, 0, 0);
-    if constexpr (STAGE) {
-    // 2. stage the activations in dot8's pair order, with per-32-value sums.
+    for (int j = 0; j < D; ++j)
+      L.wv[j] = __builtin_amdgcn_raw_buffer_load_b128(L.wres, L.wo + 64 * j, 0, 0);
+  };
+  // 2. stage the activations in dot8's pair order, with per-32-value sums.
+  auto stage_x = [&](const u32x4_t (&xv)[XU]) {
 #pragma unroll
     for (int i = 0; i < XU; ++i) {
       const int u = tid + i * BD;
@@ -196,43 +201,47 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
         if ((u & 3) == 0) xsum[u >> 2] = s8;
       }
     }
-    }
     // LDS-only barrier: the weight loads stay in flight.
     lds_barrier();
-
-    // 3. dot products, chunk by chunk as the loads land (chunks past the range weigh 0).
+  };
+  // 3. dot products, chunk by chunk as the loads land (chunks past the range weigh 0),
+  // 4. reduce the row's 4 lanes, then the waves in order, and write.
+  auto compute = [&](const Item& it, int64_t xr, auto bank_c, BankLoads& L) {
+    constexpr int BANK = decltype(bank_c)::value;
+    const bool ok = it.expert_ok && xr >= 0;
     float y = 0.f;
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
       if constexpr (D < NC) {
-        if (j + D < NC) wv[j + D] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * (j + D), 0, 0);
+        if (j + D < NC)
+          L.wv[j + D] = __builtin_amdgcn_raw_buffer_load_b128(L.wres, L.wo + 64 * (j + D), 0, 0);
       }
       const int jj = min(j, nload - 1);
       const int off = (c0 + jj) * kChunkVals + 32 * g;  // within the block range
       const u32x4_t* xp = reinterpret_cast<const u32x4_t*>(xs + off / 2);
       float acc = 0.f;
-      acc = dot8(wv[j].x, xp[0], acc);
-      acc = dot8(wv[j].y, xp[1], acc);
-      acc = dot8(wv[j].z, xp[2], acc);
-      acc = dot8(wv[j].w, xp[3], acc);
+      acc = dot8(L.wv[j].x, xp[0], acc);
+      acc = dot8(L.wv[j].y, xp[1], acc);
+      acc = dot8(L.wv[j].z, xp[2], acc);
+      acc = dot8(L.wv[j].w, xp[3], acc);
       const float use = j < nmine ? 1.f : 0.f;
       float s, b;
       if constexpr (GPC == 2) {
         // chunk j's groups are dword j: lane j % 4, slot j / 4 of the quad
-        const uint32_t sw = quad_bcast(sd[j >> 2], j & 3);
-        const uint32_t bw = quad_bcast(bd[j >> 2], j & 3);
+        const uint32_t sw = quad_bcast(L.sd[j >> 2], j & 3);
+        const uint32_t bw = quad_bcast(L.bd[j >> 2], j & 3);
         s = bf16_bits_to_f32(g >= 2 ? sw >> 16 : sw & 0xFFFFu);
         b = bf16_bits_to_f32(g >= 2 ? bw >> 16 : bw & 0xFFFFu);
       } else if constexpr (GPC == 4) {
         // chunk j's groups are dwords 2j, 2j+1: lanes g<2 take lane (2j)%4, g>=2 the next
         const int a = (2 * j) & 3;
-        const uint32_t sw = quad_pairs(sd[(2 * j) >> 2], a);
-        const uint32_t bw = quad_pairs(bd[(2 * j) >> 2], a);
+        const uint32_t sw = quad_pairs(L.sd[(2 * j) >> 2], a);
+        const uint32_t bw = quad_pairs(L.bd[(2 * j) >> 2], a);
         s = bf16_bits_to_f32((g & 1) ? sw >> 16 : sw & 0xFFFFu);
         b = bf16_bits_to_f32((g & 1) ? bw >> 16 : bw & 0xFFFFu);
       } else {
-        s = bf16_bits_to_f32(sd[j] & 0xFFFFu);
-        b = bf16_bits_to_f32(bd[j] & 0xFFFFu);
+        s = bf16_bits_to_f32(L.sd[j] & 0xFFFFu);
+        b = bf16_bits_to_f32(L.bd[j] & 0xFFFFu);
       }
       s *= use;
       b *= use;
@@ -240,7 +249,6 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
       y = fmaf(fmaf(-128.f, s, b), xsum[off >> 5], y);
       if constexpr (D < NC) __builtin_amdgcn_sched_barrier(0);  // keep the issue order
     }
-    // 4. reduce the row's 4 lanes, then the waves in order.
     y += quad_xor1(y);
     y += quad_xor2(y);
     if (g == 0) red[wave * 16 + r] = y;
@@ -265,9 +273,23 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
       }
     }
   };
-  using bank0 = std::integral_constant<int, 0>;
-  using bank1 = std::integral_constant<int, 1>;
-
+  using bank0_t = std::integral_constant<int, 0>;
+  using bank1_t = std::integral_constant<int, 1>;
+  auto process = [&](const Item& it, int64_t xr, u32x4_t (&xv)[XU]) {
+    BankLoads L0;
+    issue_bank(it, bank0_t{}, L0);
+    if constexpr (DUAL) {
+      BankLoads L1;
+      issue_bank(it, bank1_t{}, L1);
+      stage_x(xv);
+      compute(it, xr, bank0_t{}, L0);
+      lds_barrier();  // gsave written, the reduction buffer free again
+      compute(it, xr, bank1_t{}, L1);
+    } else {
+      stage_x(xv);
+      compute(it, xr, bank0_t{}, L0);
+    }
+  };
   if constexpr (DENSE) {
     // one pair, no indices: straight-line, no work-item decode
     Item it;
@@ -275,19 +297,43 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     it.cnt = 1;
     it.expert = 0;
     it.expert_ok = true;
-    process(it, 0, bank0{});
+    u32x4_t xv[XU];
+    issue_x(0, xv);
+    process(it, 0, xv);
   } else {
     const int n_items = P.items ? (int)*P.item_count : P.n_items_fixed;
+    __shared__ uint32_t route_expert;
     for (int it_i = blockIdx.z; it_i < n_items; it_i += gridDim.z) {
-      const Item it = decode_item(P, it_i);
+      Item it = decode_item(P, it_i);
       if (it.cnt <= 0) continue;
+      // the activation row does not depend on the expert: its loads go out first
       const int64_t xr = item_x_row(P, it, 0);
       if (xr == -1) continue;  // block-uniform
-      process(it, xr, bank0{});
+      u32x4_t xv[XU];
+      issue_x(xr, xv);
       if constexpr (DUAL) {
-        lds_barrier();  // gsave and the reduction buffer
-        process(it, xr, bank1{});
+        if (P.route_logits) {
+          // unsorted one-row items: item it_i is pair it_i = (token, slot)
+          const int t = it_i / P.route_k, slot = it_i - t * P.route_k;
+          if (wave == 0) {
+            uint32_t sel;
+            float w;
+            route_token<4>(P.route_logits + (int64_t)t * P.route_E, P.route_E, P.route_k, lane,
+                           sel, w);
+            if (lane == slot) {
+              route_expert = sel;
+              if (tile == 0 && ks == 0) {
+                P.route_inds[it_i] = sel;
+                P.route_scores[it_i] = (uint16_t)f32_to_bf16_bits(w);
+              }
+            }
+          }
+          lds_barrier();
+          it.expert = route_expert;
+          it.expert_ok = route_expert < (uint32_t)P.n_experts;
+        }
       }
+      process(it, xr, xv);
       lds_barrier();  // LDS is reused by the next item
     }
   }

@@ -281,6 +281,27 @@ def gather_qmv_gate_up_swiglu(x, wg, sg, bg, wu, su, bu, inds, group_size=None, 
     return y
 
 
+def moe_route_gate_up_swiglu(logits, x, wg, sg, bg, wu, su, bu, k, group_size=None, bits=None,
+                             mode="affine"):
+    """Routing + gatherQmvGateUp in one call (src/transformer.zig:17748, :20303-20396):
+    logits fp32 [T, E], x [T, K] -> (y [T, k, N], inds [T, k], bf16 scores [T, k])."""
+    _contig(logits, x, wg, sg, bg, wu, su, bu)
+    _require(logits.dtype == torch.float32, "logits must be float32")
+    T, K = x.shape
+    E = logits.shape[-1]
+    gs, nb = _resolve(_packed(wg), sg, group_size, bits, K)
+    N = wg.shape[1]
+    y = torch.empty((T, k, N), dtype=x.dtype, device=x.device)
+    inds = torch.empty((T, k), dtype=torch.int32, device=x.device)
+    scores = torch.empty((T, k), dtype=torch.bfloat16, device=x.device)
+    check(lib().mi_moe_route_gate_up_swiglu(_ptr(y), _ptr(inds), _ptr(scores), _ptr(logits),
+                                            _ptr(x), _ptr(wg), _ptr(sg), _ptr(bg), _ptr(wu),
+                                            _ptr(su), _ptr(bu), T, E, int(k), N, K, opt(gs),
+                                            opt(nb), mode.encode() if mode else None,
+                                            _dtype_code(scores, "scores"), _stream(x)))
+    return y, inds, scores
+
+
 def gather_qmv_down_reduce(act, wd, sd, bd, inds, scores, group_size=None, bits=None,
                            mode="affine"):
     """gatherQmvDownReduce (src/transformer.zig:20675-20761): act [T, k, K], inds/scores

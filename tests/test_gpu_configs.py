@@ -148,7 +148,7 @@ def route(dev, T, E, k, sd, skew_seed=None):
     inds, sc = mi_qmm.moe_route_topk(logits, k, torch.bfloat16)
     ri, _ = O.route_softmax_topk(logits.cpu().numpy(), k)
     assert np.array_equal(inds.cpu().numpy().view(np.uint32), ri)
-    return inds, sc
+    return inds, sc, logits
 
 
 def bank_host_experts(bank, experts):
@@ -172,11 +172,16 @@ def moe_bank(dev, E, N, K, bits, sd):
     return wq.view(E, N, -1), s.view(E, N, -1), b.view(E, N, -1)
 
 
-def check_decode_moe(dev, G, U, D, x, inds, sc, k):
+def check_decode_moe(dev, G, U, D, x, inds, sc, k, logits):
     """T=1 fused entry points: gate+up+SwiGLU and down+score-reduce against the split
     calls (bit-equal) and each gather against the oracle."""
     T, hidden = x.shape
     act = mi_qmm.gather_qmv_gate_up_swiglu(x, *G, *U, inds, 64, 4)
+    # the routing-fused launch the benchmark times gives the same indices, scores and
+    # activations
+    act2, inds2, sc2 = mi_qmm.moe_route_gate_up_swiglu(logits, x, *G, *U, k, 64, 4)
+    assert torch.equal(inds2, inds) and torch.equal(sc2.view(torch.int16), sc.view(torch.int16))
+    assert torch.equal(act2.view(torch.int16), act.view(torch.int16))
     y = mi_qmm.gather_qmv_down_reduce(act, *D, inds, sc, 64, 4)
     xs = x.view(T, 1, 1, hidden)  # one token broadcast over its k slots
     g = mi_qmm.gather_qmm(xs, *G, rhs_indices=inds.view(T, k), group_size=64, bits=4)
@@ -242,15 +247,15 @@ def test_config3_moe_decode(dev, qwen_banks):
     _case(t="cfg3", T=1)
     G, U, D = qwen_banks
     x = dev_x(dev, 1, 2048, seed(4, 0, 1))
-    inds, sc = route(dev, 1, 128, 8, seed(4, 2, 1))
-    check_decode_moe(dev, G, U, D, x, inds, sc, 8)
+    inds, sc, lg = route(dev, 1, 128, 8, seed(4, 2, 1))
+    check_decode_moe(dev, G, U, D, x, inds, sc, 8, lg)
 
 
 def test_config3_moe_prefill(dev, qwen_banks):
     _case(t="cfg3", T=512)
     G, U, D = qwen_banks
     x = dev_x(dev, 512, 2048, seed(4, 0, 512))
-    inds, sc = route(dev, 512, 128, 8, seed(4, 2, 512))
+    inds, sc, _ = route(dev, 512, 128, 8, seed(4, 2, 512))
     check_sorted_moe(dev, G, U, D, x, inds, sc, 8, 128, 96, 3)
 
 
@@ -268,9 +273,9 @@ def test_config4_moe(dev, dsv3_banks, T):
     _case(t="cfg4", T=T)
     G, U, D = dsv3_banks
     x = dev_x(dev, T, 7168, seed(5, 0, T))
-    inds, sc = route(dev, T, 256, 8, seed(5, 2, T), skew_seed=seed(5, 3))
+    inds, sc, lg = route(dev, T, 256, 8, seed(5, 2, T), skew_seed=seed(5, 3))
     if T == 1:
-        check_decode_moe(dev, G, U, D, x, inds, sc, 8)
+        check_decode_moe(dev, G, U, D, x, inds, sc, 8, lg)
     else:
         check_sorted_moe(dev, G, U, D, x, inds, sc, 8, 256, 40, T)
 

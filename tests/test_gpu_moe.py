@@ -203,3 +203,24 @@ def test_sorted_moe_pipeline_end_to_end(dev):
     ri, _ = O.route_softmax_topk(logits, k)
     truth = O.gather_qmm_f64(x.reshape(T, 1, K), wq, s, b, None, ri.reshape(-1), T * k, lhs_div=k)
     assert max_err_ratio(to_f64(y).reshape(T * k, 1, N), truth) <= BF16_TOL
+
+
+@pytest.mark.parametrize("T,E,k,N,K", [(1, 128, 8, 768, 2048), (1, 256, 8, 2048, 7168),
+                                       (3, 60, 4, 256, 1024), (2, 16, 2, 192, 512),
+                                       (1, 300, 8, 128, 512)])
+def test_route_fused_gate_up_matches_split(dev, T, E, k, N, K):
+    """Routing inside the gate+up launch: indices and bf16 scores equal mi_moe_route_topk's,
+    and the activations equal the fused gate+up call on those indices, bit for bit (E=300
+    takes the two-call path)."""
+    _print_case(t="route_fused", T=T, E=E, k=k, N=N, K=K)
+    gq, gs_, gb = _bank(E, N, K, 21)
+    uq, us, ub = _bank(E, N, K, 22)
+    D = lambda *a: [to_dev_u32(a[0], dev), to_dev_bf16(a[1], dev), to_dev_bf16(a[2], dev)]  # noqa
+    G, U = D(gq, gs_, gb), D(uq, us, ub)
+    x = to_dev_bf16(O.make_x_bf16(T, K, 23), dev)
+    logits = torch.from_numpy(O.randn(T * E, 24).reshape(T, E)).to(dev)
+    y, inds, sc = mi_qmm.moe_route_gate_up_swiglu(logits, x, *G, *U, k, group_size=64, bits=4)
+    ri, rs = mi_qmm.moe_route_topk(logits, k, torch.bfloat16)
+    assert torch.equal(inds, ri) and torch.equal(sc.view(torch.int16), rs.view(torch.int16))
+    act = mi_qmm.gather_qmv_gate_up_swiglu(x, *G, *U, ri, group_size=64, bits=4)
+    assert torch.equal(y.view(torch.int16), act.view(torch.int16))
