@@ -154,6 +154,17 @@ int mi_fill_randn(void* out, int64_t n, uint64_t seed, float mean, float stddev,
 int mi_moe_route_topk(uint32_t* inds, void* scores, const float* logits, int64_t T, int64_t E,
                       int k, int scores_dtype, void* stream);
 
+/* Replaces groupLimitedRouting (src/transformer.zig:17242-17347; group mask groupLimitMask
+ * :17138-17236), the DeepSeek-style router: fp32 logits [T, E] and expert bias [E] ->
+ * inds [T, k] (descending masked key, ties to the lower id) and fp32 weights [T, k]:
+ * sigmoid scores, +bias, groups of E/n_group ranked by the sum of their two largest biased
+ * values, all but the topk_group best masked to -1e4, top-k of that; weights are the
+ * unbiased scores of the selected, / (slot-order sum + 1e-20) when route_norm and k > 1,
+ * times route_scale. E <= 1024, n_group <= 64, k <= min(64, E). */
+int mi_moe_route_grouped(uint32_t* inds, float* scores, const float* logits, const float* bias,
+                         int64_t T, int64_t E, int k, int n_group, int topk_group, bool route_norm,
+                         float route_scale, void* stream);
+
 /* Replaces the sort steps of the sorted MoE path (src/transformer.zig:14965-14993):
  * order = stable argsort(flat), inv = argsort(order), sorted = flat[order],
  * lhs = order / k. seg_offsets (may be NULL) receives n_experts+1 entries: the first

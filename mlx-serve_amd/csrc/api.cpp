@@ -763,6 +763,24 @@ int mi_moe_route_topk(uint32_t* inds, void* scores, const float* logits, int64_t
   return e == hipSuccess ? MI_OK : hip_fail(e, "route launch");
 }
 
+int mi_moe_route_grouped(uint32_t* inds, float* scores, const float* logits, const float* bias,
+                         int64_t T, int64_t E, int k, int n_group, int topk_group, bool route_norm,
+                         float route_scale, void* stream) {
+  if (T < 0 || E <= 0 || k <= 0) return fail(MI_ERR_INVALID, "bad T/E/k");
+  if (n_group <= 0 || topk_group <= 0 || topk_group > n_group || E % n_group != 0 ||
+      E / n_group < 2)
+    return fail(MI_ERR_INVALID, "bad group geometry (E %% n_group, group size >= 2, "
+                "0 < topk_group <= n_group)");
+  if (E > 1024 || n_group > 64 || k > 64 || k > E)
+    return fail(MI_ERR_UNSUPPORTED, "E <= 1024, n_group <= 64, k <= min(64, E)");
+  if (T == 0) return MI_OK;
+  if (!inds || !scores || !logits || !bias) return fail(MI_ERR_INVALID, "null tensor pointer");
+  hipError_t e = mi::launch_route_grouped(logits, bias, T, (int)E, k, n_group, topk_group,
+                                          route_norm ? 1 : 0, route_scale, inds, scores,
+                                          (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : hip_fail(e, "grouped route launch");
+}
+
 int mi_moe_sort_dispatch(uint32_t* order, uint32_t* inv, uint32_t* sorted, uint32_t* lhs,
                          uint32_t* seg_offsets, const uint32_t* flat, int64_t n, int k,
                          int64_t n_experts, void* stream) {

@@ -108,6 +108,9 @@ hipError_t launch_build_items(const uint32_t* rhs, int64_t n_pairs, int M, int r
 hipError_t launch_route_topk(const float* logits, int64_t T, int E, int k, uint32_t* inds,
                              void* scores, int scores_bf16, hipStream_t s);
 size_t sort_dispatch_lds_bytes(int E);
+hipError_t launch_route_grouped(const float* logits, const float* bias, int64_t T, int E, int k,
+                                int n_group, int topk_group, int route_norm, float route_scale,
+                                uint32_t* inds, float* scores, hipStream_t s);
 hipError_t launch_sort_dispatch(const uint32_t* flat, int64_t n, int k, int E, uint32_t* order,
                                 uint32_t* inv, uint32_t* sorted, uint32_t* lhs, uint32_t* seg,
                                 hipStream_t s);

@@ -37,6 +37,111 @@ __global__ void __launch_bounds__(256) route_topk_kernel(const float* __restrict
   }
 }
 
+// Group-limited routing (groupLimitedRouting, src/transformer.zig:17242-17347, with the
+// group mask of groupLimitMask :17138-17236), one wave per token, fp32 throughout:
+// score = sigmoid(logit); biased = score + bias[e]; a group's score is the sum of its two
+// largest biased values; the topk_group best groups survive (ties to the lower group id)
+// and every other expert's key becomes -1e4; the k best keys are selected in descending
+// order (ties to the lower id); the weights are the UNBIASED scores of the selected,
+// divided by (their sum in slot order + 1e-20) when route_norm and k > 1, then times
+// route_scale. E <= 64 * NV, n_group <= 64.
+constexpr int kGroupedMaxE = 1024;
+template <int NV>
+__global__ void __launch_bounds__(256) route_grouped_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int64_t T, int E, int k,
+    int n_group, int topk_group, int route_norm, float route_scale, uint32_t* __restrict__ inds,
+    float* __restrict__ scores) {
+  __shared__ float biased_s[4][kGroupedMaxE];
+  __shared__ float gscore_s[4][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * 4 + wv;
+  if (t >= T) return;
+  using namespace route_detail;
+  const float* row = logits + t * E;
+  float* biased = biased_s[wv];
+  float sc[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E) {
+      sc[j] = 1.f / (1.f + expf(-row[e]));
+      biased[e] = sc[j] + bias[e];
+    } else {
+      sc[j] = 0.f;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  // group scores: lane g scans its group for the two largest biased values
+  const int gsz = E / n_group;
+  if (lane < n_group) {
+    float m1 = -INFINITY, m2 = -INFINITY;
+    for (int i = 0; i < gsz; ++i) {
+      const float v = biased[lane * gsz + i];
+      if (v > m1) {
+        m2 = m1;
+        m1 = v;
+      } else if (v > m2) {
+        m2 = v;
+      }
+    }
+    gscore_s[wv][lane] = m1 + m2;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  // a group survives when fewer than topk_group groups beat it (ties to the lower id)
+  bool keep_g = false;
+  if (lane < n_group) {
+    const float mine = gscore_s[wv][lane];
+    int rank = 0;
+    for (int g2 = 0; g2 < n_group; ++g2) {
+      const float o = gscore_s[wv][g2];
+      rank += (o > mine || (o == mine && g2 < lane)) ? 1 : 0;
+    }
+    keep_g = rank < topk_group;
+  }
+  const uint64_t keep_mask = __ballot(keep_g);
+  uint64_t key[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E) {
+      const float kv = ((keep_mask >> (e / gsz)) & 1) ? biased[e] : -1.0e4f;
+      key[j] = kv == kv ? ((uint64_t)ord_f32(kv) << 32) | (uint32_t)~e : 0;
+    } else {
+      key[j] = 0;
+    }
+  }
+  uint32_t sel_i = 0;
+  for (int r = 0; r < k; ++r) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) best = key[j] > best ? key[j] : best;
+    best = wave_max_u64(best, lane);
+    const uint32_t bi = best ? ~(uint32_t)best : (uint32_t)r;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+      if (best && (uint32_t)(lane + 64 * j) == bi) key[j] = 0;  // taken
+    if (lane == r) sel_i = bi;
+  }
+  // weights: the unbiased score of each selected expert, slot r in lane r
+  float w = 0.f;
+  if (lane < k) {
+    const float v = row[sel_i < (uint32_t)E ? sel_i : 0];
+    w = sel_i < (uint32_t)E ? 1.f / (1.f + expf(-v)) : NAN;
+  }
+  if (route_norm && k > 1) {
+    float sum = 0.f;
+    for (int r = 0; r < k; ++r) sum += __shfl(w, r, 64);  // ascending slot order
+    w = w / (sum + 1e-20f);
+  }
+  if (route_scale != 1.f) w = w * route_scale;
+  if (lane < k) {
+    inds[t * k + lane] = sel_i;
+    scores[t * k + lane] = w;
+  }
+}
+
 // Stable counting sort of expert ids by one 1024-thread block. Ids >= E share the
 // last bucket (kept in index order). seg may be null; otherwise seg[e] is the first
 // sorted position of expert e and seg[E] the number of in-range ids.
@@ -268,6 +373,23 @@ hipError_t launch_route_topk(const float* logits, int64_t T, int E, int k, uint3
   else if (nv <= 8) MI_ROUTE(8);
   else MI_ROUTE(16);
 #undef MI_ROUTE
+  return hipGetLastError();
+}
+
+hipError_t launch_route_grouped(const float* logits, const float* bias, int64_t T, int E, int k,
+                                int n_group, int topk_group, int route_norm, float route_scale,
+                                uint32_t* inds, float* scores, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  const unsigned grid = (unsigned)((T + 3) / 4);
+  const int nv = (E + 63) / 64;
+#define MI_ROUTEG(NVV)                                                                       \
+  hipLaunchKernelGGL(route_grouped_kernel<NVV>, dim3(grid), dim3(256), 0, s, logits, bias, T, \
+                     E, k, n_group, topk_group, route_norm, route_scale, inds, scores)
+  if (nv <= 2) MI_ROUTEG(2);
+  else if (nv <= 4) MI_ROUTEG(4);
+  else if (nv <= 8) MI_ROUTEG(8);
+  else MI_ROUTEG(16);
+#undef MI_ROUTEG
   return hipGetLastError();
 }
 

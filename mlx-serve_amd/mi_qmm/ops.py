@@ -219,6 +219,21 @@ def moe_route_topk(logits, k, scores_dtype=torch.float32):
     return inds, scores
 
 
+def moe_route_grouped(logits, bias, k, n_group, topk_group, route_norm=True, route_scale=1.0):
+    """Group-limited sigmoid routing (groupLimitedRouting, src/transformer.zig:17242-17347):
+    logits fp32 [..., E], bias fp32 [E] -> (inds int32 [..., k], weights fp32 [..., k])."""
+    _contig(logits, bias)
+    _require(logits.dtype == torch.float32 and bias.dtype == torch.float32, "fp32 inputs")
+    E = logits.shape[-1]
+    T = logits.numel() // E if E else 0
+    inds = torch.empty(logits.shape[:-1] + (k,), dtype=torch.int32, device=logits.device)
+    w = torch.empty(logits.shape[:-1] + (k,), dtype=torch.float32, device=logits.device)
+    check(lib().mi_moe_route_grouped(_ptr(inds), _ptr(w), _ptr(logits), _ptr(bias), T, E, int(k),
+                                     int(n_group), int(topk_group), bool(route_norm),
+                                     float(route_scale), _stream(logits)))
+    return inds, w
+
+
 def moe_sort_dispatch(flat, k, n_experts):
     """Sorted MoE dispatch (src/transformer.zig:14965-14993): returns (order, inv, sorted,
     lhs, seg_offsets) with order = stable argsort(flat), inv = argsort(order),

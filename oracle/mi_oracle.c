@@ -19,6 +19,8 @@
  *   mo_qmm_f64 / gather      numpy float64 matmul on independently dequantized weights,
  *                            one-hot / all-ones / integer special cases.
  *   mo_route_softmax_topk    numpy softmax + lexsort top-k.
+ *   mo_route_grouped_f64     reduces to a plain sigmoid top-k when one group or every group
+ *                            survives (numpy lexsort); a hand-built group mask case.
  *   mo_sort_dispatch         numpy stable argsort; inverse-permutation identity.
  *   mo_swiglu / down_reduce  exhaustive sigmoid table vs fp64 sigmoid; composition checks.
  *                            The table is the correctly rounded sigmoid; the reference builds
@@ -359,6 +361,76 @@ int mo_gather_qmm_f64(const void* x, int x_f32, const uint32_t* wq, const uint16
  * weights; divide by their sum. argpartition leaves the order inside the top-k
  * unspecified, so this restatement fixes it: descending logit, ties by index.
  * The weight sum runs in that slot order. */
+/* Descending selection of k of n keys, ties to the lower index (the reference test's
+ * routerRefRow, src/transformer.zig:23263-23282). */
+static void ref_row_topk(const double* keys, int n, int k, int* out) {
+  char taken[1024] = {0};
+  for (int r = 0; r < k; ++r) {
+    int bidx = 0, found = 0;
+    double best = -INFINITY;
+    for (int i = 0; i < n; ++i) {
+      if (taken[i]) continue;
+      if (!found || keys[i] > best) {
+        best = keys[i];
+        bidx = i;
+        found = 1;
+      }
+    }
+    taken[bidx] = 1;
+    out[r] = bidx;
+  }
+}
+
+/* Group-limited routing (groupLimitedRouting, src/transformer.zig:17242-17347, group mask
+ * groupLimitMask :17138-17236) in float64, as the reference's own test computes its
+ * reference (:23390-23515): sigmoid, + bias, group score = sum of the group's two largest
+ * keys, the topk_group best groups kept, other keys -1e4, top-k; weights = unbiased
+ * sigmoid of the selected, / (sum + 1e-20) when route_norm and k > 1, * route_scale. */
+int mo_route_grouped_f64(const float* logits, const float* bias, int64_t T, int64_t E, int k,
+                         int n_group, int topk_group, int route_norm, double route_scale,
+                         uint32_t* inds, double* w) {
+  if (k <= 0 || k > E || E > 1024 || n_group <= 0 || n_group > 64 || E % n_group ||
+      topk_group <= 0 || topk_group > n_group)
+    return -1;
+  const int gsz = (int)(E / n_group);
+  double sig[1024], keys[1024], gscore[64];
+  int gsel[64], ids[64];
+  for (int64_t t = 0; t < T; ++t) {
+    for (int i = 0; i < E; ++i) {
+      sig[i] = 1.0 / (1.0 + exp(-(double)logits[t * E + i]));
+      keys[i] = sig[i] + (double)bias[i];
+    }
+    for (int g = 0; g < n_group; ++g) {
+      double m1 = -INFINITY, m2 = -INFINITY;
+      for (int i = 0; i < gsz; ++i) {
+        const double v = keys[g * gsz + i];
+        if (v > m1) {
+          m2 = m1;
+          m1 = v;
+        } else if (v > m2) {
+          m2 = v;
+        }
+      }
+      gscore[g] = m1 + m2;
+    }
+    ref_row_topk(gscore, n_group, topk_group, gsel);
+    char kept[64] = {0};
+    for (int j = 0; j < topk_group; ++j) kept[gsel[j]] = 1;
+    for (int i = 0; i < E; ++i)
+      if (!kept[i / gsz]) keys[i] = -1.0e4;
+    ref_row_topk(keys, (int)E, k, ids);
+    double sum = 0.0;
+    for (int j = 0; j < k; ++j) sum += sig[ids[j]];
+    for (int j = 0; j < k; ++j) {
+      double v = sig[ids[j]];
+      if (route_norm && k > 1) v = v / (sum + 1e-20);
+      inds[t * k + j] = (uint32_t)ids[j];
+      w[t * k + j] = v * route_scale;
+    }
+  }
+  return 0;
+}
+
 int mo_route_softmax_topk(const float* logits, int64_t T, int64_t E, int k,
                           uint32_t* inds, float* scores) {
   if (k <= 0 || k > E) return -1;

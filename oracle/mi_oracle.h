@@ -93,6 +93,11 @@ void mo_down_reduce_bf16(const uint16_t* v, const uint16_t* scores, int64_t topk
 int mo_affine_params_from_geometry(int64_t w_cols, int64_t s_cols, int64_t in_dim,
                                    int* bits, int* gs);
 
+/* ---- group-limited routing (a8) ----------------------------------------- */
+int mo_route_grouped_f64(const float* logits, const float* bias, int64_t T, int64_t E, int k,
+                         int n_group, int topk_group, int route_norm, double route_scale,
+                         uint32_t* inds, double* w);
+
 #ifdef __cplusplus
 }
 #endif

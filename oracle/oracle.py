@@ -50,6 +50,7 @@ def lib():
                                         i64, i64, i32, i32, P]
         L.mo_route_softmax_topk.argtypes = [P, i64, i64, i32, P, P]
         L.mo_sort_dispatch.argtypes = [P, i64, i32, P, P, P, P]
+        L.mo_route_grouped_f64.argtypes = [P, P, i64, i64, i32, i32, i32, i32, f64, P, P]
         L.mo_sigmoid_table_bf16.argtypes = [P]
         L.mo_swiglu_bf16.argtypes = [P, P, i64, P]
         L.mo_down_reduce_bf16.argtypes = [P, P, i64, i64, P]
@@ -211,6 +212,19 @@ def route_softmax_topk(logits, k):
     scores = np.empty((T, k), dtype=np.float32)
     _check(lib().mo_route_softmax_topk(_p(logits), T, E, k, _p(inds), _p(scores)), "route")
     return inds, scores
+
+
+def route_grouped(logits, bias, k, n_group, topk_group, route_norm=True, route_scale=1.0):
+    """Group-limited routing in float64 -> (inds uint32 [T, k], weights float64 [T, k])."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    bias = np.ascontiguousarray(bias, dtype=np.float32)
+    T, E = logits.shape
+    inds = np.empty((T, k), dtype=np.uint32)
+    w = np.empty((T, k), dtype=np.float64)
+    _check(lib().mo_route_grouped_f64(_p(logits), _p(bias), T, E, k, n_group, topk_group,
+                                      int(route_norm), float(route_scale), _p(inds), _p(w)),
+           "route_grouped")
+    return inds, w
 
 
 def sort_dispatch(flat, k):

@@ -224,3 +224,26 @@ def test_route_fused_gate_up_matches_split(dev, T, E, k, N, K):
     assert torch.equal(inds, ri) and torch.equal(sc.view(torch.int16), rs.view(torch.int16))
     act = mi_qmm.gather_qmv_gate_up_swiglu(x, *G, *U, ri, group_size=64, bits=4)
     assert torch.equal(y.view(torch.int16), act.view(torch.int16))
+
+
+@pytest.mark.parametrize("E,k,ng,tg", [(512, 8, 8, 4), (256, 8, 8, 4), (64, 4, 4, 2),
+                                       (128, 6, 1, 1)])
+def test_route_grouped_matches_oracle(dev, E, k, ng, tg):
+    """Group-limited routing against the float64 oracle (the reference test's own
+    reference, src/transformer.zig:23390): indices exact on 256 rows of the reference
+    test's data shape, weights within 1e-5 relative."""
+    _print_case(t="route_grouped", E=E, k=k, ng=ng, tg=tg)
+    rng = np.random.default_rng(E + ng)
+    T = 256
+    logits = ((rng.random((T, E)) - 0.5) * 6.0 + (np.arange(T * E) % 7).reshape(T, E) * 0.011)
+    logits = logits.astype(np.float32)
+    bias = ((rng.random(E) - 0.5) * 0.2).astype(np.float32)
+    inds, w = mi_qmm.moe_route_grouped(torch.from_numpy(logits).to(dev),
+                                       torch.from_numpy(bias).to(dev), k, ng, tg, True, 2.5)
+    ri, rw = O.route_grouped(logits, bias, k, ng, tg, True, 2.5)
+    assert np.array_equal(_u32(inds), ri)
+    wg = w.cpu().numpy().astype(np.float64)
+    assert np.max(np.abs(wg - rw) / np.abs(rw)) <= 1e-5
+    if ng > tg:  # the limit must bite on this data: some rows differ from the unmasked top-k
+        free, _ = O.route_grouped(logits, bias, k, ng, ng, True, 2.5)
+        assert (np.sort(free, axis=1) != np.sort(ri, axis=1)).any()

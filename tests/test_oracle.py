@@ -435,3 +435,44 @@ def test_dequantize_fp_closed_form(mode):
     assert np.array_equal(O.dequantize_fp(wq, sc, mode, out_bf16=True),
                           O.f32_to_bf16(exact.astype(np.float32)))
     assert np.array_equal(O.bf16_to_f32(O.dequantize_fp(wq, sc, mode, out_bf16=True)), f32)
+
+
+def _sigmoid_topk_np(logits, bias, k):
+    """Plain descending top-k of sigmoid(logits) + bias, ties to the lower id (numpy)."""
+    keys = 1.0 / (1.0 + np.exp(-logits.astype(np.float64))) + bias.astype(np.float64)
+    E = keys.shape[-1]
+    return np.stack([np.lexsort((np.arange(E), -row))[:k] for row in keys])
+
+
+def test_route_grouped_reduces_to_plain_topk():
+    """One group, or every group surviving, leaves nothing masked: the selection is the
+    plain top-k of sigmoid + bias, and the weights are the unbiased sigmoids normalized
+    over the selected (then scaled)."""
+    rng = np.random.default_rng(3)
+    T, E, k = 40, 64, 6
+    logits = ((rng.random((T, E)) - 0.5) * 6).astype(np.float32)
+    bias = ((rng.random(E) - 0.5) * 0.2).astype(np.float32)
+    want = _sigmoid_topk_np(logits, bias, k)
+    for ng, tg in ((1, 1), (8, 8), (4, 4)):
+        inds, w = O.route_grouped(logits, bias, k, ng, tg, True, 2.5)
+        assert np.array_equal(inds, want)
+        sig = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+        sel = np.take_along_axis(sig, want.astype(np.int64), axis=1)
+        assert np.allclose(w, 2.5 * sel / (sel.sum(1, keepdims=True) + 1e-20), rtol=1e-12)
+    # route_norm off and k == 1: raw sigmoid times the scale
+    inds, w = O.route_grouped(logits, bias, 1, 1, 1, True, 1.0)
+    sig = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    assert np.allclose(w[:, 0], sig[np.arange(T), inds[:, 0]], rtol=1e-12)
+
+
+def test_route_grouped_masks_losing_groups():
+    """Two groups of four, one kept: expert 0 has the single largest key but its group's
+    top-two sum loses, so every selected expert comes from group 1."""
+    logits = np.full((1, 8), -5.0, np.float32)
+    logits[0, 0] = 5.0                      # best single expert, group 0
+    logits[0, 4:7] = [3.0, 2.9, 2.8]        # group 1: larger top-two sum
+    bias = np.zeros(8, np.float32)
+    inds, _ = O.route_grouped(logits, bias, 2, 2, 1, True, 1.0)
+    assert list(inds[0]) == [4, 5]
+    inds, _ = O.route_grouped(logits, bias, 2, 2, 2, True, 1.0)  # no limit
+    assert list(inds[0]) == [0, 4]
