@@ -105,15 +105,20 @@ int mi_gather_qmm_noalloc(void* y, const void* x, const uint32_t* w, const void*
                           const char* mode, bool sorted_indices, int x_dtype, int sb_dtype,
                           void* stream);
 
-/* Replaces mlx_dequantize (src/mlx.zig:271), mode "affine", no global scale:
- *   out[r,k] = scale[r,k/gs] * q[r,k] + bias[r,k/gs]
- * Modes "nvfp4" / "mxfp4" / "mxfp8" (uint8 scales, no biases): out = element(q) *
- * scale, exact in float32 and bfloat16.
+/* Replaces mlx_dequantize (src/mlx.zig:271), same argument order (mlx_array handles become
+ * pointers plus rows/K; the optional output dtype becomes out_dtype):
+ *   affine: out[r,k] = scale[r,k/gs] * q[r,k] + bias[r,k/gs]
+ * Modes "nvfp4" / "mxfp4" / "mxfp8" (uint8 scales, no biases): out = element(q) * scale,
+ * exact in float32 and bfloat16. global_scale (nullable device pointer to one fp32, nvfp4
+ * only; the reference passes none at every call site): out = (element(q) * scale) *
+ * global_scale, the first product exact, one rounding. NULL for the other modes, else
+ * MI_ERR_INVALID.
  * out_dtype float32: exact fp32 result. out_dtype bfloat16: rounded like MLX's
  * composed dequantize (a bf16 multiply then a bf16 add). */
 int mi_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,
                   int64_t rows, int64_t K, mi_optional_int group_size, mi_optional_int bits,
-                  const char* mode, int sb_dtype, int out_dtype, void* stream);
+                  const char* mode, const float* global_scale, int sb_dtype, int out_dtype,
+                  void* stream);
 
 /* Same as mi_dequantize with an explicit bf16 rounding: rounding 0 = one rounding
  * of s*q+b, 1 = op-by-op (the mi_dequantize default). No mlx-c counterpart: MLX's
@@ -121,14 +126,16 @@ int mi_dequantize(void* out, const uint32_t* w, const void* scales, const void* 
  * build, so both are offered. */
 int mi_dequantize_rounding(void* out, const uint32_t* w, const void* scales, const void* biases,
                            int64_t rows, int64_t K, mi_optional_int group_size,
-                           mi_optional_int bits, const char* mode, int sb_dtype, int out_dtype,
-                           int rounding, void* stream);
+                           mi_optional_int bits, const char* mode, const float* global_scale,
+                           int sb_dtype, int out_dtype, int rounding, void* stream);
 
-/* Replaces mlx_quantize (src/mlx.zig:275), mode "affine": w [rows,K] (bfloat16 or
- * float32) -> packed uint32 wq, scales/biases in w's dtype (bfloat16 only here). */
+/* Replaces mlx_quantize (src/mlx.zig:275), mode "affine", same argument order: w [rows,K]
+ * (bfloat16 or float32) -> packed uint32 wq, scales/biases in bfloat16. global_scale must
+ * be NULL (it belongs to nvfp4 quantization, which this library does not perform; the
+ * reference passes none). */
 int mi_quantize(uint32_t* wq, void* scales, void* biases, const void* w, int64_t rows, int64_t K,
-                mi_optional_int group_size, mi_optional_int bits, const char* mode, int w_dtype,
-                void* stream);
+                mi_optional_int group_size, mi_optional_int bits, const char* mode,
+                const float* global_scale, int w_dtype, void* stream);
 
 /* Solve (bits, group_size) from packed geometry, as affineParamsFromGeometry
  * (src/transformer.zig:16763-16782): bits = w_cols*32/in_dim, gs = in_dim/s_cols.

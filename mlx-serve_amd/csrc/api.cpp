@@ -577,7 +577,7 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
     void* data = nullptr;
     rc = workspace(s, wbytes + mi::kDqGemmBlasWs, &data);
     if (rc) return rc;
-    hipError_t e = mi::launch_dequantize_fp(data, w, (const uint8_t*)scales, N, K, fm, 0, s);
+    hipError_t e = mi::launch_dequantize_fp(data, w, (const uint8_t*)scales, N, K, fm, 0, nullptr, s);
     if (e != hipSuccess) return hip_fail(e, "dequantize launch");
     const char* err = nullptr;
     if (mi::dq_gemm((const uint16_t*)x, (const uint16_t*)data, (uint16_t*)y, (int)M, (int)N,
@@ -679,11 +679,13 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
 
 int mi_dequantize_rounding(void* out, const uint32_t* w, const void* scales, const void* biases,
                            int64_t rows, int64_t K, mi_optional_int group_size,
-                           mi_optional_int bits, const char* mode, int sb_dtype, int out_dtype,
-                           int rounding, void* stream) {
+                           mi_optional_int bits, const char* mode, const float* global_scale,
+                           int sb_dtype, int out_dtype, int rounding, void* stream) {
   int gs = 0, nb = 0;
   const int fm = fp_mode_of(mode);
-  if (fm >= 0) {  // exact in either output dtype: rounding does not apply
+  if (global_scale && fm != 0)
+    return fail(MI_ERR_INVALID, "global_scale applies to mode nvfp4 only");
+  if (fm >= 0) {  // exact in either output dtype without a global scale: rounding does not apply
     int rc = resolve_fp(fm, group_size, bits, true, K, sb_dtype, &gs, &nb);
     if (rc) return rc;
     if (out_dtype != MI_DTYPE_BFLOAT16 && out_dtype != MI_DTYPE_FLOAT32)
@@ -692,7 +694,8 @@ int mi_dequantize_rounding(void* out, const uint32_t* w, const void* scales, con
     if (rows == 0) return MI_OK;
     if (!out || !w || !scales) return fail(MI_ERR_INVALID, "null tensor pointer");
     hipError_t e = mi::launch_dequantize_fp(out, w, (const uint8_t*)scales, rows, K, fm,
-                                            out_dtype == MI_DTYPE_FLOAT32, (hipStream_t)stream);
+                                            out_dtype == MI_DTYPE_FLOAT32, global_scale,
+                                            (hipStream_t)stream);
     return e == hipSuccess ? MI_OK : hip_fail(e, "dequantize launch");
   }
   int rc = resolve_common(group_size, bits, mode, true, K, &gs, &nb);
@@ -713,15 +716,18 @@ int mi_dequantize_rounding(void* out, const uint32_t* w, const void* scales, con
 
 int mi_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,
                   int64_t rows, int64_t K, mi_optional_int group_size, mi_optional_int bits,
-                  const char* mode, int sb_dtype, int out_dtype, void* stream) {
-  return mi_dequantize_rounding(out, w, scales, biases, rows, K, group_size, bits, mode, sb_dtype,
-                                out_dtype, 1, stream);
+                  const char* mode, const float* global_scale, int sb_dtype, int out_dtype,
+                  void* stream) {
+  return mi_dequantize_rounding(out, w, scales, biases, rows, K, group_size, bits, mode,
+                                global_scale, sb_dtype, out_dtype, 1, stream);
 }
 
 int mi_quantize(uint32_t* wq, void* scales, void* biases, const void* w, int64_t rows, int64_t K,
-                mi_optional_int group_size, mi_optional_int bits, const char* mode, int w_dtype,
-                void* stream) {
+                mi_optional_int group_size, mi_optional_int bits, const char* mode,
+                const float* global_scale, int w_dtype, void* stream) {
   int gs = 0, nb = 0;
+  if (global_scale)
+    return fail(MI_ERR_UNSUPPORTED, "global_scale: quantize takes affine only here");
   int rc = resolve_common(group_size, bits, mode, true, K, &gs, &nb);
   if (rc) return rc;
   if (w_dtype != MI_DTYPE_BFLOAT16 && w_dtype != MI_DTYPE_FLOAT32)

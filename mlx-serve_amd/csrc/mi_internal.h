@@ -122,7 +122,7 @@ hipError_t launch_down_reduce(uint16_t* y, const uint16_t* v, const uint16_t* sc
                               int k, int64_t N, hipStream_t s);
 // nvfp4 (mode 0) / mxfp4 (1) / mxfp8 (2) dequantize, uint8 scales, no biases (quant.hip).
 hipError_t launch_dequantize_fp(void* out, const uint32_t* w, const uint8_t* s, int64_t rows,
-                                int64_t K, int mode, int out_f32, hipStream_t st);
+                                int64_t K, int mode, int out_f32, const float* gscale, hipStream_t st);
 // Decode GEMV for 2/3/5/6-bit affine weights (fp_mode -1, bf16 scales/biases) and the
 // nvfp4 / mxfp4 / mxfp8 modes (fp_mode 0/1/2, uint8 scales), 1..8 bf16 activation rows
 // (qmv_any.hip). hipErrorNotSupported when the shape is outside its scope.

@@ -97,10 +97,13 @@ MI_DEV float fp_e4m3(uint32_t b) {
 }
 MI_DEV float fp_e8m0(uint32_t b) { return __builtin_ldexpf(1.0f, b == 0 ? -127 : (int)b - 127); }
 
+// gscale (nullable, nvfp4's optional fp32 global scale): element * scale is exact in fp32,
+// the global scale multiplies that product with one rounding.
 __global__ void dequant_fp_kernel(void* __restrict__ out, const uint32_t* __restrict__ w,
                                   const uint8_t* __restrict__ s, int64_t n_words, int64_t K,
-                                  int mode, int out_f32) {
+                                  int mode, int out_f32, const float* __restrict__ gscale) {
   const int bits = mode == 2 ? 8 : 4, gs = mode == 0 ? 16 : 32, pf = 32 / bits;
+  const float gsc = gscale ? *gscale : 1.f;
   const int64_t wpr = K / pf, G = K / gs;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_words;
        i += (int64_t)gridDim.x * blockDim.x) {
@@ -110,7 +113,8 @@ __global__ void dequant_fp_kernel(void* __restrict__ out, const uint32_t* __rest
       const int64_t k = k0 + j;
       const uint32_t q = (word >> (j * bits)) & ((1u << bits) - 1u);
       const uint32_t sb = s[row * G + k / gs];
-      const float v = (mode == 2 ? fp_e4m3(q) : fp_e2m1(q)) * (mode == 0 ? fp_e4m3(sb) : fp_e8m0(sb));
+      float v = (mode == 2 ? fp_e4m3(q) : fp_e2m1(q)) * (mode == 0 ? fp_e4m3(sb) : fp_e8m0(sb));
+      if (gscale) v *= gsc;
       if (out_f32) ((float*)out)[row * K + k] = v;
       else ((uint16_t*)out)[row * K + k] = (uint16_t)f32_to_bf16_bits(v);
     }
@@ -401,11 +405,12 @@ hipError_t launch_dequantize(void* out, const uint32_t* w, const uint16_t* s, co
 }
 
 hipError_t launch_dequantize_fp(void* out, const uint32_t* w, const uint8_t* s, int64_t rows,
-                                int64_t K, int mode, int out_f32, hipStream_t st) {
+                                int64_t K, int mode, int out_f32, const float* gscale,
+                                hipStream_t st) {
   const int64_t n_words = rows * (K * (mode == 2 ? 8 : 4) / 32);
   if (n_words == 0) return hipSuccess;
   hipLaunchKernelGGL(dequant_fp_kernel, dim3(grid_for(n_words, 256)), dim3(256), 0, st, out, w, s,
-                     n_words, K, mode, out_f32);
+                     n_words, K, mode, out_f32, gscale);
   return hipGetLastError();
 }
 

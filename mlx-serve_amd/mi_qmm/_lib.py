@@ -44,10 +44,10 @@ def lib():
                                       i32, P]
     L.mi_gather_qmm.argtypes = [P, P, P, P, P, P, P, i64, i64, i64, i64, i64, i64, i64, b,
                                 OptInt, OptInt, s, b, i32, i32, P]
-    L.mi_dequantize.argtypes = [P, P, P, P, i64, i64, OptInt, OptInt, s, i32, i32, P]
-    L.mi_dequantize_rounding.argtypes = [P, P, P, P, i64, i64, OptInt, OptInt, s, i32, i32, i32,
-                                         P]
-    L.mi_quantize.argtypes = [P, P, P, P, i64, i64, OptInt, OptInt, s, i32, P]
+    L.mi_dequantize.argtypes = [P, P, P, P, i64, i64, OptInt, OptInt, s, P, i32, i32, P]
+    L.mi_dequantize_rounding.argtypes = [P, P, P, P, i64, i64, OptInt, OptInt, s, P, i32, i32,
+                                         i32, P]
+    L.mi_quantize.argtypes = [P, P, P, P, i64, i64, OptInt, OptInt, s, P, i32, P]
     L.mi_affine_params_from_geometry.argtypes = [i64, i64, i64, ctypes.POINTER(i32),
                                                  ctypes.POINTER(i32)]
     L.mi_fill_randn.argtypes = [P, i64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, i32, P]

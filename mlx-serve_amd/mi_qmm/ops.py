@@ -154,10 +154,11 @@ def gather_qmm(x, w, scales, biases, lhs_indices=None, rhs_indices=None, transpo
 
 
 def dequantize(w, scales, biases, group_size=None, bits=None, mode="affine", dtype=None,
-               rounding=None):
+               rounding=None, global_scale=None):
     """mlx_dequantize (src/mlx.zig:271). dtype defaults to the scales dtype.
-    rounding (bf16 output only): None/1 = op-by-op bf16, 0 = single rounding."""
-    _contig(w, scales, biases)
+    rounding (bf16 output only): None/1 = op-by-op bf16, 0 = single rounding.
+    global_scale: nvfp4 only, a one-element fp32 device tensor."""
+    _contig(w, scales, biases, global_scale)
     K = w.shape[-1] * 32 // (_defaults(mode)[1] if bits is None else int(bits))
     gs, nb = _resolve(_packed(w), scales, group_size, bits, K, mode)
     dtype = (torch.bfloat16 if scales.dtype == torch.uint8 else scales.dtype) if dtype is None else dtype
@@ -165,6 +166,7 @@ def dequantize(w, scales, biases, group_size=None, bits=None, mode="affine", dty
     out = torch.empty(tuple(w.shape[:-1]) + (K,), dtype=dtype, device=w.device)
     check(lib().mi_dequantize_rounding(_ptr(out), _ptr(w), _ptr(scales), _ptr(biases), rows, K,
                                        opt(gs), opt(nb), mode.encode() if mode else None,
+                                       _ptr(global_scale),
                                        _dtype_code(scales, "scales"), _dtype_code(out, "out"),
                                        1 if rounding is None else int(rounding), _stream(w)))
     return out
@@ -184,7 +186,8 @@ def quantize(w, group_size=None, bits=None, mode="affine"):
     s = torch.empty(lead + (K // gs,), dtype=sdt, device=w.device)
     b = torch.empty(lead + (K // gs,), dtype=sdt, device=w.device)
     check(lib().mi_quantize(_ptr(wq), _ptr(s), _ptr(b), _ptr(w), rows, K, opt(gs), opt(nb),
-                            mode.encode() if mode else None, _dtype_code(w, "w"), _stream(w)))
+                            mode.encode() if mode else None, None, _dtype_code(w, "w"),
+                            _stream(w)))
     return wq, s, b
 
 

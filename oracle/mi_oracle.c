@@ -569,6 +569,14 @@ float mo_e8m0(uint32_t b) { return ldexpf(1.0f, b == 0 ? -127 : (int)b - 127); }
 /* mode: 0 nvfp4, 1 mxfp4, 2 mxfp8. out_bf16: 0 fp32, 1 bf16 (exact either way). */
 int mo_dequantize_fp(const uint32_t* wq, const uint8_t* scales, int64_t rows, int64_t K,
                      int mode, int out_bf16, void* out) {
+  return mo_dequantize_fp_gs(wq, scales, rows, K, mode, out_bf16, 0, 1.0f, out);
+}
+
+/* nvfp4's optional global scale (mlx_dequantize's global_scale, src/mlx.zig:271): the
+ * element * scale product (exact in fp32) times the fp32 global scale, one rounding. */
+int mo_dequantize_fp_gs(const uint32_t* wq, const uint8_t* scales, int64_t rows, int64_t K,
+                        int mode, int out_bf16, int has_gscale, float gscale, void* out) {
+  if (has_gscale && mode != 0) return -1;
   if (mode < 0 || mode > 2) return -1;
   const int bits = mode == 2 ? 8 : 4, gs = mode == 0 ? 16 : 32;
   if (K % gs) return -1;
@@ -579,7 +587,8 @@ int mo_dequantize_fp(const uint32_t* wq, const uint8_t* scales, int64_t rows, in
       const uint32_t sb = scales[r * ng + k / gs];
       const float el = mode == 2 ? mo_e4m3(q) : mo_e2m1(q);
       const float sc = mode == 0 ? mo_e4m3(sb) : mo_e8m0(sb);
-      const float v = el * sc;
+      volatile float v = el * sc;
+      if (has_gscale) v = v * gscale;
       if (out_bf16) ((uint16_t*)out)[r * K + k] = mo_f32_to_bf16(v);
       else ((float*)out)[r * K + k] = v;
     }

@@ -93,6 +93,14 @@ void mo_down_reduce_bf16(const uint16_t* v, const uint16_t* scores, int64_t topk
 int mo_affine_params_from_geometry(int64_t w_cols, int64_t s_cols, int64_t in_dim,
                                    int* bits, int* gs);
 
+/* ---- microscaling fp modes (f4) ------------------------------------------ */
+/* mode 0 nvfp4, 1 mxfp4, 2 mxfp8; out fp32 (out_bf16 0) or bf16 bits. */
+int mo_dequantize_fp(const uint32_t* wq, const uint8_t* scales, int64_t rows, int64_t K,
+                     int mode, int out_bf16, void* out);
+/* nvfp4 with the optional fp32 global scale (has_gscale 1; other modes: -1). */
+int mo_dequantize_fp_gs(const uint32_t* wq, const uint8_t* scales, int64_t rows, int64_t K,
+                        int mode, int out_bf16, int has_gscale, float gscale, void* out);
+
 /* ---- group-limited routing (a8) ----------------------------------------- */
 int mo_route_grouped_f64(const float* logits, const float* bias, int64_t T, int64_t E, int k,
                          int n_group, int topk_group, int route_norm, double route_scale,

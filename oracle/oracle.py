@@ -41,6 +41,7 @@ def lib():
         L.mo_quantize_bf16.argtypes = [P, i64, i64, i32, i32, P, P, P]
         L.mo_dequantize.argtypes = [P, P, P, i64, i64, i32, i32, i32, P]
         L.mo_dequantize_fp.argtypes = [P, P, i64, i64, i32, i32, P]
+        L.mo_dequantize_fp_gs.argtypes = [P, P, i64, i64, i32, i32, i32, ctypes.c_float, P]
         for f in (L.mo_e2m1, L.mo_e4m3, L.mo_e8m0):
             f.argtypes = [ctypes.c_uint32]
             f.restype = ctypes.c_float
@@ -137,7 +138,7 @@ def fp_element(code, fmt):
     return float({"e2m1": lib().mo_e2m1, "e4m3": lib().mo_e4m3, "e8m0": lib().mo_e8m0}[fmt](code))
 
 
-def dequantize_fp(wq, scales_u8, mode, out_bf16=False):
+def dequantize_fp(wq, scales_u8, mode, out_bf16=False, global_scale=None):
     """Bias-less microscaling modes: wq [..., K*bits/32] u32, scales [..., K/gs] uint8."""
     m, bits, gs = FP_MODES[mode]
     wq = np.ascontiguousarray(wq, dtype=np.uint32)
@@ -145,7 +146,10 @@ def dequantize_fp(wq, scales_u8, mode, out_bf16=False):
     K = wq.shape[-1] * 32 // bits
     rows = wq.size // wq.shape[-1]
     out = np.empty(tuple(wq.shape[:-1]) + (K,), dtype=np.uint16 if out_bf16 else np.float32)
-    _check(lib().mo_dequantize_fp(_p(wq), _p(sc), rows, K, m, int(out_bf16), _p(out)),
+    _check(lib().mo_dequantize_fp_gs(_p(wq), _p(sc), rows, K, m, int(out_bf16),
+                                     int(global_scale is not None),
+                                     float(1.0 if global_scale is None else global_scale),
+                                     _p(out)),
            "dequantize_fp")
     return out
 

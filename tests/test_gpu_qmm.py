@@ -390,3 +390,32 @@ def test_graph_replay_after_workspace_growth(dev):
     torch.cuda.synchronize()
     mi_qmm._lib.check(mi_qmm._lib.lib().mi_workspace_release(None))
     assert np.array_equal(bf16_bits(mi_qmm.gather_qmm(x, *args, **kw)), eager)
+
+
+@pytest.mark.parametrize("g", [0.25, 1.0 / 3.0, 7.5])
+def test_dequantize_nvfp4_global_scale(dev, g):
+    """mlx_dequantize's global_scale (nvfp4): bit-exact against the oracle in fp32 and bf16;
+    other modes and mi_quantize refuse a global scale."""
+    _print_case(t="nvfp4_gscale", g=g)
+    wq, sc = _fp_weight("nvfp4", 64, 256, 41)
+    W, S = to_dev_u32(wq, dev), torch.from_numpy(sc).to(dev)
+    gs_t = torch.tensor([g], dtype=torch.float32, device=dev)
+    f32 = mi_qmm.dequantize(W, S, None, mode="nvfp4", dtype=torch.float32, global_scale=gs_t)
+    ref = O.dequantize_fp(wq, sc, "nvfp4", global_scale=float(np.float32(g)))
+    assert np.array_equal(f32.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    bf = bf16_bits(mi_qmm.dequantize(W, S, None, mode="nvfp4", global_scale=gs_t))
+    assert np.array_equal(bf, O.dequantize_fp(wq, sc, "nvfp4", out_bf16=True,
+                                              global_scale=float(np.float32(g))))
+    wq2, sc2 = _fp_weight("mxfp4", 64, 256, 42)
+    with pytest.raises(mi_qmm.MiError):
+        mi_qmm.dequantize(to_dev_u32(wq2, dev), torch.from_numpy(sc2).to(dev), None,
+                          mode="mxfp4", global_scale=gs_t)
+    w = torch.zeros(4, 64, dtype=torch.bfloat16, device=dev)
+    out = [torch.empty(4, 8, dtype=torch.int32, device=dev),
+           torch.empty(4, 1, dtype=torch.bfloat16, device=dev),
+           torch.empty(4, 1, dtype=torch.bfloat16, device=dev)]
+    from mi_qmm._lib import opt
+    rc = mi_qmm._lib.lib().mi_quantize(out[0].data_ptr(), out[1].data_ptr(), out[2].data_ptr(),
+                                      w.data_ptr(), 4, 64, opt(64), opt(4), b"affine",
+                                      gs_t.data_ptr(), 12, None)
+    assert rc == 1  # MI_ERR_UNSUPPORTED

@@ -476,3 +476,25 @@ def test_route_grouped_masks_losing_groups():
     assert list(inds[0]) == [4, 5]
     inds, _ = O.route_grouped(logits, bias, 2, 2, 2, True, 1.0)  # no limit
     assert list(inds[0]) == [0, 4]
+
+
+def test_dequantize_fp_global_scale():
+    """nvfp4's global scale: 1.0 changes nothing; a power of two scales every value
+    exactly (fp32 and bf16 alike); other modes refuse it."""
+    rng = np.random.default_rng(8)
+    q = rng.integers(0, 16, size=(4, 64)).astype(np.uint8)
+    wq = O.pack(q, 4)
+    sc = rng.integers(0x20, 0x48, size=(4, 4)).astype(np.uint8)
+    base = O.dequantize_fp(wq, sc, "nvfp4")
+    assert np.array_equal(O.dequantize_fp(wq, sc, "nvfp4", global_scale=1.0).view(np.uint32),
+                          base.view(np.uint32))
+    for p2 in (0.25, 8.0):
+        assert np.array_equal(O.dequantize_fp(wq, sc, "nvfp4", global_scale=p2), base * p2)
+        assert np.array_equal(O.dequantize_fp(wq, sc, "nvfp4", out_bf16=True, global_scale=p2),
+                              O.f32_to_bf16(base * np.float32(p2)))
+    # a general scale: the exact element*scale product times g, rounded once in fp32
+    g = np.float32(1 / 3)
+    assert np.array_equal(O.dequantize_fp(wq, sc, "nvfp4", global_scale=float(g)), base * g)
+    with pytest.raises(ValueError):
+        O.dequantize_fp(O.pack(q, 4), rng.integers(118, 126, (4, 2)).astype(np.uint8), "mxfp4",
+                        global_scale=2.0)
