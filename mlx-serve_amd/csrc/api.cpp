@@ -428,6 +428,11 @@ size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
 }  // namespace
 
+namespace mi {
+// Error reporting for the other translation units of the library (the checkpoint loader).
+int report_error(int code, const std::string& msg) { return fail(code, "%s", msg.c_str()); }
+}  // namespace mi
+
 extern "C" {
 
 const char* mi_last_error(void) { return g_err.c_str(); }

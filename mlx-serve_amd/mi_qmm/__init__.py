@@ -11,3 +11,4 @@ from .ops import (quantized_matmul, gather_qmm, dequantize, quantize, fill_randn
                   swiglu, moe_down_reduce, gather_qmv_gate_up_swiglu, gather_qmv_down_reduce,
                   workspace_reserve, moe_route_gate_up_swiglu,
                   moe_route_grouped)
+from .ckpt import Checkpoint, parse_quant_config  # noqa: F401

@@ -67,6 +67,22 @@ def lib():
     L.mi_workspace_reserve.argtypes = [i64, P]
     L.mi_workspace_release.argtypes = [P]
     L.mi_last_error.restype = ctypes.c_char_p
+    PP = ctypes.POINTER(P)
+    L.mi_ckpt_open.argtypes = [s, i32, PP]
+    L.mi_ckpt_open_file.argtypes = [s, PP]
+    L.mi_ckpt_close.argtypes = [P]
+    L.mi_ckpt_close.restype = None
+    L.mi_parse_quant_config.argtypes = [s, ctypes.c_size_t, P]
+    L.mi_ckpt_quant_config.argtypes = [P, P]
+    L.mi_ckpt_set_quant_config.argtypes = [P, P]
+    L.mi_ckpt_count.argtypes = [P]
+    L.mi_ckpt_count.restype = i64
+    L.mi_ckpt_name.argtypes = [P, i64]
+    L.mi_ckpt_name.restype = ctypes.c_char_p
+    L.mi_ckpt_info.argtypes = [P, s, P]
+    L.mi_ckpt_read.argtypes = [P, s, P, ctypes.c_size_t]
+    L.mi_ckpt_upload.argtypes = [P, s, P, ctypes.c_size_t]
+    L.mi_ckpt_linear.argtypes = [P, s, i64, P]
     L.mi_version.restype = ctypes.c_char_p
     for name in EXTRA_SIGNATURES:
         if hasattr(L, name):

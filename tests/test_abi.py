@@ -10,12 +10,14 @@ import pytest
 from mi_qmm import _lib as L
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "mi_qmm.h")
+INCLUDE = os.path.join(ROOT, "include")
 
 
 def header_symbols():
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(mi_\w+)\s*\(", text, re.M)))
+    text = "".join(open(os.path.join(INCLUDE, h)).read()
+                   for h in sorted(os.listdir(INCLUDE)) if h.endswith(".h"))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|void|const char\*)\s+(mi_\w+)\s*\(",
+                                 text, re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -27,7 +29,7 @@ def lib():
 
 def test_exports_every_header_symbol(lib):
     syms = header_symbols()
-    assert len(syms) >= 10
+    assert len(syms) >= 10 and "mi_ckpt_open" in syms and "mi_ckpt_close" in syms
     for s in syms:
         assert hasattr(lib, s), s
 
