@@ -478,6 +478,36 @@ def test_route_grouped_masks_losing_groups():
     assert list(inds[0]) == [0, 4]
 
 
+def test_route_grouped_shipped_geometry_numpy():
+    """The reference test's geometry (src/transformer.zig:23390: E=512, 8 groups, 4 kept,
+    k=8, route_scale 2.5, 256 rows, logits (u-0.5)*6 + (i%7)*0.011, bias (u-0.5)*0.2)
+    against an independent numpy statement: group scores from a sort, groups and experts
+    chosen by lexsort (ties to the lower id)."""
+    rng = np.random.default_rng(0x116C0DE)
+    R, E, k, NG, TG, scale = 256, 512, 8, 8, 4, 2.5
+    logits = ((rng.random((R, E)) - 0.5) * 6.0 +
+              (np.arange(R * E) % 7).reshape(R, E) * 0.011).astype(np.float32)
+    bias = ((rng.random(E) - 0.5) * 0.2).astype(np.float32)
+    inds, w = O.route_grouped(logits, bias, k, NG, TG, True, scale)
+    sig = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    keys = sig + bias.astype(np.float64)
+    gsz = E // NG
+    gs = np.sort(keys.reshape(R, NG, gsz), axis=2)[:, :, -2:].sum(2)
+    dropped = 0
+    for r in range(R):
+        keep = np.lexsort((np.arange(NG), -gs[r]))[:TG]
+        allowed = np.zeros(E, bool)
+        for g in keep:
+            allowed[g * gsz:(g + 1) * gsz] = True
+        masked = np.where(allowed, keys[r], -1e4)
+        want = np.lexsort((np.arange(E), -masked))[:k]
+        assert list(inds[r]) == list(want), r
+        sel = sig[r, want]
+        assert np.allclose(w[r], scale * sel / (sel.sum() + 1e-20), rtol=1e-12)
+        dropped += int(np.any(np.lexsort((np.arange(E), -keys[r]))[:k] != want))
+    assert dropped > 0  # the group limit changed some rows' selection
+
+
 def test_dequantize_fp_global_scale():
     """nvfp4's global scale: 1.0 changes nothing; a power of two scales every value
     exactly (fp32 and bf16 alike); other modes refuse it."""
