@@ -402,6 +402,71 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
   return MI_OK;
 }
 
+// fp-mode gathers (nvfp4 fpm 0, mxfp4 1, mxfp8 2) on the few-row MFMA kernel: sorted runs
+// cut into work items as for the affine kernels, unsorted pairs one item per pair (and
+// 32-row slice). Returns MI_ERR_UNSUPPORTED when the call does not fit the plan: the
+// caller then takes the per-pair kernel, which serves up to 8 rows per pair.
+int gather_prepare_fp(GatherJob& J, int fpm, int gs, void* y, const void* x, const uint32_t* w,
+                      const void* scales, const uint32_t* lhs_indices,
+                      const uint32_t* rhs_indices, int64_t n_idx, int64_t lhs_div,
+                      int64_t x_batch, int64_t M, int64_t N, int64_t K, int64_t n_experts,
+                      bool sorted_indices) {
+  static const int use_fp_mfma = env_int("MI_QMM_FP_MFMA", 1);
+  if (!use_fp_mfma || fpm < 0 || fpm > 2) return MI_ERR_UNSUPPORTED;
+  if (N > (int64_t)1 << 30 || M > (int64_t)1 << 30 || n_idx * M >= ((int64_t)1 << 32) ||
+      x_batch * M * K * 2 >= ((int64_t)1 << 32) || x_batch == 0 || n_experts == 0)
+    return MI_ERR_UNSUPPORTED;
+  mi::QmvParams& P = J.P;
+  P.w = w;
+  P.scales = (const uint16_t*)scales;  // uint8 scales; the kernel reads them as bytes
+  P.biases = nullptr;
+  P.x = x;
+  P.y = y;
+  P.lhs = lhs_indices;
+  P.rhs = rhs_indices;
+  P.n_pairs = n_idx;
+  P.lhs_div = lhs_div;
+  P.x_batch = x_batch;
+  P.n_experts = n_experts;
+  P.M = (int)M;
+  P.N = (int)N;
+  P.K = (int)K;
+  P.bits = fpm == 2 ? 8 : 4;
+  P.group_size = gs;
+  P.x_f32 = 0;
+  J.use_items = sorted_indices && rhs_indices != nullptr && n_idx > 1;
+  const int64_t PT = n_idx * M;
+  int64_t n_items;
+  if (J.use_items) {
+    // rows a distinct expert gets under uniform routing plus 3 standard deviations (as
+    // for the affine items); about one row per run stays on the per-pair kernel
+    const double e = (double)n_experts, distinct = e * (1.0 - std::pow(1.0 - 1.0 / e, (double)PT));
+    const double mu = distinct > 0 ? (double)PT / distinct : 1.0;
+    const int64_t avg = mu <= 1.3 ? 1 : (int64_t)std::ceil(mu + 3.0 * std::sqrt(mu));
+    P.rpi = avg <= 1 ? 1 : avg <= 2 ? 2 : avg <= 4 ? 4 : avg <= 8 ? 8 : avg <= 16 ? 16 : 32;
+    J.max_items = (PT + P.rpi - 1) / P.rpi + n_idx;
+    const int64_t runs_bound = n_idx < n_experts ? n_idx : n_experts;
+    n_items = (PT + P.rpi - 1) / P.rpi + runs_bound;
+    P.items_per_pair = 1;
+    P.n_items_fixed = 0;
+  } else {
+    P.rpi = 32;
+    P.items_per_pair = ceil_div(M, P.rpi);
+    n_items = n_idx * P.items_per_pair;
+    if (n_items > INT32_MAX) return MI_ERR_UNSUPPORTED;
+    P.n_items_fixed = (int)n_items;
+  }
+  const int item_rows = J.use_items ? P.rpi : (int)(M < P.rpi ? M : P.rpi);
+  if (!mi::qmvm_plan_fp(item_rows, P.N, P.K, fpm, n_items, &J.planm)) return MI_ERR_UNSUPPORTED;
+  J.multi_row = true;
+  P.ks = J.planm.ks;
+  J.plan.cfg.grid_z = (int)(n_items < 65535 ? n_items : 65535);
+  if (P.ks > 1 && PT * N >= ((int64_t)1 << 32)) return MI_ERR_UNSUPPORTED;
+  J.items_bytes = J.use_items ? (size_t)J.max_items * 16 + 256 : 0;
+  J.part_bytes = P.ks > 1 ? (size_t)P.ks * PT * N * 4 : 0;
+  return MI_OK;
+}
+
 // Launch a prepared gather on `s`; `ws` holds at least J.ws_bytes() bytes.
 int gather_launch(GatherJob& J, void* ws, hipStream_t s) {
   mi::QmvParams& P = J.P;
@@ -499,6 +564,19 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
     if (n_idx == 0 || M == 0 || N == 0) return MI_OK;
     if (!y || !x || !w || !scales || (fm < 0 && !biases))
       return fail(MI_ERR_INVALID, "null tensor pointer");
+    if (fm >= 0) {  // 2..32-row items on the MFMA kernel
+      GatherJob J;
+      if (gather_prepare_fp(J, fm, gs, y, x, w, scales, lhs_indices, rhs_indices, n_idx,
+                            lhs_div, x_batch, M, N, K, n_experts, sorted_indices) == MI_OK) {
+        hipStream_t s = (hipStream_t)stream;
+        void* data = nullptr;
+        if (J.ws_bytes()) {
+          rc = workspace(s, J.ws_bytes(), &data);
+          if (rc) return rc;
+        }
+        return gather_launch(J, data, s);
+      }
+    }
     hipError_t e = mi::launch_qmv_any_gather(
         (const uint16_t*)x, w, scales, fm < 0 ? (const uint16_t*)biases : nullptr, (uint16_t*)y,
         M, N, K, gs, nb, fm, lhs_indices, rhs_indices, n_idx, lhs_div, x_batch, n_experts,
@@ -535,8 +613,25 @@ int mi_gather_qmm_noalloc(void* y, const void* x, const uint32_t* w, const void*
   int rc = scratch_address(&data);
   if (rc) return rc;
   const int fm = fp_mode_of(mode);
+  if (fm >= 0) {
+    // fp-mode gathers of multi-row items run the MFMA kernel with items / partials in scratch
+    int gs = 0, nb = 0;
+    rc = resolve_fp(fm, group_size, bits, transpose, K, sb_dtype, &gs, &nb);
+    if (rc) return rc;
+    if (x_dtype == MI_DTYPE_BFLOAT16 && n_idx > 0 && M > 0 && N > 0 && lhs_div > 0 && y && x &&
+        w && scales) {
+      GatherJob J;
+      if (gather_prepare_fp(J, fm, gs, y, x, w, scales, lhs_indices, rhs_indices, n_idx,
+                            lhs_div, x_batch, M, N, K, n_experts, sorted_indices) == MI_OK) {
+        if (J.ws_bytes() > kNoAllocScratchBytes)
+          return fail(MI_ERR_WORKSPACE, "gather_qmm_noalloc: the call needs %zu bytes of "
+                      "scratch, the fixed maximum is %zu", J.ws_bytes(), kNoAllocScratchBytes);
+        return gather_launch(J, data, (hipStream_t)stream);
+      }
+    }
+  }
   if (fm >= 0 || (bits.has_value && bits.value != 4 && bits.value != 8 && fm == -1))
-    // the odd-width and fp-mode gathers use no scratch: the allocating entry point
+    // the other odd-width and fp-mode gathers use no scratch: the allocating entry point
     // allocates nothing on that path
     return mi_gather_qmm(y, x, w, scales, biases, lhs_indices, rhs_indices, n_idx, lhs_div,
                          x_batch, M, N, K, n_experts, transpose, group_size, bits, mode,
@@ -572,6 +667,23 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
     if (N > (int64_t)1 << 30 || M > (int64_t)1 << 30 || N * K * 2 > ((int64_t)1 << 34))
       return fail(MI_ERR_INVALID, "N, M or N*K too large");
     hipStream_t s = (hipStream_t)stream;
+    // 1..32 rows: the few-row MFMA kernel (code x scale exact in bf16)
+    static const int fp_mfma = env_int("MI_QMM_FP_MFMA", 1);
+    static const int fp_mfma_min = env_int("MI_QMM_FP_MFMA_MIN", 1);
+    mi::QmvmPlan fp{};
+    if (fp_mfma && M >= fp_mfma_min && M <= 32 &&
+        mi::qmvm_plan_fp((int)M, (int)N, (int)K, fm, 1, &fp)) {
+      mi::QmvmParams Q{x, w, (const uint16_t*)scales, nullptr, (uint16_t*)y, nullptr, (int)M,
+                       (int)N, (int)K, gs, fp.kr, fp.wr};
+      if (fp.part_bytes) {
+        void* data = nullptr;
+        rc = workspace(s, fp.part_bytes, &data);
+        if (rc) return rc;
+        Q.part = (float*)data;
+      }
+      hipError_t e = mi::launch_qmvm(Q, fp, s);
+      return e == hipSuccess ? MI_OK : hip_fail(e, "qmvm fp launch");
+    }
     static const int fp_any_max = env_int("MI_QMM_ANY_MAX", 8);
     if (M <= fp_any_max) {  // decode rows: straight from the packed codes
       hipError_t e = mi::launch_qmv_any((const uint16_t*)x, w, scales, nullptr, (uint16_t*)y, M,
@@ -847,6 +959,33 @@ int mi_gather_qmv_gate_up_swiglu(void* y, const void* x, const uint32_t* w_gate,
   if (T < 0 || k <= 0) return fail(MI_ERR_INVALID, "bad T/k");
   if (!inds && T > 0) return fail(MI_ERR_INVALID, "null indices");
   const int64_t n_idx = T * k;
+  if (const int fm = fp_mode_of(mode); fm >= 0) {
+    // bias-less modes: gate into the workspace, then up with SwiGLU applied as it writes
+    int gs = 0, nb = 0;
+    int rc = resolve_fp(fm, group_size, bits, true, K, MI_DTYPE_UINT8, &gs, &nb);
+    if (rc) return rc;
+    if (T == 0 || N == 0) return MI_OK;
+    if (!y || !x || !w_gate || !s_gate || !w_up || !s_up)
+      return fail(MI_ERR_INVALID, "null tensor pointer");
+    GatherJob G, U;
+    if (gather_prepare_fp(G, fm, gs, y, x, w_gate, s_gate, nullptr, inds, n_idx, k, T, 1, N, K,
+                          n_experts, false) != MI_OK ||
+        gather_prepare_fp(U, fm, gs, y, x, w_up, s_up, nullptr, inds, n_idx, k, T, 1, N, K,
+                          n_experts, false) != MI_OK)
+      return fail(MI_ERR_UNSUPPORTED, "gate/up at mode %s: shape outside the few-row kernel",
+                  mode);
+    hipStream_t s = (hipStream_t)stream;
+    const size_t half = round256((size_t)n_idx * N * 2);
+    void* data = nullptr;
+    rc = workspace(s, half + std::max(G.ws_bytes(), U.ws_bytes()), &data);
+    if (rc) return rc;
+    uint16_t* g = (uint16_t*)data;
+    G.P.y = g;
+    if ((rc = gather_launch(G, (char*)data + half, s)) != MI_OK) return rc;
+    U.P.y = y;
+    U.P.swiglu_gate = g;
+    return gather_launch(U, (char*)data + half, s);
+  }
   GatherJob G, U;
   // Every (token, slot) pair reads its token's row: lhs(i) = i / k.
   int rc = gather_prepare(G, y, x, w_gate, s_gate, b_gate, nullptr, inds, n_idx, k, T, 1, N, K,
@@ -901,6 +1040,12 @@ int mi_moe_route_gate_up_swiglu(void* y, uint32_t* inds, void* scores, const flo
   if (!inds || !scores || !logits) return fail(MI_ERR_INVALID, "null routing pointer");
   if (k > E || k > 64) return fail(MI_ERR_INVALID, "k must be <= min(64, E)");
   const int64_t n_idx = T * k;
+  if (fp_mode_of(mode) >= 0) {  // bias-less modes: route, then the fused gate + up call
+    int rc = mi_moe_route_topk(inds, scores, logits, T, E, k, scores_dtype, stream);
+    if (rc) return rc;
+    return mi_gather_qmv_gate_up_swiglu(y, x, w_gate, s_gate, b_gate, w_up, s_up, b_up, inds, T,
+                                        k, N, K, E, group_size, bits, mode, stream);
+  }
   GatherJob G;
   int rc = gather_prepare(G, y, x, w_gate, s_gate, b_gate, nullptr, inds, n_idx, k, T, 1, N, K, E,
                           true, group_size, bits, mode, false, MI_DTYPE_BFLOAT16,
@@ -938,6 +1083,28 @@ int mi_gather_qmv_down_reduce(void* y, const void* act, const uint32_t* w_down,
   if (T > 65535) return fail(MI_ERR_UNSUPPORTED, "more than 65535 tokens per call");
   if ((!inds || !scores) && T > 0) return fail(MI_ERR_INVALID, "null indices or scores");
   const int64_t n_idx = T * k;
+  if (const int fm = fp_mode_of(mode); fm >= 0) {
+    // bias-less modes: the k down rows per token into the workspace, then the weighted sum
+    int gs = 0, nb = 0;
+    int rc = resolve_fp(fm, group_size, bits, true, K, MI_DTYPE_UINT8, &gs, &nb);
+    if (rc) return rc;
+    if (T == 0 || N == 0) return MI_OK;
+    if (!y || !act || !w_down || !s_down) return fail(MI_ERR_INVALID, "null tensor pointer");
+    GatherJob D;
+    if (gather_prepare_fp(D, fm, gs, y, act, w_down, s_down, nullptr, inds, n_idx, 1, n_idx, 1,
+                          N, K, n_experts, false) != MI_OK)
+      return fail(MI_ERR_UNSUPPORTED, "down at mode %s: shape outside the few-row kernel", mode);
+    hipStream_t s = (hipStream_t)stream;
+    const size_t vb = round256((size_t)n_idx * N * 2);
+    void* data = nullptr;
+    rc = workspace(s, vb + D.ws_bytes(), &data);
+    if (rc) return rc;
+    uint16_t* v = (uint16_t*)data;
+    D.P.y = v;
+    if ((rc = gather_launch(D, (char*)data + vb, s)) != MI_OK) return rc;
+    hipError_t e = mi::launch_down_reduce((uint16_t*)y, v, (const uint16_t*)scores, T, k, N, s);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "down_reduce launch");
+  }
   GatherJob D;
   // act holds one row per (token, slot) pair: lhs(i) = i.
   int rc = gather_prepare(D, y, act, w_down, s_down, b_down, nullptr, inds, n_idx, 1, n_idx, 1, N,

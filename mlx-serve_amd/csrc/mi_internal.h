@@ -85,10 +85,13 @@ struct QmvmParams {
 };
 struct QmvmPlan {
   int wr, ks, kr, waves, nc, xu, depth, tiles, mt, lds, sbf32, rows, bits;
+  int fpm;  // -1 affine; 0 nvfp4, 1 mxfp4 (bias-less, uint8 scales)
   size_t part_bytes;
 };
 // rows = activation rows per call (dense) or per work item (gathers, n_items items).
 bool qmvm_plan(int rows, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan* out);
+// The fp4 modes (fpm 0 nvfp4, 1 mxfp4) at 2..32 rows per call or item.
+bool qmvm_plan_fp(int rows, int N, int K, int fpm, int64_t n_items, QmvmPlan* out);
 hipError_t launch_qmvm(const QmvmParams& P, const QmvmPlan& plan, hipStream_t s);
 hipError_t launch_qmvm_gather(const QmvParams& G, const QmvmPlan& plan, int grid_z, hipStream_t s);
 

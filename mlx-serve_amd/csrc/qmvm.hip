@@ -27,6 +27,30 @@ extern template void launch_family<8, 16, false, false>(const QmvmParams&, const
                                                      const QmvmPlan&, dim3, hipStream_t);
 extern template void launch_family<8, 32, false, false>(const QmvmParams&, const QmvParams&,
                                                      const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 16, false, false, 0>(const QmvmParams&, const QmvParams&,
+                                                        const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 32, false, false, 0>(const QmvmParams&, const QmvParams&,
+                                                        const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 16, false, false, 1>(const QmvmParams&, const QmvParams&,
+                                                        const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 32, false, false, 1>(const QmvmParams&, const QmvParams&,
+                                                        const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 16, false, true, 0>(const QmvmParams&, const QmvParams&,
+                                                       const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 32, false, true, 0>(const QmvmParams&, const QmvParams&,
+                                                       const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 16, false, true, 1>(const QmvmParams&, const QmvParams&,
+                                                       const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 32, false, true, 1>(const QmvmParams&, const QmvParams&,
+                                                       const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<8, 16, false, false, 2>(const QmvmParams&, const QmvParams&,
+                                                        const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<8, 32, false, false, 2>(const QmvmParams&, const QmvParams&,
+                                                        const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<8, 16, false, true, 2>(const QmvmParams&, const QmvParams&,
+                                                        const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<8, 32, false, true, 2>(const QmvmParams&, const QmvParams&,
+                                                        const QmvmPlan&, dim3, hipStream_t);
 extern template void launch_family<4, 64, false, false>(const QmvmParams&, const QmvParams&,
                                                      const QmvmPlan&, dim3, hipStream_t);
 extern template void launch_family<8, 64, false, false>(const QmvmParams&, const QmvParams&,
@@ -62,6 +86,19 @@ void launch_any(QmvmParams P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
   using namespace qmvm_detail;
   P.upr_mr = div_magic((uint32_t)(pl.kr / 8));
   P.spr_mr = div_magic((uint32_t)(pl.kr / P.group_size / 2));
+  if (pl.fpm >= 0) {
+    const bool m16 = pl.mt == 16;
+    if (pl.fpm == 0)
+      m16 ? launch_family<4, 16, false, GATHER, 0>(P, G, pl, grid, s)
+          : launch_family<4, 32, false, GATHER, 0>(P, G, pl, grid, s);
+    else if (pl.fpm == 2)
+      m16 ? launch_family<8, 16, false, GATHER, 2>(P, G, pl, grid, s)
+          : launch_family<8, 32, false, GATHER, 2>(P, G, pl, grid, s);
+    else
+      m16 ? launch_family<4, 16, false, GATHER, 1>(P, G, pl, grid, s)
+          : launch_family<4, 32, false, GATHER, 1>(P, G, pl, grid, s);
+    return;
+  }
   if (pl.bits == 8) {
     if constexpr (!GATHER) {  // 8-bit instances are dense only
       if (pl.mt == 16 && pl.sbf32) launch_family<8, 16, true, false>(P, G, pl, grid, s);
@@ -79,11 +116,15 @@ void launch_any(QmvmParams P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
 
 }  // namespace
 
-bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan* out) {
-  if ((bits != 4 && bits != 8) || M < 2 || M > 64) return false;
+namespace {
+// fpm -1: affine (gs 64, scale/bias pairs staged in LDS); 0 / 1: the fp4 modes (scales
+// loaded with the weights: no staging, no even-group constraint).
+bool plan_impl(int M, int N, int K, int gs, int bits, int64_t n_items, int fpm, QmvmPlan* out) {
+  const bool fp = fpm >= 0;
+  if ((bits != 4 && bits != 8) || M < (fp ? 1 : 2) || M > (fp ? 32 : 64)) return false;
   const int cv = 512 / bits;  // values per 64-byte chunk of a row
   if (K % cv != 0) return false;
-  if (gs != 64) return false;  // the other group sizes take the general decode kernels
+  if (!fp && gs != 64) return false;  // the other group sizes take the general decode kernels
   if ((int64_t)N * (K * bits / 8) >= ((int64_t)1 << 31) || (int64_t)M * K * 2 >= ((int64_t)1 << 31))
     return false;
   static const int env_wr = env_or("MI_QMVM_WR", 0);
@@ -110,22 +151,23 @@ bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan*
       if (nch % ks) continue;
       const int chs = nch / ks;  // chunks per range
       const int nvals = chs * cv;
-      if (gs <= 64 && (nvals / gs) % 2) continue;  // scale/bias pairs: an even group count
+      if (!fp && (nvals / gs) % 2) continue;  // scale/bias pairs: an even group count
       const int max_waves = mt == 64 ? 8 : 16;  // the 64-row instances' launch bound
       for (int wk = 1; wk * wr <= max_waves; ++wk) {
         if (chs % wk) continue;
         const int nc = chs / wk;
         if (nc > 8) continue;
         const int waves = wk * wr;
-        for (int f32 = mt == 16 ? 1 : 0; f32 >= 0; --f32) {
-          const qmvm_detail::QmvmLds L = qmvm_detail::qmvm_lds(mp, nvals, gs, 16 * wr, waves, mt, f32 != 0);
+        for (int f32 = mt == 16 && !fp ? 1 : 0; f32 >= 0; --f32) {
+          qmvm_detail::QmvmLds L = qmvm_detail::qmvm_lds(mp, nvals, gs, 16 * wr, waves, mt, f32 != 0);
+          if (fp) L.sbbytes = 0;
           if ((size_t)L.total() > lds_max) continue;
           const int units = mp * nvals / 8;
           const int xu = (units + 64 * waves - 1) / (64 * waves);
           if (xu > 8) continue;
           const int gr = nvals / gs;
           const int sload = 16 * wr * (gs <= 64 ? gr / 2 : gr);
-          if (sload > 4 * 64 * waves) continue;
+          if (!fp && sload > 4 * 64 * waves) continue;
           const int64_t blocks = (int64_t)tiles * ks * std::max<int64_t>(1, n_items);
           const double cost = 3.0 * (ks - 1) + (blocks < 256 ? 4.0 * (256 - blocks) / 256 : 0) +
                               std::abs(nc - target) + 0.05 * (16 - waves) + (f32 ? 0 : 0.5);
@@ -152,6 +194,7 @@ bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan*
   best.depth = env_depth ? env_depth : 2;
   best.rows = M;
   best.bits = bits;
+  best.fpm = fpm;
   best.part_bytes = best.ks > 1 ? (size_t)best.ks * M * N * 4 : 0;
   static const int verbose = env_or("MI_QMVM_VERBOSE", 0);
   static int64_t last_key = -1;
@@ -163,6 +206,16 @@ bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan*
                  best.lds);
   *out = best;
   return true;
+}
+}  // namespace
+
+bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan* out) {
+  return plan_impl(M, N, K, gs, bits, n_items, -1, out);
+}
+
+bool qmvm_plan_fp(int M, int N, int K, int fpm, int64_t n_items, QmvmPlan* out) {
+  if (fpm < 0 || fpm > 2) return false;
+  return plan_impl(M, N, K, fpm == 0 ? 16 : 32, fpm == 2 ? 8 : 4, n_items, fpm, out);
 }
 
 hipError_t launch_qmvm(const QmvmParams& P, const QmvmPlan& pl, hipStream_t s) {

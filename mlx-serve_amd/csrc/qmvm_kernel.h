@@ -3,6 +3,13 @@
 // weights held in registers) and gather_qmm work items of 2..32 rows (sorted expert runs). The weights stream straight into registers the way the one-row kernel
 // streams them (no LDS copy of the weights).
 //
+// Bias-less fp4 modes (FPM 0 nvfp4: e2m1 codes, 16-value groups, e4m3 scales; FPM 1 mxfp4:
+// 32-value groups, e8m0 scales) share the 4-bit chunk layout and transpose. Their group
+// scale is exact in the product: each 8-code run converts to bf16 pairs of code x scale
+// (v_cvt_scalef32_pk_bf16_fp4), so the MFMA accumulates across groups with no epilogue,
+// no all-ones MFMA and no scale staging; the activations stay in natural order. A lane's
+// scales come with its weight chunk (one dword per 128 codes for mxfp4, two for nvfp4).
+//
 // Block = WR weight tiles of 16 rows x one K range (x one work item for gathers); its W
 // waves are WR x WK: wave (rt, kp) owns tile rt and the kp-th run of NC 128-value chunks
 // of the range. The block stages the range's activations (its rows, nibble-pair order)
@@ -114,10 +121,74 @@ __host__ __device__ inline QmvmLds qmvm_lds(int M, int nvals, int gs, int rows, 
 
 // G is read only by gathers (work items, index arrays, expert bank); dense calls pass
 // their shapes in P.
-template <int BITS, int GS, int NC, int XU, int DEPTH, int MT, bool SBF32, bool GATHER>
+// e4m3 (nvfp4 scales) with the reference's reading of every code as finite, as fp32.
+MI_DEV float fp_e4m3(uint32_t b) {
+  const uint32_t m = b & 0x7Fu, e = m >> 3, f = m & 7u;
+  const float mag = e ? __uint_as_float(((e + 120u) << 23) | (f << 20)) : (float)f * 0.001953125f;
+  return (b & 0x80u) ? -mag : mag;
+}
+
+// 8 e2m1 codes (one per nibble, low nibble first) times one power-of-two scale -> 4 bf16
+// pairs. v_cvt_scalef32_pk_bf16_fp4 reads only the exponent field of its fp32 scale, as an
+// e8m0 byte (0 -> 2^-127), which is exactly mxfp4's scale: pass the byte as the exponent.
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+MI_DEV u32x4_t fp4_run(uint32_t codes, float sc) {
+  return u32x4_t{
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, sc, 0)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, sc, 1)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, sc, 2)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, sc, 3))};
+}
+// nvfp4: e4m3 scales are not powers of two. The code converts to fp32 with the scale's
+// power of two, is multiplied by the scale's signed mantissa factor (exact: at most 2 x 4
+// significant bits) and rounds to bf16 without loss.
+MI_DEV u32x4_t fp4_run_e4m3(uint32_t codes, float sc) {
+  const uint32_t sb = __float_as_uint(sc);
+  const float p = __uint_as_float(sb & 0x7F800000u);
+  const float m = sc == 0.f ? 0.f : __uint_as_float((sb & 0x807FFFFFu) | 0x3F800000u);
+  auto pair = [&](f32x2v v) {
+    const f32x2v w = {v.x * m, v.y * m};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(w, bf16x2v));
+  };
+  return u32x4_t{pair(__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, p, 0)),
+                 pair(__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, p, 1)),
+                 pair(__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, p, 2)),
+                 pair(__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, p, 3))};
+}
+
+// 8 e4m3 codes (two words, low byte first) times an e8m0 scale -> 4 bf16 pairs.
+// v_cvt_scalef32_pk_bf16_fp8 reads 0x7F / 0xFF as NaN; the reference reads them as +-480
+// (2^8 x 1.875), so a word holding one takes the exact per-code route (rare: the
+// largest magnitude of the format).
+MI_DEV uint32_t fp8_pair_exact(uint32_t w, int hi, float sc) {
+  const f32x2v v = {fp_e4m3((w >> (16 * hi)) & 0xFFu) * sc,
+                    fp_e4m3((w >> (16 * hi + 8)) & 0xFFu) * sc};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
+}
+MI_DEV u32x4_t fp8_run(uint32_t w0, uint32_t w1, float sc) {
+  const uint32_t m7 = 0x7F7F7F7Fu, c1 = 0x01010101u, top = 0x80808080u;
+  const bool odd = (((w0 & m7) + c1) | ((w1 & m7) + c1)) & top;
+  if (__builtin_expect(odd, 0)) {
+    const float s = sc == 0.f ? __uint_as_float(0x00400000u) : sc;  // e8m0 byte 0: 2^-127
+    return u32x4_t{fp8_pair_exact(w0, 0, s), fp8_pair_exact(w0, 1, s),
+                   fp8_pair_exact(w1, 0, s), fp8_pair_exact(w1, 1, s)};
+  }
+  return u32x4_t{
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, false)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, true)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, false)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, true))};
+}
+
+template <int BITS, int GS, int NC, int XU, int DEPTH, int MT, bool SBF32, bool GATHER, int FPM = -1>
 // MT 64 keeps four accumulator tiles and the second pass's activations in registers:
 // blocks of up to 8 waves (256 VGPRs per lane) instead of 16.
 __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams P, QmvParams Gp) {
+  constexpr bool FP4 = FPM >= 0;  // any bias-less fp mode (the name predates mxfp8)
+  static_assert(!FP4 || (BITS == (FPM == 2 ? 8 : 4) && MT <= 32),
+                "fp modes: 4-bit (nvfp4, mxfp4) or 8-bit (mxfp8) codes, at most 32 rows");
+  constexpr int FGS = FPM == 0 ? 16 : 32;  // fp group size
   constexpr int CV = 512 / BITS;        // values per 64-byte chunk of a row
   constexpr int NSTEP = CV / 32;        // MFMA steps per chunk
   constexpr float BOFF = BITS == 4 ? -128.f : 0.f;  // 4-bit A holds 128 + q
@@ -141,7 +212,7 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
   const int WR = P.wr;
   const int rt = wave % WR, kp = wave / WR;
   const int i = lane & 15, q = lane >> 4;
-  const int N = P.N, K = P.K, G = K / GS;
+  const int N = P.N, K = P.K, G = K / (FP4 ? FGS : GS);
   const int kb0 = blockIdx.y * P.kr;
   const int nvals = min(K - kb0, P.kr);
   const int gr = nvals / GS, g0 = kb0 / GS;
@@ -181,8 +252,12 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
         __builtin_amdgcn_make_buffer_rsrc((void*)P.x, (short)0, xbytes_all, kBufFlags);
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(P.w + mat * (uint32_t)(K * BITS / 32)), (short)0, N * (K * BITS / 8), kBufFlags);
-    const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(P.scales + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
+    const __amdgpu_buffer_rsrc_t sres =
+        FP4 ? __builtin_amdgcn_make_buffer_rsrc(
+                  (void*)((const unsigned char*)P.scales + mat * (uint32_t)G), (short)0, N * G,
+                  kBufFlags)
+            : __builtin_amdgcn_make_buffer_rsrc((void*)(P.scales + mat * (uint32_t)G), (short)0,
+                                                N * G * 2, kBufFlags);
     const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(P.biases + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
 
@@ -209,7 +284,7 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
     if constexpr (!GATHER) load_x(0);
     uint32_t sv[SU], bv[SU];
 #pragma unroll
-    for (int t = 0; t < SU; ++t) {
+    for (int t = 0; t < (FP4 ? 0 : SU); ++t) {
       const int v = tid + t * BD;
       const int rr = spr == 1 ? v : (int)__umulhi((uint32_t)v, P.spr_mr), gp = v - rr * spr;
       const bool ok = rr < rows && row0 + rr < N;
@@ -227,9 +302,25 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
     const uint32_t wo = (uint32_t)wrow * (uint32_t)(K * BITS / 8) +
                         (uint32_t)(kb0 + c0 * CV) * BITS / 8 + 16 * q;
     u32x4_t wv[NC];
+    // fp scales of the lane's row for chunk j: bytes (4 for mxfp4, 8 for nvfp4, 2 for mxfp8)
+    constexpr int SPC = FPM == 0 ? 8 : FPM == 1 ? 4 : 2;
+    const uint32_t fso = (uint32_t)wrow * (uint32_t)G + (uint32_t)(kb0 + c0 * CV) / FGS;
+    u32x2_t fsw[NC];
+    auto load_fs = [&](int j) __attribute__((always_inline)) {
+      if constexpr (FPM == 0) {
+        fsw[j] = __builtin_bit_cast(
+            u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(sres, fso + SPC * j, 0, 0));
+      } else if constexpr (FPM == 1) {
+        fsw[j].x = __builtin_amdgcn_raw_buffer_load_b32(sres, fso + SPC * j, 0, 0);
+      } else if constexpr (FPM == 2) {
+        fsw[j].x = __builtin_amdgcn_raw_buffer_load_b16(sres, fso + SPC * j, 0, 0);
+      }
+    };
 #pragma unroll
-    for (int j = 0; j < D; ++j)
+    for (int j = 0; j < D; ++j) {
       wv[j] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * j, 0, 0);
+      load_fs(j);
+    }
     if constexpr (GATHER) {
       lds_barrier();  // the row table
       load_x(0);
@@ -243,8 +334,8 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
       const int m = (int)__umulhi((uint32_t)u, P.upr_mr), k8 = u - m * upr;
       const u32x4_t X = xv[t];
       if (m < Mp) {
-        u32x4_t p = X;  // 8-bit: natural order
-        if constexpr (BITS == 4) {
+        u32x4_t p = X;  // 8-bit and fp4: natural order
+        if constexpr (BITS == 4 && !FP4) {
           p.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
           p.y = perm_b32(X.w, X.z, 0x05040100u);  // (x4, x6)
           p.z = perm_b32(X.y, X.x, 0x07060302u);  // (x1, x3)
@@ -256,7 +347,7 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
     };
     stage_x(Mp0);
 #pragma unroll
-    for (int t = 0; t < SU; ++t) {
+    for (int t = 0; t < (FP4 ? 0 : SU); ++t) {
       const int v = tid + t * BD;
       const int rr = spr == 1 ? v : (int)__umulhi((uint32_t)v, P.spr_mr), gp = v - rr * spr;
       if (rr < rows) {
@@ -304,11 +395,54 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
         if constexpr (D < NC) {
-          if (j + D < NC)
+          if (j + D < NC) {
             wv[j + D] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * (j + D), 0, 0);
+            load_fs(j + D);
+          }
         }
         const u32x4_t tw = BITS == 4 ? xpose4(wv[j]) : wv[j];
         const int kc = (c0 + j) * CV;  // chunk start within the range
+        if constexpr (FPM == 2) {
+          // step t: words 2t, 2t+1 of the lane's 16 bytes, codes 16q + 8t .. + 7 of the
+          // chunk, all in group q/2 (byte q/2 of the chunk's two scale bytes)
+          const float sc = __uint_as_float(((fsw[j].x >> (8 * (q >> 1))) & 0xFFu) << 23);
+#pragma unroll
+          for (int t = 0; t < NSTEP; ++t) {
+            const uint32_t w0 = t == 0 ? tw.x : tw.z, w1 = t == 0 ? tw.y : tw.w;
+            const u32x4_t a = fp8_run(w0, w1, sc);
+            const int kb = (kc + 8 * t) * 2;
+#pragma unroll
+            for (int tt = 0; tt < NTP; ++tt) {
+              const u32x4_t b = *reinterpret_cast<const u32x4_t*>(xrow[tt] + kb);
+              acc[tt] = mfma16(a, b, acc[tt]);
+            }
+          }
+          if constexpr (D < NC) __builtin_amdgcn_sched_barrier(0);
+          continue;
+        }
+        if constexpr (FP4) {
+          // run t holds codes 32t + 8q .. + 7 of the chunk: mxfp4 group t (byte t of the
+          // dword), nvfp4 group 2t + q/2 (byte 2t + q/2 of the two dwords)
+#pragma unroll
+          for (int t = 0; t < NSTEP; ++t) {
+            const uint32_t codes = t == 0 ? tw.x : t == 1 ? tw.y : t == 2 ? tw.z : tw.w;
+            u32x4_t a;
+            if constexpr (FPM == 0) {
+              const uint32_t word = t < 2 ? fsw[j].x : fsw[j].y;
+              a = fp4_run_e4m3(codes, fp_e4m3((word >> (8 * (2 * (t & 1) + (q >> 1)))) & 0xFFu));
+            } else {
+              a = fp4_run(codes, __uint_as_float(((fsw[j].x >> (8 * t)) & 0xFFu) << 23));
+            }
+            const int kb = (kc + 32 * t) * 2;
+#pragma unroll
+            for (int tt = 0; tt < NTP; ++tt) {
+              const u32x4_t b = *reinterpret_cast<const u32x4_t*>(xrow[tt] + kb);
+              acc[tt] = mfma16(a, b, acc[tt]);
+            }
+          }
+          if constexpr (D < NC) __builtin_amdgcn_sched_barrier(0);
+          continue;
+        }
         f32x4_t c[NTP], cx[NTP];
 #pragma unroll
         for (int tt = 0; tt < NTP; ++tt) c[tt] = cx[tt] = zero;
@@ -427,18 +561,18 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
 
 // Launches one instance family; explicitly instantiated per (MT, SBF32, GATHER) in
 // qmvm.hip (dense) and qmvm_gather.hip (gathers) so the instances compile in parallel.
-template <int BITS, int MT, bool SBF32, bool GATHER>
+template <int BITS, int MT, bool SBF32, bool GATHER, int FPM = -1>
 void launch_family(const QmvmParams& P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
                    hipStream_t s);
 
-template <int BITS, int NC, int MT, bool SBF32, bool GATHER>
+template <int BITS, int NC, int MT, bool SBF32, bool GATHER, int FPM = -1>
 void launch_xd(const QmvmParams& P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
                hipStream_t s) {
   const dim3 block(64 * pl.waves);
   const size_t lds = (size_t)pl.lds;
 #define MI_QMVM_LAUNCH(XU, DP)                                                              \
   do {                                                                                      \
-    auto k = qmvm_kernel<BITS, 64, NC, XU, DP, MT, SBF32, GATHER>;                          \
+    auto k = qmvm_kernel<BITS, 64, NC, XU, DP, MT, SBF32, GATHER, FPM>;                     \
     static bool attr = false; /* LDS above 64 KiB needs the attribute, once per kernel */ \
     if (!attr) {                                                                            \
       (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, \
@@ -467,18 +601,18 @@ void launch_xd(const QmvmParams& P, const QmvParams& G, const QmvmPlan& pl, dim3
 #undef MI_QMVM_LAUNCH
 }
 
-template <int BITS, int MT, bool SBF32, bool GATHER>
+template <int BITS, int MT, bool SBF32, bool GATHER, int FPM>
 void launch_family(const QmvmParams& P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
                    hipStream_t s) {
   switch (pl.nc) {
-    case 1: launch_xd<BITS, 1, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    case 2: launch_xd<BITS, 2, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    case 3: launch_xd<BITS, 3, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    case 4: launch_xd<BITS, 4, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    case 5: launch_xd<BITS, 5, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    case 6: launch_xd<BITS, 6, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    case 7: launch_xd<BITS, 7, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
-    default: launch_xd<BITS, 8, MT, SBF32, GATHER>(P, G, pl, grid, s); break;
+    case 1: launch_xd<BITS, 1, MT, SBF32, GATHER, FPM>(P, G, pl, grid, s); break;
+    case 2: launch_xd<BITS, 2, MT, SBF32, GATHER, FPM>(P, G, pl, grid, s); break;
+    case 3: launch_xd<BITS, 3, MT, SBF32, GATHER, FPM>(P, G, pl, grid, s); break;
+    case 4: launch_xd<BITS, 4, MT, SBF32, GATHER, FPM>(P, G, pl, grid, s); break;
+    case 5: launch_xd<BITS, 5, MT, SBF32, GATHER, FPM>(P, G, pl, grid, s); break;
+    case 6: launch_xd<BITS, 6, MT, SBF32, GATHER, FPM>(P, G, pl, grid, s); break;
+    case 7: launch_xd<BITS, 7, MT, SBF32, GATHER, FPM>(P, G, pl, grid, s); break;
+    default: launch_xd<BITS, 8, MT, SBF32, GATHER, FPM>(P, G, pl, grid, s); break;
   }
 }
 

@@ -289,7 +289,7 @@ def gather_qmv_gate_up_swiglu(x, wg, sg, bg, wu, su, bu, inds, group_size=None, 
     _contig(x, wg, sg, bg, wu, su, bu, inds)
     T, K = x.shape
     k = inds.shape[-1]
-    gs, nb = _resolve(_packed(wg), sg, group_size, bits, K)
+    gs, nb = _resolve(_packed(wg), sg, group_size, bits, K, mode)
     E, N = wg.shape[0], wg.shape[1]
     y = torch.empty((T, k, N), dtype=x.dtype, device=x.device)
     check(lib().mi_gather_qmv_gate_up_swiglu(_ptr(y), _ptr(x), _ptr(wg), _ptr(sg), _ptr(bg),
@@ -307,7 +307,7 @@ def moe_route_gate_up_swiglu(logits, x, wg, sg, bg, wu, su, bu, k, group_size=No
     _require(logits.dtype == torch.float32, "logits must be float32")
     T, K = x.shape
     E = logits.shape[-1]
-    gs, nb = _resolve(_packed(wg), sg, group_size, bits, K)
+    gs, nb = _resolve(_packed(wg), sg, group_size, bits, K, mode)
     N = wg.shape[1]
     y = torch.empty((T, k, N), dtype=x.dtype, device=x.device)
     inds = torch.empty((T, k), dtype=torch.int32, device=x.device)
@@ -326,7 +326,7 @@ def gather_qmv_down_reduce(act, wd, sd, bd, inds, scores, group_size=None, bits=
     [T, k] -> [T, N]."""
     _contig(act, wd, sd, bd, inds, scores)
     T, k, K = act.shape
-    gs, nb = _resolve(_packed(wd), sd, group_size, bits, K)
+    gs, nb = _resolve(_packed(wd), sd, group_size, bits, K, mode)
     E, N = wd.shape[0], wd.shape[1]
     y = torch.empty((T, N), dtype=act.dtype, device=act.device)
     check(lib().mi_gather_qmv_down_reduce(_ptr(y), _ptr(act), _ptr(wd), _ptr(sd), _ptr(bd),

@@ -247,3 +247,63 @@ def test_route_grouped_matches_oracle(dev, E, k, ng, tg):
     if ng > tg:  # the limit must bite on this data: some rows differ from the unmasked top-k
         free, _ = O.route_grouped(logits, bias, k, ng, ng, True, 2.5)
         assert (np.sort(free, axis=1) != np.sort(ri, axis=1)).any()
+
+
+def _fp_bank(mode, E, N, K, seed):
+    m, bits, gs = O.FP_MODES[mode]
+    rng = np.random.default_rng(seed)
+    q = rng.integers(0, 1 << bits, size=(E * N, K)).astype(np.uint8)
+    lo, hi = (0x20, 0x48) if mode == "nvfp4" else (118, 126)
+    sc = rng.integers(lo, hi, size=(E, N, K // gs)).astype(np.uint8)
+    return O.pack(q, bits).reshape(E, N, -1), sc
+
+
+@pytest.mark.parametrize("mode", ["nvfp4", "mxfp4", "mxfp8"])
+@pytest.mark.parametrize("T", [1, 3])
+def test_fused_decode_mlp_fp_modes(dev, mode, T):
+    """The fused decode MoE entry points at the bias-less modes: gate + up + SwiGLU and
+    down + slot sum are bit-equal to the split calls (gather_qmm, swiglu, moe_down_reduce),
+    the routed variant equals route + fused, and the whole MLP is within tolerance of fp64."""
+    _print_case(t="fused_fp", mode=mode, T=T)
+    E, k, N, K = 16, 4, 256, 512
+    wg, sg = _fp_bank(mode, E, N, K, 70)
+    wu, su = _fp_bank(mode, E, N, K, 71)
+    wd, sd = _fp_bank(mode, E, K, N, 72)
+    D = lambda a: to_dev_u32(a, dev)
+    S = lambda a: torch.from_numpy(a).to(dev)
+    x = O.make_x_bf16(T, K, 73)
+    logits = torch.from_numpy(O.randn(T * E, 74).reshape(T, E)).to(dev)
+    inds, sc = mi_qmm.moe_route_topk(logits, k, torch.bfloat16)
+    xd = to_dev_bf16(x, dev)
+    act = mi_qmm.gather_qmv_gate_up_swiglu(xd, D(wg), S(sg), None, D(wu), S(su), None, inds,
+                                           mode=mode)
+    # split: two gathers and SwiGLU
+    lhs = to_dev_u32(np.repeat(np.arange(T, dtype=np.uint32), k), dev)
+    rhs = inds.reshape(-1)
+    g = mi_qmm.gather_qmm(xd.view(T, 1, K), D(wg), S(sg), None, lhs_indices=lhs,
+                          rhs_indices=rhs, mode=mode)
+    u = mi_qmm.gather_qmm(xd.view(T, 1, K), D(wu), S(su), None, lhs_indices=lhs,
+                          rhs_indices=rhs, mode=mode)
+    act_split = mi_qmm.swiglu(g, u).view(T, k, N)
+    assert np.array_equal(bf16_bits(act), bf16_bits(act_split))
+    a2, i2, s2 = mi_qmm.moe_route_gate_up_swiglu(logits, xd, D(wg), S(sg), None, D(wu), S(su),
+                                                 None, k, mode=mode)
+    assert torch.equal(i2.view(torch.int32), inds.view(torch.int32))
+    assert np.array_equal(bf16_bits(a2), bf16_bits(act))
+    y = mi_qmm.gather_qmv_down_reduce(act, D(wd), S(sd), None, inds, sc, mode=mode)
+    v = mi_qmm.gather_qmm(act.view(T * k, 1, N), D(wd), S(sd), None, rhs_indices=rhs, mode=mode)
+    y_split = mi_qmm.moe_down_reduce(v.view(T, k, K), sc)
+    assert np.array_equal(bf16_bits(y), bf16_bits(y_split))
+    # fp64 truth of the whole routed MLP over the same routing
+    ii = inds.view(torch.int32).cpu().numpy()
+    scf = sc.float().cpu().numpy().astype(np.float64)
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    deq = lambda w, s_, e: O.dequantize_fp(w[e], s_[e], mode).astype(np.float64)
+    want = np.zeros((T, K))
+    for t in range(T):
+        for j in range(k):
+            e = ii[t, j]
+            gg, uu = xf[t] @ deq(wg, sg, e).T, xf[t] @ deq(wu, su, e).T
+            h = gg / (1.0 + np.exp(-gg)) * uu
+            want[t] += scf[t, j] * (h @ deq(wd, sd, e).T)
+    assert max_err_ratio(to_f64(y), want) <= 3 * BF16_TOL

@@ -355,6 +355,70 @@ def test_qmm_fp_modes(dev, mode, M, N, K):
     assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
 
 
+@pytest.mark.parametrize("mode", ["nvfp4", "mxfp4", "mxfp8"])
+@pytest.mark.parametrize("M,N,K", [(2, 100, 2048), (7, 64, 512), (16, 256, 4096), (17, 48, 7168),
+                                   (32, 512, 14336), (24, 80, 384)])
+def test_qmm_fp4_mfma(dev, mode, M, N, K):
+    """Bias-less modes at 2..32 rows (the few-row MFMA kernel: code x scale converted to bf16,
+    exact, per 8-code run; mxfp8's 0x7F / 0xFF codes take the exact per-code route; K = 14336
+    at 32 rows takes the K split)."""
+    _print_case(t="qmm_fp4_mfma", mode=mode, M=M, N=N, K=K)
+    wq, sc = _fp_weight(mode, N, K, 50 + M)
+    x = O.make_x_bf16(M, K, 51 + N)
+    y = mi_qmm.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(wq, dev),
+                                torch.from_numpy(sc).to(dev), None, True, mode=mode)
+    truth = O.bf16_to_f32(x).astype(np.float64) @ O.dequantize_fp(wq, sc, mode).astype(np.float64).T
+    assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+
+
+@pytest.mark.parametrize("mode", ["nvfp4", "mxfp4"])
+def test_qmm_fp4_mfma_scale_edges(dev, mode):
+    """Scale bytes at the ends of their formats: e4m3 0x7F (480 in the reference's
+    reading) and 0x01 (2^-9), e8m0 1 and 254 groups mixed with ordinary ones."""
+    _print_case(t="qmm_fp4_edges", mode=mode)
+    N, K, M = 64, 512, 8
+    wq, sc = _fp_weight(mode, N, K, 77)
+    if mode == "nvfp4":
+        sc[0, :] = 0x7F
+        sc[1, 2] = 0x01
+        sc[2, 5] = 0x80 | 0x30  # a negative scale
+    else:
+        sc[0, 1] = 1
+        sc[1, :] = 140  # 2^13
+    x = O.make_x_bf16(M, K, 78)
+    y = mi_qmm.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(wq, dev),
+                                torch.from_numpy(sc).to(dev), None, True, mode=mode)
+    truth = O.bf16_to_f32(x).astype(np.float64) @ O.dequantize_fp(wq, sc, mode).astype(np.float64).T
+    yf = to_f64(y)
+    for n in range(N):  # per output column: the scales differ by orders of magnitude
+        assert max_err_ratio(yf[:, n:n + 1], truth[:, n:n + 1]) <= BF16_TOL, n
+
+
+@pytest.mark.parametrize("mode", ["nvfp4", "mxfp4", "mxfp8"])
+def test_gather_fp4_sorted(dev, mode):
+    """Sorted fp4 gather of a skewed MoE routing (T = 64, k = 8, 16 experts): runs of
+    several rows per expert become work items of the MFMA kernel."""
+    _print_case(t="gather_fp4_sorted", mode=mode)
+    E, N, K, T, k = 16, 96, 1024, 64, 8
+    banks = [_fp_weight(mode, N, K, 60 + e) for e in range(E)]
+    wq = np.stack([bk[0] for bk in banks])
+    sc = np.stack([bk[1] for bk in banks])
+    rng = np.random.default_rng(61)
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.uint32)
+    flat = inds.reshape(-1)
+    order = np.argsort(flat, kind="stable").astype(np.uint32)
+    srt = flat[order]
+    lhs = (order // k).astype(np.uint32)
+    x = O.make_x_bf16(T, K, 62)
+    y = mi_qmm.gather_qmm(to_dev_bf16(x, dev).reshape(T, 1, K), to_dev_u32(wq, dev),
+                          torch.from_numpy(sc).to(dev), None, lhs_indices=to_dev_u32(lhs, dev),
+                          rhs_indices=to_dev_u32(srt, dev), mode=mode, sorted_indices=True)
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    wd = [O.dequantize_fp(wq[e], sc[e], mode).astype(np.float64) for e in range(E)]
+    truth = np.stack([xf[lhs[i]] @ wd[srt[i]].T for i in range(T * k)])
+    assert max_err_ratio(to_f64(y).reshape(T * k, N), truth) <= BF16_TOL
+
+
 def test_graph_replay_after_workspace_growth(dev):
     """A sorted gather captured in a HIP graph keeps its workspace address; a later,
     larger uncaptured call grows the workspace, and every replay of the old graph must

@@ -52,6 +52,30 @@ def test_noalloc_matches_gather(dev, first, second):
         assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("mode", ["nvfp4", "mxfp4", "mxfp8"])
+def test_noalloc_matches_gather_fp4(dev, mode):
+    """fp4 sorted gathers (work items in scratch) through both entry points, two calls in a
+    row, the second smaller."""
+    for i, (E, N, K, T, topk) in enumerate(((16, 96, 4096, 64, 8), (8, 64, 1024, 16, 4))):
+        _case(t="noalloc_fp4", mode=mode, call=i)
+        m, bits, gs = O.FP_MODES[mode]
+        rng = np.random.default_rng(400 + i)
+        q = rng.integers(0, 1 << bits, size=(E * N, K)).astype(np.uint8)
+        wq = O.pack(q, bits).reshape(E, N, -1)
+        lo, hi = (0x20, 0x48) if mode == "nvfp4" else (118, 126)
+        sc = rng.integers(lo, hi, size=(E, N, K // gs)).astype(np.uint8)
+        flat = np.concatenate([rng.permutation(E)[:topk] for _ in range(T)]).astype(np.uint32)
+        _, _, srt, lhs = O.sort_dispatch(flat, topk)
+        x = to_dev_bf16(O.make_x_bf16(T, K, 401 + i).reshape(T, 1, K), dev)
+        W, S = to_dev_u32(wq, dev), torch.from_numpy(sc).to(dev)
+        kw = dict(lhs_indices=to_dev_u32(lhs, dev), rhs_indices=to_dev_u32(srt, dev),
+                  mode=mode, sorted_indices=True)
+        y0 = mi_qmm.gather_qmm(x, W, S, None, noalloc=True, **kw)
+        y1 = mi_qmm.gather_qmm(x, W, S, None, **kw)
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(y0), bf16_bits(y1))
+
+
 def test_noalloc_rejects_oversized_scratch(dev):
     """4M one-row pairs need 128 MiB of work items: refused before any launch."""
     _case(t="noalloc_oversize")
