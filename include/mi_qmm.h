@@ -71,8 +71,8 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
 /* Replaces mlx_gather_qmm (src/mlx.zig:265), transpose=true, mode "affine":
  *   y[i] = x[lhs(i)] @ dequant(w[rhs(i)])^T      for i in [0, n_idx)
  * x: [x_batch, M, K]; w: [n_experts, N, K*bits/32]; scales/biases [n_experts, N, K/gs];
- * y: [n_idx, M, N]. Formats as mi_quantized_matmul; affine 2/3/5/6 bits and the fp
- * modes take at most 8 rows per pair and bfloat16 x (else MI_ERR_UNSUPPORTED).
+ * y: [n_idx, M, N]. Formats as mi_quantized_matmul; affine 2/3/5/6 bits take at most 8
+ * rows per pair, and they and the fp modes take bfloat16 x only (else MI_ERR_UNSUPPORTED).
  * lhs_indices may be NULL: lhs(i) = i / lhs_div (lhs_div=1 is MLX's
  * default arange; lhs_div=top_k is one token broadcast over its top-k slots, the
  * reference's decode call). rhs_indices may be NULL: rhs(i) = i.
@@ -202,7 +202,8 @@ int mi_moe_down_reduce(void* y, const void* v, const void* scores, int64_t T, in
 /* Replaces gatherQmvGateUp (src/transformer.zig:20303-20396): for each token t and slot s,
  * g = x[t] @ dequant(w_gate[inds[t*k+s]])^T and u likewise, each rounded to bf16, then
  * y[t*k+s] = swiglu(g, u) exactly as mi_swiglu. x [T, K] bf16, y [T*k, N] bf16. Bit-equal
- * to two mi_gather_qmm calls followed by mi_swiglu. */
+ * to two mi_gather_qmm calls followed by mi_swiglu. Formats: affine 4/8 bits, and the
+ * bias-less modes nvfp4 / mxfp4 / mxfp8 (b_gate / b_up NULL, uint8 scales). */
 int mi_gather_qmv_gate_up_swiglu(void* y, const void* x, const uint32_t* w_gate,
                                  const void* s_gate, const void* b_gate, const uint32_t* w_up,
                                  const void* s_up, const void* b_up, const uint32_t* inds,
@@ -227,7 +228,7 @@ int mi_moe_route_gate_up_swiglu(void* y, uint32_t* inds, void* scores, const flo
 /* Replaces gatherQmvDownReduce (src/transformer.zig:20675-20761): v[t*k+s] =
  * act[t*k+s] @ dequant(w_down[inds[t*k+s]])^T rounded to bf16, then y[t] as
  * mi_moe_down_reduce. act [T*k, K] bf16, scores [T*k] bf16, y [T, N] bf16. Bit-equal to
- * mi_gather_qmm followed by mi_moe_down_reduce. */
+ * mi_gather_qmm followed by mi_moe_down_reduce. Formats as mi_gather_qmv_gate_up_swiglu. */
 int mi_gather_qmv_down_reduce(void* y, const void* act, const uint32_t* w_down,
                               const void* s_down, const void* b_down, const uint32_t* inds,
                               const void* scores, int64_t T, int k, int64_t N, int64_t K,
