@@ -402,24 +402,26 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
   return MI_OK;
 }
 
-// fp-mode gathers (nvfp4 fpm 0, mxfp4 1, mxfp8 2) on the few-row MFMA kernel: sorted runs
+// fp-mode gathers (nvfp4 fpm 0, mxfp4 1, mxfp8 2) and affine 2/3/5/6-bit gathers (fpm
+// 100 + bits, gs 64) on the few-row MFMA kernel: sorted runs
 // cut into work items as for the affine kernels, unsorted pairs one item per pair (and
 // 32-row slice). Returns MI_ERR_UNSUPPORTED when the call does not fit the plan: the
 // caller then takes the per-pair kernel, which serves up to 8 rows per pair.
 int gather_prepare_fp(GatherJob& J, int fpm, int gs, void* y, const void* x, const uint32_t* w,
-                      const void* scales, const uint32_t* lhs_indices,
+                      const void* scales, const void* biases, const uint32_t* lhs_indices,
                       const uint32_t* rhs_indices, int64_t n_idx, int64_t lhs_div,
                       int64_t x_batch, int64_t M, int64_t N, int64_t K, int64_t n_experts,
                       bool sorted_indices) {
   static const int use_fp_mfma = env_int("MI_QMM_FP_MFMA", 1);
-  if (!use_fp_mfma || fpm < 0 || fpm > 2) return MI_ERR_UNSUPPORTED;
+  const bool odd = fpm >= 100;
+  if (!use_fp_mfma || fpm < 0 || (fpm > 2 && !odd)) return MI_ERR_UNSUPPORTED;
   if (N > (int64_t)1 << 30 || M > (int64_t)1 << 30 || n_idx * M >= ((int64_t)1 << 32) ||
       x_batch * M * K * 2 >= ((int64_t)1 << 32) || x_batch == 0 || n_experts == 0)
     return MI_ERR_UNSUPPORTED;
   mi::QmvParams& P = J.P;
   P.w = w;
-  P.scales = (const uint16_t*)scales;  // uint8 scales; the kernel reads them as bytes
-  P.biases = nullptr;
+  P.scales = (const uint16_t*)scales;  // fp modes: uint8 scales, read as bytes
+  P.biases = odd ? (const uint16_t*)biases : nullptr;
   P.x = x;
   P.y = y;
   P.lhs = lhs_indices;
@@ -431,7 +433,7 @@ int gather_prepare_fp(GatherJob& J, int fpm, int gs, void* y, const void* x, con
   P.M = (int)M;
   P.N = (int)N;
   P.K = (int)K;
-  P.bits = fpm == 2 ? 8 : 4;
+  P.bits = odd ? fpm - 100 : fpm == 2 ? 8 : 4;
   P.group_size = gs;
   P.x_f32 = 0;
   J.use_items = sorted_indices && rhs_indices != nullptr && n_idx > 1;
@@ -457,7 +459,9 @@ int gather_prepare_fp(GatherJob& J, int fpm, int gs, void* y, const void* x, con
     P.n_items_fixed = (int)n_items;
   }
   const int item_rows = J.use_items ? P.rpi : (int)(M < P.rpi ? M : P.rpi);
-  if (!mi::qmvm_plan_fp(item_rows, P.N, P.K, fpm, n_items, &J.planm)) return MI_ERR_UNSUPPORTED;
+  if (!(odd ? mi::qmvm_plan_odd(item_rows, P.N, P.K, gs, fpm - 100, n_items, &J.planm)
+            : mi::qmvm_plan_fp(item_rows, P.N, P.K, fpm, n_items, &J.planm)))
+    return MI_ERR_UNSUPPORTED;
   J.multi_row = true;
   P.ks = J.planm.ks;
   J.plan.cfg.grid_z = (int)(n_items < 65535 ? n_items : 65535);
@@ -564,10 +568,11 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
     if (n_idx == 0 || M == 0 || N == 0) return MI_OK;
     if (!y || !x || !w || !scales || (fm < 0 && !biases))
       return fail(MI_ERR_INVALID, "null tensor pointer");
-    if (fm >= 0) {  // 2..32-row items on the MFMA kernel
+    {  // items of up to 32 rows on the MFMA kernel
       GatherJob J;
-      if (gather_prepare_fp(J, fm, gs, y, x, w, scales, lhs_indices, rhs_indices, n_idx,
-                            lhs_div, x_batch, M, N, K, n_experts, sorted_indices) == MI_OK) {
+      if (gather_prepare_fp(J, fm >= 0 ? fm : 100 + nb, gs, y, x, w, scales, biases,
+                            lhs_indices, rhs_indices, n_idx, lhs_div, x_batch, M, N, K,
+                            n_experts, sorted_indices) == MI_OK) {
         hipStream_t s = (hipStream_t)stream;
         void* data = nullptr;
         if (J.ws_bytes()) {
@@ -613,16 +618,19 @@ int mi_gather_qmm_noalloc(void* y, const void* x, const uint32_t* w, const void*
   int rc = scratch_address(&data);
   if (rc) return rc;
   const int fm = fp_mode_of(mode);
-  if (fm >= 0) {
-    // fp-mode gathers of multi-row items run the MFMA kernel with items / partials in scratch
+  const bool odd_w = fm == -1 && bits.has_value && bits.value != 4 && bits.value != 8;
+  if (fm >= 0 || odd_w) {
+    // fp-mode and odd-width gathers run the MFMA kernel with items / partials in scratch
     int gs = 0, nb = 0;
-    rc = resolve_fp(fm, group_size, bits, transpose, K, sb_dtype, &gs, &nb);
+    rc = fm >= 0 ? resolve_fp(fm, group_size, bits, transpose, K, sb_dtype, &gs, &nb)
+                 : resolve_common(group_size, bits, mode, transpose, K, &gs, &nb);
     if (rc) return rc;
     if (x_dtype == MI_DTYPE_BFLOAT16 && n_idx > 0 && M > 0 && N > 0 && lhs_div > 0 && y && x &&
-        w && scales) {
+        w && scales && (fm >= 0 || (biases && sb_dtype == MI_DTYPE_BFLOAT16))) {
       GatherJob J;
-      if (gather_prepare_fp(J, fm, gs, y, x, w, scales, lhs_indices, rhs_indices, n_idx,
-                            lhs_div, x_batch, M, N, K, n_experts, sorted_indices) == MI_OK) {
+      if (gather_prepare_fp(J, fm >= 0 ? fm : 100 + nb, gs, y, x, w, scales, biases,
+                            lhs_indices, rhs_indices, n_idx, lhs_div, x_batch, M, N, K,
+                            n_experts, sorted_indices) == MI_OK) {
         if (J.ws_bytes() > kNoAllocScratchBytes)
           return fail(MI_ERR_WORKSPACE, "gather_qmm_noalloc: the call needs %zu bytes of "
                       "scratch, the fixed maximum is %zu", J.ws_bytes(), kNoAllocScratchBytes);
@@ -738,6 +746,22 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   const bool odd_width = nb != 4 && nb != 8;
   if (odd_width && (x_dtype != MI_DTYPE_BFLOAT16 || N * K * 2 > ((int64_t)1 << 34)))
     return fail(MI_ERR_UNSUPPORTED, "bits=%d: bf16 activations only", nb);
+  static const int odd_mfma = env_int("MI_QMM_ODD_MFMA", 1);
+  mi::QmvmPlan op{};
+  // 2..32 rows, gs 64 (and one row at 2 bits, where the per-code kernel is VALU-bound)
+  if (odd_width && odd_mfma && M <= 32 && (M >= 2 || nb == 2) &&
+      mi::qmvm_plan_odd((int)M, (int)N, (int)K, gs, nb, 1, &op)) {
+    mi::QmvmParams Q{x, w, (const uint16_t*)scales, (const uint16_t*)biases, (uint16_t*)y,
+                     nullptr, (int)M, (int)N, (int)K, gs, op.kr, op.wr};
+    if (op.part_bytes) {
+      void* data = nullptr;
+      rc = workspace(s, op.part_bytes, &data);
+      if (rc) return rc;
+      Q.part = (float*)data;
+    }
+    hipError_t e = mi::launch_qmvm(Q, op, s);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "qmvm odd-width launch");
+  }
   static const int any_max = env_int("MI_QMM_ANY_MAX", 8);
   if (odd_width && M <= any_max) {  // decode rows: straight from the packed bitstream
     hipError_t e = mi::launch_qmv_any((const uint16_t*)x, w, scales, (const uint16_t*)biases,
@@ -968,10 +992,10 @@ int mi_gather_qmv_gate_up_swiglu(void* y, const void* x, const uint32_t* w_gate,
     if (!y || !x || !w_gate || !s_gate || !w_up || !s_up)
       return fail(MI_ERR_INVALID, "null tensor pointer");
     GatherJob G, U;
-    if (gather_prepare_fp(G, fm, gs, y, x, w_gate, s_gate, nullptr, inds, n_idx, k, T, 1, N, K,
-                          n_experts, false) != MI_OK ||
-        gather_prepare_fp(U, fm, gs, y, x, w_up, s_up, nullptr, inds, n_idx, k, T, 1, N, K,
-                          n_experts, false) != MI_OK)
+    if (gather_prepare_fp(G, fm, gs, y, x, w_gate, s_gate, nullptr, nullptr, inds, n_idx, k, T,
+                          1, N, K, n_experts, false) != MI_OK ||
+        gather_prepare_fp(U, fm, gs, y, x, w_up, s_up, nullptr, nullptr, inds, n_idx, k, T, 1,
+                          N, K, n_experts, false) != MI_OK)
       return fail(MI_ERR_UNSUPPORTED, "gate/up at mode %s: shape outside the few-row kernel",
                   mode);
     hipStream_t s = (hipStream_t)stream;
@@ -1091,8 +1115,8 @@ int mi_gather_qmv_down_reduce(void* y, const void* act, const uint32_t* w_down,
     if (T == 0 || N == 0) return MI_OK;
     if (!y || !act || !w_down || !s_down) return fail(MI_ERR_INVALID, "null tensor pointer");
     GatherJob D;
-    if (gather_prepare_fp(D, fm, gs, y, act, w_down, s_down, nullptr, inds, n_idx, 1, n_idx, 1,
-                          N, K, n_experts, false) != MI_OK)
+    if (gather_prepare_fp(D, fm, gs, y, act, w_down, s_down, nullptr, nullptr, inds, n_idx, 1,
+                          n_idx, 1, N, K, n_experts, false) != MI_OK)
       return fail(MI_ERR_UNSUPPORTED, "down at mode %s: shape outside the few-row kernel", mode);
     hipStream_t s = (hipStream_t)stream;
     const size_t vb = round256((size_t)n_idx * N * 2);

@@ -85,13 +85,15 @@ struct QmvmParams {
 };
 struct QmvmPlan {
   int wr, ks, kr, waves, nc, xu, depth, tiles, mt, lds, sbf32, rows, bits;
-  int fpm;  // -1 affine; 0 nvfp4, 1 mxfp4 (bias-less, uint8 scales)
+  int fpm;  // -1 affine 4/8 bits; 0 nvfp4, 1 mxfp4, 2 mxfp8 (uint8 scales); 100 + b: affine b bits
   size_t part_bytes;
 };
 // rows = activation rows per call (dense) or per work item (gathers, n_items items).
 bool qmvm_plan(int rows, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan* out);
-// The fp4 modes (fpm 0 nvfp4, 1 mxfp4) at 2..32 rows per call or item.
+// The fp modes (fpm 0 nvfp4, 1 mxfp4, 2 mxfp8) at 1..32 rows per call or item.
 bool qmvm_plan_fp(int rows, int N, int K, int fpm, int64_t n_items, QmvmPlan* out);
+// Affine 2/3/5/6 bits (gs 64) at 1..32 rows per call or item.
+bool qmvm_plan_odd(int rows, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan* out);
 hipError_t launch_qmvm(const QmvmParams& P, const QmvmPlan& plan, hipStream_t s);
 hipError_t launch_qmvm_gather(const QmvParams& G, const QmvmPlan& plan, int grid_z, hipStream_t s);
 

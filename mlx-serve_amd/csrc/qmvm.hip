@@ -51,6 +51,38 @@ extern template void launch_family<8, 16, false, true, 2>(const QmvmParams&, con
                                                         const QmvmPlan&, dim3, hipStream_t);
 extern template void launch_family<8, 32, false, true, 2>(const QmvmParams&, const QmvParams&,
                                                         const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 16, false, false, 102>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 32, false, false, 102>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 16, false, true, 102>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 32, false, true, 102>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 16, false, false, 103>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 32, false, false, 103>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 16, false, true, 103>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 32, false, true, 103>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 16, false, false, 105>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 32, false, false, 105>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 16, false, true, 105>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 32, false, true, 105>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 16, false, false, 106>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 32, false, false, 106>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 16, false, true, 106>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
+extern template void launch_family<4, 32, false, true, 106>(const QmvmParams&, const QmvParams&,
+                                                           const QmvmPlan&, dim3, hipStream_t);
 extern template void launch_family<4, 64, false, false>(const QmvmParams&, const QmvParams&,
                                                      const QmvmPlan&, dim3, hipStream_t);
 extern template void launch_family<8, 64, false, false>(const QmvmParams&, const QmvParams&,
@@ -86,6 +118,20 @@ void launch_any(QmvmParams P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
   using namespace qmvm_detail;
   P.upr_mr = div_magic((uint32_t)(pl.kr / 8));
   P.spr_mr = div_magic((uint32_t)(pl.kr / P.group_size / 2));
+  if (pl.fpm >= 100) {  // affine 2/3/5/6 bits
+    const bool m16 = pl.mt == 16;
+    switch (pl.fpm) {
+      case 102: m16 ? launch_family<4, 16, false, GATHER, 102>(P, G, pl, grid, s)
+                    : launch_family<4, 32, false, GATHER, 102>(P, G, pl, grid, s); break;
+      case 103: m16 ? launch_family<4, 16, false, GATHER, 103>(P, G, pl, grid, s)
+                    : launch_family<4, 32, false, GATHER, 103>(P, G, pl, grid, s); break;
+      case 105: m16 ? launch_family<4, 16, false, GATHER, 105>(P, G, pl, grid, s)
+                    : launch_family<4, 32, false, GATHER, 105>(P, G, pl, grid, s); break;
+      default: m16 ? launch_family<4, 16, false, GATHER, 106>(P, G, pl, grid, s)
+                   : launch_family<4, 32, false, GATHER, 106>(P, G, pl, grid, s); break;
+    }
+    return;
+  }
   if (pl.fpm >= 0) {
     const bool m16 = pl.mt == 16;
     if (pl.fpm == 0)
@@ -117,11 +163,14 @@ void launch_any(QmvmParams P, const QmvParams& G, const QmvmPlan& pl, dim3 grid,
 }  // namespace
 
 namespace {
-// fpm -1: affine (gs 64, scale/bias pairs staged in LDS); 0 / 1: the fp4 modes (scales
-// loaded with the weights: no staging, no even-group constraint).
+// fpm -1: affine (gs 64, scale/bias pairs staged in LDS); 0 / 1 / 2: the fp modes (scales
+// loaded with the weights: no staging, no even-group constraint); 100 + b: affine b = 2, 3,
+// 5, 6 bits on the 4-bit layout (bits = 4 here), staged like the affine 4-bit plans.
 bool plan_impl(int M, int N, int K, int gs, int bits, int64_t n_items, int fpm, QmvmPlan* out) {
-  const bool fp = fpm >= 0;
-  if ((bits != 4 && bits != 8) || M < (fp ? 1 : 2) || M > (fp ? 32 : 64)) return false;
+  const bool fp = fpm >= 0 && fpm < 100, odd = fpm >= 100;
+  if ((bits != 4 && bits != 8) || M < (fp || odd ? 1 : 2) || M > (fp || odd ? 32 : 64))
+    return false;
+  if (odd && (int64_t)N * (K * (fpm - 100) / 8) >= ((int64_t)1 << 31)) return false;
   const int cv = 512 / bits;  // values per 64-byte chunk of a row
   if (K % cv != 0) return false;
   if (!fp && gs != 64) return false;  // the other group sizes take the general decode kernels
@@ -158,7 +207,7 @@ bool plan_impl(int M, int N, int K, int gs, int bits, int64_t n_items, int fpm, 
         const int nc = chs / wk;
         if (nc > 8) continue;
         const int waves = wk * wr;
-        for (int f32 = mt == 16 && !fp ? 1 : 0; f32 >= 0; --f32) {
+        for (int f32 = mt == 16 && !fp && !odd ? 1 : 0; f32 >= 0; --f32) {
           qmvm_detail::QmvmLds L = qmvm_detail::qmvm_lds(mp, nvals, gs, 16 * wr, waves, mt, f32 != 0);
           if (fp) L.sbbytes = 0;
           if ((size_t)L.total() > lds_max) continue;
@@ -211,6 +260,11 @@ bool plan_impl(int M, int N, int K, int gs, int bits, int64_t n_items, int fpm, 
 
 bool qmvm_plan(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan* out) {
   return plan_impl(M, N, K, gs, bits, n_items, -1, out);
+}
+
+bool qmvm_plan_odd(int M, int N, int K, int gs, int bits, int64_t n_items, QmvmPlan* out) {
+  if (bits != 2 && bits != 3 && bits != 5 && bits != 6) return false;
+  return plan_impl(M, N, K, gs, 4, n_items, 100 + bits, out);
 }
 
 bool qmvm_plan_fp(int M, int N, int K, int fpm, int64_t n_items, QmvmPlan* out) {

@@ -10,6 +10,13 @@
 // no all-ones MFMA and no scale staging; the activations stay in natural order. A lane's
 // scales come with its weight chunk (one dword per 128 codes for mxfp4, two for nvfp4).
 //
+// Affine 2/3/5/6-bit weights (FPM 100 + bits) keep the 4-bit instances' k mapping (step t
+// = codes 32t..32t+31 of a 128-code chunk, lane block q = codes 32t + 8q..+7) and their
+// affine epilogue; only the loads and the unpack differ. A row is one LSB-first bitstream,
+// so a lane's 8 codes are `bits` bytes at byte 4t bits + q bits of the chunk: one 8-byte
+// load from the dword below them covers them at every width, and the codes come out of
+// a 64-bit shift as bf16 0x43qq (= 128 + q) pairs in natural order.
+//
 // Block = WR weight tiles of 16 rows x one K range (x one work item for gathers); its W
 // waves are WR x WK: wave (rt, kp) owns tile rt and the kp-th run of NC 128-value chunks
 // of the range. The block stages the range's activations (its rows, nibble-pair order)
@@ -181,13 +188,32 @@ MI_DEV u32x4_t fp8_run(uint32_t w0, uint32_t w1, float sc) {
       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, true))};
 }
 
+// 8 codes of `OB` bits (LSB-first, starting `sh` bits into the 64-bit pair d1:d0) ->
+// bf16 pairs (128 + q0, 128 + q1) .. (128 + q6, 128 + q7).
+template <int OB>
+MI_DEV u32x4_t odd_run(uint32_t d0, uint32_t d1, uint32_t sh) {
+  const uint64_t v = ((((uint64_t)d1) << 32) | d0) >> sh;
+  constexpr uint32_t mask = (1u << OB) - 1u;
+  auto pr = [&](int p) {
+    const uint32_t c0 = (uint32_t)(v >> (2 * p * OB)) & mask;
+    const uint32_t c1 = (uint32_t)(v >> ((2 * p + 1) * OB)) & mask;
+    return (c0 | (c1 << 16)) | 0x43004300u;
+  };
+  return u32x4_t{pr(0), pr(1), pr(2), pr(3)};
+}
+
 template <int BITS, int GS, int NC, int XU, int DEPTH, int MT, bool SBF32, bool GATHER, int FPM = -1>
 // MT 64 keeps four accumulator tiles and the second pass's activations in registers:
 // blocks of up to 8 waves (256 VGPRs per lane) instead of 16.
 __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams P, QmvParams Gp) {
-  constexpr bool FP4 = FPM >= 0;  // any bias-less fp mode (the name predates mxfp8)
+  constexpr bool FP4 = FPM >= 0 && FPM < 100;  // any bias-less fp mode (the name predates mxfp8)
+  constexpr bool ODD = FPM >= 100;             // affine 2/3/5/6 bits, 4-bit chunk layout
+  constexpr int OB = ODD ? FPM - 100 : 0;
   static_assert(!FP4 || (BITS == (FPM == 2 ? 8 : 4) && MT <= 32),
                 "fp modes: 4-bit (nvfp4, mxfp4) or 8-bit (mxfp8) codes, at most 32 rows");
+  static_assert(!ODD || (BITS == 4 && MT <= 32 && (OB == 2 || OB == 3 || OB == 5 || OB == 6)),
+                "odd widths: 2/3/5/6 bits on the 4-bit layout, at most 32 rows");
+  constexpr int WB = ODD ? OB : BITS;  // stored bits per code
   constexpr int FGS = FPM == 0 ? 16 : 32;  // fp group size
   constexpr int CV = 512 / BITS;        // values per 64-byte chunk of a row
   constexpr int NSTEP = CV / 32;        // MFMA steps per chunk
@@ -251,7 +277,7 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
     const __amdgpu_buffer_rsrc_t xres =
         __builtin_amdgcn_make_buffer_rsrc((void*)P.x, (short)0, xbytes_all, kBufFlags);
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(P.w + mat * (uint32_t)(K * BITS / 32)), (short)0, N * (K * BITS / 8), kBufFlags);
+        (void*)(P.w + mat * (uint32_t)(K * WB / 32)), (short)0, N * (K * WB / 8), kBufFlags);
     const __amdgpu_buffer_rsrc_t sres =
         FP4 ? __builtin_amdgcn_make_buffer_rsrc(
                   (void*)((const unsigned char*)P.scales + mat * (uint32_t)G), (short)0, N * G,
@@ -299,9 +325,26 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
       }
     }
     const int wrow = min(row0 + rt * 16 + i, N - 1);
-    const uint32_t wo = (uint32_t)wrow * (uint32_t)(K * BITS / 8) +
-                        (uint32_t)(kb0 + c0 * CV) * BITS / 8 + 16 * q;
-    u32x4_t wv[NC];
+    const uint32_t wo = ODD ? (uint32_t)wrow * (uint32_t)(K * WB / 8) +
+                                  (uint32_t)(kb0 + c0 * CV) * WB / 8 + ((uint32_t)(q * OB) & ~3u)
+                            : (uint32_t)wrow * (uint32_t)(K * BITS / 8) +
+                                  (uint32_t)(kb0 + c0 * CV) * BITS / 8 + 16 * q;
+    const uint32_t osh = (uint32_t)(q * OB & 3) * 8;  // odd widths: bits below the lane's codes
+    u32x4_t wv[NC], wv2[NC];  // odd widths: steps 0, 1 in wv and 2, 3 in wv2 (two dwords each)
+    auto load_w = [&](int j) __attribute__((always_inline)) {
+      if constexpr (ODD) {
+        const uint32_t o = wo + 16 * OB * j;  // a chunk is 128 codes = 16 OB bytes
+        auto ld = [&](int t) {
+          return __builtin_bit_cast(
+              u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(wres, o + 4 * OB * t, 0, 0));
+        };
+        const u32x2_t s0 = ld(0), s1 = ld(1), s2 = ld(2), s3 = ld(3);
+        wv[j] = u32x4_t{s0.x, s0.y, s1.x, s1.y};
+        wv2[j] = u32x4_t{s2.x, s2.y, s3.x, s3.y};
+      } else {
+        wv[j] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * j, 0, 0);
+      }
+    };
     // fp scales of the lane's row for chunk j: bytes (4 for mxfp4, 8 for nvfp4, 2 for mxfp8)
     constexpr int SPC = FPM == 0 ? 8 : FPM == 1 ? 4 : 2;
     const uint32_t fso = (uint32_t)wrow * (uint32_t)G + (uint32_t)(kb0 + c0 * CV) / FGS;
@@ -318,7 +361,7 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
     };
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-      wv[j] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * j, 0, 0);
+      load_w(j);
       load_fs(j);
     }
     if constexpr (GATHER) {
@@ -334,8 +377,8 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
       const int m = (int)__umulhi((uint32_t)u, P.upr_mr), k8 = u - m * upr;
       const u32x4_t X = xv[t];
       if (m < Mp) {
-        u32x4_t p = X;  // 8-bit and fp4: natural order
-        if constexpr (BITS == 4 && !FP4) {
+        u32x4_t p = X;  // 8-bit, fp modes and odd widths: natural order
+        if constexpr (BITS == 4 && !FP4 && !ODD) {
           p.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
           p.y = perm_b32(X.w, X.z, 0x05040100u);  // (x4, x6)
           p.z = perm_b32(X.y, X.x, 0x07060302u);  // (x1, x3)
@@ -396,11 +439,11 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
       for (int j = 0; j < NC; ++j) {
         if constexpr (D < NC) {
           if (j + D < NC) {
-            wv[j + D] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * (j + D), 0, 0);
+            load_w(j + D);
             load_fs(j + D);
           }
         }
-        const u32x4_t tw = BITS == 4 ? xpose4(wv[j]) : wv[j];
+        const u32x4_t tw = BITS == 4 && !ODD ? xpose4(wv[j]) : wv[j];
         const int kc = (c0 + j) * CV;  // chunk start within the range
         if constexpr (FPM == 2) {
           // step t: words 2t, 2t+1 of the lane's 16 bytes, codes 16q + 8t .. + 7 of the
@@ -449,7 +492,10 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
 #pragma unroll
         for (int t = 0; t < NSTEP; ++t) {
           u32x4_t a;
-          if constexpr (BITS == 4) {
+          if constexpr (ODD) {
+            const u32x4_t& h = t < 2 ? wv[j] : wv2[j];
+            a = (t & 1) ? odd_run<OB>(h.z, h.w, osh) : odd_run<OB>(h.x, h.y, osh);
+          } else if constexpr (BITS == 4) {
             a = unpack8(t == 0 ? tw.x : t == 1 ? tw.y : t == 2 ? tw.z : tw.w);
           } else {
             a = t == 0 ? unpack8b(tw.x, tw.y) : unpack8b(tw.z, tw.w);
@@ -581,8 +627,9 @@ void launch_xd(const QmvmParams& P, const QmvParams& G, const QmvmPlan& pl, dim3
     }                                                                                       \
     hipLaunchKernelGGL(k, grid, block, lds, s, P, G);                                       \
   } while (0)
-  bool d2 = false;
-  if constexpr (NC > 2) d2 = pl.depth == 2;
+  // odd widths: the plans' two-chunk window only (fewer instances)
+  bool d2 = FPM >= 100;
+  if constexpr (NC > 2) d2 = d2 || pl.depth == 2;
   if (d2) {
     switch (pl.xu) {
       case 1: MI_QMVM_LAUNCH(1, 2); break;
@@ -590,7 +637,7 @@ void launch_xd(const QmvmParams& P, const QmvParams& G, const QmvmPlan& pl, dim3
       case 4: MI_QMVM_LAUNCH(4, 2); break;
       default: MI_QMVM_LAUNCH(8, 2); break;
     }
-  } else {
+  } else if constexpr (FPM < 100) {
     switch (pl.xu) {
       case 1: MI_QMVM_LAUNCH(1, 4); break;
       case 2: MI_QMVM_LAUNCH(2, 4); break;

@@ -419,6 +419,44 @@ def test_gather_fp4_sorted(dev, mode):
     assert max_err_ratio(to_f64(y).reshape(T * k, N), truth) <= BF16_TOL
 
 
+@pytest.mark.parametrize("bits", [2, 3, 5, 6])
+@pytest.mark.parametrize("M,N,K", [(1, 200, 4096), (5, 64, 512), (16, 96, 2048), (32, 256, 14336),
+                                   (24, 40, 384)])
+def test_qmm_odd_mfma(dev, bits, M, N, K):
+    """Affine 2/3/5/6 bits, gs 64, 1..32 rows on the few-row MFMA kernel (8 codes per lane
+    from one 8-byte load of the row's bitstream; K = 14336 at 32 rows takes the K split)."""
+    _print_case(t="qmm_odd_mfma", M=M, N=N, K=K, bits=bits)
+    wq, s, b = weights(1, N, K, bits, 64, 90 + bits + M)
+    x = O.make_x_bf16(M, K, 91 + N)
+    y = mi_qmm.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(wq[0], dev),
+                                to_dev_bf16(s[0], dev), to_dev_bf16(b[0], dev), True, 64, bits)
+    truth = O.qmm_f64(x, wq[0], s[0], b[0], 64, bits)
+    assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+
+
+@pytest.mark.parametrize("bits", [2, 3, 5, 6])
+def test_gather_odd_sorted(dev, bits):
+    """Sorted odd-width gather (T = 64, k = 8, 16 experts): multi-row work items of the MFMA
+    kernel, against the oracle."""
+    _print_case(t="gather_odd_sorted", bits=bits)
+    E, N, K, T, k = 16, 96, 1024, 64, 8
+    wq, s, b = weights(E, N, K, bits, 64, 95 + bits)
+    rng = np.random.default_rng(96)
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.uint32)
+    flat = inds.reshape(-1)
+    order = np.argsort(flat, kind="stable").astype(np.uint32)
+    srt = flat[order]
+    lhs = (order // k).astype(np.uint32)
+    x = O.make_x_bf16(T, K, 97)
+    y = mi_qmm.gather_qmm(to_dev_bf16(x, dev).reshape(T, 1, K), to_dev_u32(wq, dev),
+                          to_dev_bf16(s, dev), to_dev_bf16(b, dev), lhs_indices=to_dev_u32(lhs, dev),
+                          rhs_indices=to_dev_u32(srt, dev), group_size=64, bits=bits,
+                          sorted_indices=True)
+    truth = O.gather_qmm_f64(x.reshape(T, 1, K), wq, s, b, lhs, srt, T * k, group_size=64,
+                             bits=bits)
+    assert max_err_ratio(to_f64(y).reshape(T * k, 1, N), truth) <= BF16_TOL
+
+
 def test_graph_replay_after_workspace_growth(dev):
     """A sorted gather captured in a HIP graph keeps its workspace address; a later,
     larger uncaptured call grows the workspace, and every replay of the old graph must
