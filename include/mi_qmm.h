@@ -71,8 +71,9 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
 /* Replaces mlx_gather_qmm (src/mlx.zig:265), transpose=true, mode "affine":
  *   y[i] = x[lhs(i)] @ dequant(w[rhs(i)])^T      for i in [0, n_idx)
  * x: [x_batch, M, K]; w: [n_experts, N, K*bits/32]; scales/biases [n_experts, N, K/gs];
- * y: [n_idx, M, N]. Formats as mi_quantized_matmul; affine 2/3/5/6 bits take at most 8
- * rows per pair, and they and the fp modes take bfloat16 x only (else MI_ERR_UNSUPPORTED).
+ * y: [n_idx, M, N]. Formats as mi_quantized_matmul; affine 2/3/5/6 bits at group sizes
+ * other than 64 take at most 8 rows per pair, and they and the fp modes take bfloat16 x
+ * only (else MI_ERR_UNSUPPORTED).
  * lhs_indices may be NULL: lhs(i) = i / lhs_div (lhs_div=1 is MLX's
  * default arange; lhs_div=top_k is one token broadcast over its top-k slots, the
  * reference's decode call). rhs_indices may be NULL: rhs(i) = i.
