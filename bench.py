@@ -465,6 +465,22 @@ def main():
             extra[f"q8_M{M}_tok_s"] = round(r["tokens_per_s"], 1)
         del layers8
         torch.cuda.empty_cache()
+        # the other formats at M = 1 and 8 (16 layers: 0.5 GB and up, beyond the caches)
+        for b in (2, 3, 5, 6):
+            lo = build_mlp_layers(torch, mi, 16, b, gs, dev)
+            for M in (1, 8):
+                r = decode_mlp(torch, mi, lo, M, b, gs, dev, max(5, args.steps // 5), 2)
+                extra[f"q{b}_M{M}_GBs"] = round(r["GBs"], 1)
+            del lo
+            torch.cuda.empty_cache()
+        for fm, (fgs, fb) in FP_MODES.items():
+            lo = build_fp_layers(torch, 16, fm, dev)
+            for M in (1, 8):
+                r = decode_mlp(torch, mi, lo, M, fb, fgs, dev, max(5, args.steps // 5), 2,
+                               mode=fm)
+                extra[f"{fm}_M{M}_GBs"] = round(r["GBs"], 1)
+            del lo
+            torch.cuda.empty_cache()
         extra.update(single_qmv(torch, mi, dev))
         extra.update(prefill(torch, mi, dev, (512, 2048, 8192)))
         extra.update(moe_layer(torch, mi, dev, 3, 128, 2048, 768, 8, (1, 512)))
