@@ -457,6 +457,38 @@ def test_gather_odd_sorted(dev, bits):
     assert max_err_ratio(to_f64(y).reshape(T * k, 1, N), truth) <= BF16_TOL
 
 
+@pytest.mark.parametrize("mode", ["nvfp4", "mxfp4", "mxfp8"])
+@pytest.mark.parametrize("sorted_", [False, True])
+def test_gather_fp_out_of_range_is_nan(dev, mode, sorted_):
+    """An expert id past the bank gives a NaN row on the fp-mode MFMA path too (sorted work
+    items and unsorted pairs); every other row matches the oracle."""
+    _print_case(t="gather_fp_oob", mode=mode, sorted=sorted_)
+    E, N, K, T, k = 6, 64, 512, 8, 2
+    banks = [_fp_weight(mode, N, K, 110 + e) for e in range(E)]
+    wq = np.stack([bk[0] for bk in banks])
+    sc = np.stack([bk[1] for bk in banks])
+    rng = np.random.default_rng(111)
+    flat = rng.integers(0, E, size=T * k).astype(np.uint32)
+    flat[5] = E + 3
+    if sorted_:
+        order = np.argsort(flat, kind="stable").astype(np.uint32)
+        rhs, lhs = flat[order], (order // k).astype(np.uint32)
+    else:
+        rhs, lhs = flat, (np.arange(T * k) // k).astype(np.uint32)
+    x = O.make_x_bf16(T, K, 112)
+    y = mi_qmm.gather_qmm(to_dev_bf16(x, dev).reshape(T, 1, K), to_dev_u32(wq, dev),
+                          torch.from_numpy(sc).to(dev), None, lhs_indices=to_dev_u32(lhs, dev),
+                          rhs_indices=to_dev_u32(rhs, dev), mode=mode, sorted_indices=sorted_)
+    yf = to_f64(y).reshape(T * k, N)
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    for i in range(T * k):
+        if rhs[i] >= E:
+            assert np.isnan(yf[i]).all(), i
+        else:
+            truth = xf[lhs[i]] @ O.dequantize_fp(wq[rhs[i]], sc[rhs[i]], mode).astype(np.float64).T
+            assert max_err_ratio(yf[i:i + 1], truth[None]) <= BF16_TOL, i
+
+
 def test_graph_replay_after_workspace_growth(dev):
     """A sorted gather captured in a HIP graph keeps its workspace address; a later,
     larger uncaptured call grows the workspace, and every replay of the old graph must
