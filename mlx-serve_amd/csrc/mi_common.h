@@ -29,8 +29,17 @@ MI_DEV uint16_t bf16_mul(uint16_t a, uint16_t b) {
 
 // Sigmoid of a bf16 value, rounded once to fp32 from a double evaluation and then to
 // bf16: the correctly rounded table value for all but astronomically rare inputs.
+// Fast path: the fp32 evaluation 1/(1+expf(-v)) is within 3 fp32 ulp of that fp32
+// rounding (expf <= 1 ulp, the add and the correctly rounded divide 0.5 ulp each), so both
+// round to the same bf16 unless a bf16 rounding midpoint (low 16 bits 0x8000) lies within
+// 8 ulp of it; those values, and v <= -80 (where expf(-v) overflows while the true value
+// is still a representable fp32), take the double evaluation.
 MI_DEV uint16_t sigmoid_bf16(uint16_t g) {
-  const double v = (double)bf16_bits_to_f32(g);
+  const float vf = bf16_bits_to_f32(g);
+  const float sf = 1.f / (1.f + expf(-vf));
+  const uint32_t lo = __float_as_uint(sf) & 0xFFFFu;
+  if (vf > -80.f && lo - (0x8000u - 8u) > 16u) return (uint16_t)f32_to_bf16_bits(sf);
+  const double v = (double)vf;
   const float s = (float)(1.0 / (1.0 + exp(-v)));
   return (uint16_t)f32_to_bf16_bits(s);
 }

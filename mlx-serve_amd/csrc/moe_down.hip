@@ -36,6 +36,8 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDownParams P) {
   constexpr int GS = 64;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ int okf[16];
+  __shared__ uint16_t score_l[16];
+  __shared__ uint16_t prod[16][16];  // [slot][row]: bf16(bf16(v_s) * score_s)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int W = blockDim.x >> 6;
@@ -56,7 +58,9 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDownParams P) {
   const uint32_t nn = (uint32_t)min(n, N - 1);
   const int c0 = kp * NC;
 
-  // 1. loads: this slot's activation row, scale/bias dwords, then the weights.
+  // 1. loads: the token's scores, this slot's activation row, scale/bias dwords, then the
+  //    weights. Everything is in flight before the first wait.
+  const uint16_t my_score = tid < k ? P.scores[(int64_t)t * k + tid] : (uint16_t)0;
   const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(P.act + pair * K), (short)0, K * 2, kBufFlags);
   const size_t mat = (size_t)e * (uint32_t)N;
@@ -107,6 +111,7 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDownParams P) {
     }
   }
   if (kp == 0 && lane == 0) okf[s] = ok;
+  if (tid < k) score_l[tid] = my_score;
   lds_barrier();
 
   // 3. dot products of the wave's chunks.
@@ -129,20 +134,23 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDownParams P) {
     yv = fmaf(fmaf(-128.f, sc, bi), xsum[off >> 5], yv);
   }
 
-  // 4. reduce the row's 4 lanes, then per slot over its waves, then the slots in order.
+  // 4. reduce the row's 4 lanes, then per slot over its waves (one thread per slot and
+  //    row), then the slots in ascending order.
   yv += quad_xor1(yv);
   yv += quad_xor2(yv);
   if (g == 0) red[wave * 16 + r] = yv;
   lds_barrier();
+  if (tid < 16 * k) {
+    const int s2 = tid >> 4, row = tid & 15;
+    float v = 0.f;
+    for (int w2 = 0; w2 < WS; ++w2) v += red[(s2 * WS + w2) * 16 + row];
+    if (!okf[s2]) v = __builtin_nanf("");
+    prod[s2][row] = bf16_mul((uint16_t)f32_to_bf16_bits(v), score_l[s2]);
+  }
+  lds_barrier();
   if (tid < 16 && tile * 16 + tid < N) {
     uint16_t total = 0;  // bf16 zero
-    for (int s2 = 0; s2 < k; ++s2) {
-      float v = 0.f;
-      for (int w2 = 0; w2 < WS; ++w2) v += red[(s2 * WS + w2) * 16 + tid];
-      if (!okf[s2]) v = __builtin_nanf("");
-      const uint16_t vb = (uint16_t)f32_to_bf16_bits(v);
-      total = bf16_add_bits(total, bf16_mul(vb, P.scores[(int64_t)t * k + s2]));
-    }
+    for (int s2 = 0; s2 < k; ++s2) total = bf16_add_bits(total, prod[s2][tid]);
     P.y[(int64_t)t * N + tile * 16 + tid] = total;
   }
   (void)W;
@@ -152,7 +160,7 @@ template <int NC, int XU>
 void launch_one(const MoeDownParams& P, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
   static const bool big_lds = hipFuncSetAttribute(
       reinterpret_cast<const void*>(&moe_down_kernel<NC, XU>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 256) == hipSuccess;
+      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024) == hipSuccess;
   (void)big_lds;  // a failure shows as a launch error for plans above 64 KiB
   hipLaunchKernelGGL((moe_down_kernel<NC, XU>), grid, block, lds, s, P);
 }
@@ -177,7 +185,7 @@ bool moe_down_supported(int64_t T, int k, int64_t N, int64_t K, int gs, int bits
   if (N * (K / 2) >= ((int64_t)1 << 31) || k * ws > 16 || ws * nc != K / 128) return false;
   if (!((nc >= 1 && nc <= 8) || nc == 10 || nc == 12 || nc == 14 || nc == 16)) return false;
   const size_t lds = (size_t)k * (K * 2 + (K / 32) * 4) + (size_t)k * ws * 16 * 4;
-  return (K / 8 + 64 * ws - 1) / (64 * ws) <= 8 && lds <= 160 * 1024 - 256;
+  return (K / 8 + 64 * ws - 1) / (64 * ws) <= 8 && lds <= 160 * 1024 - 1024;
 }
 
 hipError_t launch_moe_down(uint16_t* y, const uint16_t* act, const uint32_t* w,
@@ -210,3 +218,4 @@ hipError_t launch_moe_down(uint16_t* y, const uint16_t* act, const uint32_t* w,
 }
 
 }  // namespace mi
+

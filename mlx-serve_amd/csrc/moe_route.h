@@ -64,25 +64,71 @@ MI_DEV float unord_f32(uint32_t u) {
 
 }  // namespace route_detail
 
+// Wave maximum of a 32-bit key, the same butterfly as wave_reduce_f32.
+MI_DEV uint32_t wave_max_u32(uint32_t v, int lane) {
+  using namespace route_detail;
+  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  v = mx(v, dpp_u32<0xB1>(v));
+  v = mx(v, dpp_u32<0x4E>(v));
+  v = mx(v, dpp_u32<0x141>(v));
+  v = mx(v, dpp_u32<0x140>(v));
+  v = mx(v, xor16_u32(v, lane));
+  v = mx(v, xor32_u32(v, lane));
+  return v;
+}
+
+// k rounds of selection over order-preserving 32-bit keys of the ids lane + 64 j (key 0:
+// not a candidate). Each round takes the wave's largest key and, among the ids holding
+// it, the lowest (ids ascend with j, then with the lane: one ballot per j); that id's key
+// becomes 0. A round with no candidate takes id r and key 0. Lane r < k ends with round
+// r's id and key. Every lane of the wave must call it.
+template <int NV>
+MI_DEV void select_topk(uint32_t (&key)[NV], int k, int lane, uint32_t& sel_i,
+                        uint32_t& sel_key) {
+  sel_i = 0;
+  sel_key = 0;
+  for (int r = 0; r < k; ++r) {
+    uint32_t lb = key[0];
+#pragma unroll
+    for (int j = 1; j < NV; ++j) lb = key[j] > lb ? key[j] : lb;
+    const uint32_t m = __builtin_amdgcn_readfirstlane(wave_max_u32(lb, lane));
+    uint32_t bi = (uint32_t)r;
+    if (m) {
+      bi = 0xFFFFFFFFu;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const uint64_t b = __builtin_amdgcn_ballot_w64(key[j] == m);
+        if (bi == 0xFFFFFFFFu && b) bi = 64u * j + (uint32_t)__builtin_ctzll(b);
+      }
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+        if ((uint32_t)(lane + 64 * j) == bi) key[j] = 0;  // taken
+    }
+    if (lane == r) {
+      sel_i = bi;
+      sel_key = m;
+    }
+  }
+}
+
 // Softmax over the E logits of `row`, top-k, weights renormalized over the k selected.
 // Lane r < k ends with slot r: its expert id and its weight (slots in descending logit
-// order, ties to the lower id). Selection key = (ordered value, ~expert id): the wave
-// maximum is the larger logit, the lower id on ties; NaN logits and taken experts have
-// key 0 and never win (a round with no candidate takes id r, as an all-NaN row does).
-// NV = ceil(E / 64) values per lane. Every lane of the wave must call it.
+// order, ties to the lower id). NaN logits never win; a round with no candidate takes id
+// r with a NaN weight, as an all-NaN row does. NV = ceil(E / 64) values per lane. Every
+// lane of the wave must call it.
 template <int NV>
 MI_DEV void route_token(const float* __restrict__ row, int E, int k, int lane, uint32_t& sel_i,
                         float& weight) {
   using namespace route_detail;
   float v[NV];
-  uint64_t key[NV];
+  uint32_t key[NV];
   float mx = -INFINITY;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int e = lane + 64 * j;
     v[j] = e < E ? row[e] : -INFINITY;
     mx = fmaxf(mx, v[j]);
-    key[j] = (e < E && v[j] == v[j]) ? ((uint64_t)ord_f32(v[j]) << 32) | (uint32_t)~e : 0;
+    key[j] = (e < E && v[j] == v[j]) ? ord_f32(v[j]) : 0u;  // never 0 for a non-NaN
   }
   mx = wave_reduce_f32<true>(mx, lane);
   float den = 0.f;
@@ -91,27 +137,14 @@ MI_DEV void route_token(const float* __restrict__ row, int E, int k, int lane, u
     if (lane + 64 * j < E) den += expf(v[j] - mx);
   den = wave_reduce_f32<false>(den, lane);
 
-  sel_i = 0;
-  float sel_v = 0.f;
-  for (int r = 0; r < k; ++r) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) best = key[j] > best ? key[j] : best;
-    best = wave_max_u64(best, lane);
-    const uint32_t bi = best ? ~(uint32_t)best : (uint32_t)r;
-    const float bv = best ? unord_f32((uint32_t)(best >> 32)) : NAN;
-#pragma unroll
-    for (int j = 0; j < NV; ++j)
-      if (best && (uint32_t)(lane + 64 * j) == bi) key[j] = 0;  // taken
-    if (lane == r) {
-      sel_i = bi;
-      sel_v = bv;
-    }
-  }
+  uint32_t sel_key;
+  select_topk<NV>(key, k, lane, sel_i, sel_key);
+  const float sel_v = sel_key ? unord_f32(sel_key) : NAN;
   // Renormalized softmax weights of the selected experts; slot r lives in lane r.
   const float w = lane < k ? expf(sel_v - mx) / den : 0.f;
   float sum = 0.f;
-  for (int r = 0; r < k; ++r) sum += __shfl(w, r, 64);  // ascending slot order
+  for (int r = 0; r < k; ++r)  // ascending slot order
+    sum += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(w), r));
   weight = w / sum;
 }
 

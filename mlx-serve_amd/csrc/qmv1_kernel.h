@@ -318,8 +318,9 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
           if (wave == 0) {
             uint32_t sel;
             float w;
-            route_token<4>(P.route_logits + (int64_t)t * P.route_E, P.route_E, P.route_k, lane,
-                           sel, w);
+            const float* lg = P.route_logits + (int64_t)t * P.route_E;
+            if (P.route_E <= 128) route_token<2>(lg, P.route_E, P.route_k, lane, sel, w);
+            else route_token<4>(lg, P.route_E, P.route_k, lane, sel, w);
             if (lane == slot) {
               route_expert = sel;
               if (tile == 0 && ks == 0) {

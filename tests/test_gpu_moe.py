@@ -97,6 +97,12 @@ def test_swiglu_exhaustive(dev):
     g8, u8 = g[: g.size // 8 * 8], u[: g.size // 8 * 8]
     y8 = mi_qmm.swiglu(to_dev_bf16(g8, dev), to_dev_bf16(u8, dev))
     assert np.array_equal(bf16_bits(y8), O.swiglu_bf16(g8, u8))
+    # u = 1 and u = 2^-10: the output is bf16(g * sigmoid(g)) (scaled exactly), so a wrong
+    # sigmoid rounding shows up unless the product's rounding hides it
+    for uv in (0x3F80, 0x3A80):
+        u1 = np.full(g.size, uv, dtype=np.uint16)
+        y1 = mi_qmm.swiglu(to_dev_bf16(g, dev), to_dev_bf16(u1, dev))
+        assert np.array_equal(bf16_bits(y1), O.swiglu_bf16(g, u1))
 
 
 @pytest.mark.parametrize("N", [2048, 2044])
