@@ -319,8 +319,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
             uint32_t sel;
             float w;
             const float* lg = P.route_logits + (int64_t)t * P.route_E;
-            if (P.route_E <= 128) route_token<2>(lg, P.route_E, P.route_k, lane, sel, w);
-            else route_token<4>(lg, P.route_E, P.route_k, lane, sel, w);
+            route_token<4>(lg, P.route_E, P.route_k, lane, sel, w);
             if (lane == slot) {
               route_expert = sel;
               if (tile == 0 && ks == 0) {
