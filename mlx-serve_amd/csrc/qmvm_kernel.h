@@ -115,13 +115,19 @@ struct QmvmLds {
   }
 };
 
+// Row stride (in (group, row) entries) of the staged scale/bias table: padded past the
+// block's rows so that the staging writes of one row's consecutive groups, 2 x stride words
+// apart, fall in different banks (a multiple of 64 words put them all in one bank), while
+// the 16-byte reads of 4 rows stay aligned.
+__host__ __device__ inline int qmvm_sb_stride(int rows, bool sbf32) { return rows + (sbf32 ? 2 : 4); }
+
 __host__ __device__ inline QmvmLds qmvm_lds(int M, int nvals, int gs, int rows, int waves, int mt,
                                             bool sbf32) {
   QmvmLds L;
   L.xstride = nvals * 2 + 16;  // +16 B: the 16 rows of a B read start in different banks
   L.xbytes = M * L.xstride;
   // per group and row: fp32 (s, b - 128 s), or the bf16 pair (s, b) when LDS is tight
-  L.sbbytes = (nvals / gs) * rows * (sbf32 ? 8 : 4);
+  L.sbbytes = (nvals / gs) * qmvm_sb_stride(rows, sbf32) * (sbf32 ? 8 : 4);
   L.redbytes = waves * 16 * mt * 4;
   return L;
 }
@@ -243,6 +249,7 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
   const int nvals = min(K - kb0, P.kr);
   const int gr = nvals / GS, g0 = kb0 / GS;
   const int rows = 16 * WR;
+  const int rs = qmvm_sb_stride(rows, SBF32);  // staged scale/bias row stride
   const int row0 = blockIdx.x * rows;
   const int upr = nvals / 8;  // staging units per activation row
   const int spr = PAIRS ? gr / 2 : gr;  // scale/bias loads per row
@@ -397,20 +404,20 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
         if constexpr (!SBF32) {
           uint32_t* sbu = reinterpret_cast<uint32_t*>(sb);
           if constexpr (PAIRS) {
-            sbu[(2 * gp) * rows + rr] = perm_b32(bv[t], sv[t], 0x05040100u);
-            sbu[(2 * gp + 1) * rows + rr] = perm_b32(bv[t], sv[t], 0x07060302u);
+            sbu[(2 * gp) * rs + rr] = perm_b32(bv[t], sv[t], 0x05040100u);
+            sbu[(2 * gp + 1) * rs + rr] = perm_b32(bv[t], sv[t], 0x07060302u);
           } else {
-            sbu[gp * rows + rr] = (sv[t] & 0xFFFFu) | (bv[t] << 16);
+            sbu[gp * rs + rr] = (sv[t] & 0xFFFFu) | (bv[t] << 16);
           }
         } else if constexpr (PAIRS) {
           const float s0 = lo_bf16(sv[t]), s1 = hi_bf16(sv[t]);
-          *reinterpret_cast<f32x2_t*>(sb + 2 * ((2 * gp) * rows + rr)) =
+          *reinterpret_cast<f32x2_t*>(sb + 2 * ((2 * gp) * rs + rr)) =
               f32x2_t{s0, fmaf(BOFF, s0, lo_bf16(bv[t]))};
-          *reinterpret_cast<f32x2_t*>(sb + 2 * ((2 * gp + 1) * rows + rr)) =
+          *reinterpret_cast<f32x2_t*>(sb + 2 * ((2 * gp + 1) * rs + rr)) =
               f32x2_t{s1, fmaf(BOFF, s1, hi_bf16(bv[t]))};
         } else {
           const float s0 = lo_bf16(sv[t]);
-          *reinterpret_cast<f32x2_t*>(sb + 2 * (gp * rows + rr)) =
+          *reinterpret_cast<f32x2_t*>(sb + 2 * (gp * rs + rr)) =
               f32x2_t{s0, fmaf(BOFF, s0, lo_bf16(bv[t]))};
         }
       }
@@ -434,7 +441,7 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
 #pragma unroll
       for (int tt = 0; tt < NTP; ++tt) xrow[tt] = xs + min(16 * tt + i, Mp - 1) * L.xstride + QB * q;
       // per-group pointer, stepped by one group at a time (no multiplies in the loop)
-      const float* sbp = sb + SBW * ((c0 * GPC) * rows + rt * 16 + 4 * q);
+      const float* sbp = sb + SBW * ((c0 * GPC) * rs + rt * 16 + 4 * q);
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
         if constexpr (D < NC) {
@@ -525,7 +532,7 @@ __global__ void __launch_bounds__(MT == 64 ? 512 : 1024) qmvm_kernel(QmvmParams 
               sb23.z = lo_bf16(ev.w);
               sb23.w = fmaf(BOFF, sb23.z, hi_bf16(ev.w));
             }
-            sbp += SBW * rows;
+            sbp += SBW * rs;
 #pragma unroll
             for (int tt = 0; tt < NTP; ++tt) {
               f32x4_t& ac = acc[tt];
