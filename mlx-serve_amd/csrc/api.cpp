@@ -786,20 +786,38 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   // 2..64 rows: the few-row MFMA kernel (33..64 rows as two 32-row passes per block)
   static const int use_qmvm = env_int("MI_QMM_QMVM", 1);
   static const int qmvm_max = env_int("MI_QMM_QMVM_MAX", 64);
-  mi::QmvmPlan qp{};
-  if (use_qmvm && x_dtype == MI_DTYPE_BFLOAT16 && M >= 2 && M <= qmvm_max &&
-      mi::qmvm_plan((int)M, (int)N, (int)K, gs, nb, 1, &qp)) {
-    mi::QmvmParams Q{x, w, (const uint16_t*)scales, (const uint16_t*)biases, (uint16_t*)y,
-                     nullptr, (int)M, (int)N, (int)K, gs, qp.kr, qp.wr};
-    if (qp.part_bytes) {
+  // 33..64 rows: by default as two launches (32 rows, then the rest) on disjoint output rows.
+  // Each re-reads the weights and still beats the 64-row instance's two passes over the
+  // staged rows (Llama-3-8B MLP, 4-bit M=64: 36.9 against 48.1 us per call; M=48: 30.6
+  // against 44.9).
+  static const int qmvm_split = env_int("MI_QMM_QMVM_SPLIT64", 1);
+  auto run_qmvm = [&](const void* xc, void* yc, int64_t Mc, const mi::QmvmPlan& pl) -> int {
+    mi::QmvmParams Q{xc, w, (const uint16_t*)scales, (const uint16_t*)biases, (uint16_t*)yc,
+                     nullptr, (int)Mc, (int)N, (int)K, gs, pl.kr, pl.wr};
+    if (pl.part_bytes) {
       void* data = nullptr;
-      rc = workspace(s, qp.part_bytes, &data);
-      if (rc) return rc;
+      int rc2 = workspace(s, pl.part_bytes, &data);
+      if (rc2) return rc2;
       Q.part = (float*)data;
     }
-    hipError_t e = mi::launch_qmvm(Q, qp, s);
+    hipError_t e = mi::launch_qmvm(Q, pl, s);
     return e == hipSuccess ? MI_OK : hip_fail(e, "qmvm launch");
+  };
+  mi::QmvmPlan qp{};
+  if (use_qmvm && qmvm_split && x_dtype == MI_DTYPE_BFLOAT16 && M > 32 && M <= qmvm_max) {
+    const int64_t m2 = M - 32;
+    mi::QmvmPlan q1{}, q2{};
+    // only when a 32-row launch fills the GPU by itself (on narrow shapes, e.g. the
+    // DeepSeek-V3 shared expert, it has 56..112 blocks and the split measured slower)
+    if (mi::qmvm_plan(32, (int)N, (int)K, gs, nb, 1, &q1) && q1.tiles * q1.ks >= 192 &&
+        mi::qmvm_plan((int)m2, (int)N, (int)K, gs, nb, 1, &q2)) {
+      if ((rc = run_qmvm(x, y, 32, q1)) != MI_OK) return rc;
+      return run_qmvm((const uint16_t*)x + 32 * K, (uint16_t*)y + 32 * N, m2, q2);
+    }
   }
+  if (use_qmvm && x_dtype == MI_DTYPE_BFLOAT16 && M >= 2 && M <= qmvm_max &&
+      mi::qmvm_plan((int)M, (int)N, (int)K, gs, nb, 1, &qp))
+    return run_qmvm(x, y, M, qp);
   if (x_dtype == MI_DTYPE_BFLOAT16 && M > 32 && mi::qmm_supported((int)M, (int)N, (int)K, nb, gs)) {
     mi::QmmParams Q{w, (const uint16_t*)scales, (const uint16_t*)biases, (const uint16_t*)x,
                     (uint16_t*)y, (int)M, (int)N, (int)K, nb, gs, nullptr, 1, 0, 0};

@@ -88,6 +88,26 @@ def test_config1_decode_sweep(dev, N, K, name, bits):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
+def test_config1_decode_33_to_64_rows(dev, N, K, bits):
+    """33..64 rows at the Llama-3-8B MLP shapes run as a 32-row launch plus one for the rest:
+    bit-equal to those two calls made separately, and sampled rows (both sides of the cut)
+    against the oracle."""
+    W = dev_weight(dev, N, K, bits, seed(2, 1, 9 + bits))
+    x = dev_x(dev, 64, K, seed(2, 0, 5 + bits))
+    for M in (33, 48, 64):
+        _case(t="cfg1_split", N=N, K=K, bits=bits, M=M)
+        y = mi_qmm.quantized_matmul(x[:M].contiguous(), *W, True, 64, bits)
+        a = mi_qmm.quantized_matmul(x[:32].contiguous(), *W, True, 64, bits)
+        b = mi_qmm.quantized_matmul(x[32:M].contiguous(), *W, True, 64, bits)
+        if M - 32 >= 2:  # one row takes the one-row kernel instead of a split
+            assert torch.equal(y.view(torch.int16), torch.cat([a, b]).view(torch.int16)), M
+        rows = [0, 31, 32, M - 1]
+        truth = O.qmm_f64(host_x(x[rows].contiguous()), *host(*W), 64, bits)
+        assert max_err_ratio(to_f64(y[rows]), truth) <= BF16_TOL, M
+
+
+@pytest.mark.parametrize("bits", [4, 8])
 def test_config1_fp32_activations_long_k(dev, bits):
     """fp32 activations at K = 14336 (the down projection), where the affine
     refactoring sum(x*(128+q)) - 128*s*sum(x) cancels the most: 1e-3 relative."""
