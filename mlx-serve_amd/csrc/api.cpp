@@ -804,15 +804,22 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
     return e == hipSuccess ? MI_OK : hip_fail(e, "qmvm launch");
   };
   mi::QmvmPlan qp{};
-  if (use_qmvm && qmvm_split && x_dtype == MI_DTYPE_BFLOAT16 && M > 32 && M <= qmvm_max) {
-    const int64_t m2 = M - 32;
+  static const int split_max = env_int("MI_QMM_QMVM_SPLIT_MAX", 64);
+  // (above 64 rows the chunks measured no better than qmm_kernel / prefill_kernel: 4-bit
+  // M=96 54.7 against 57.7 us, 8-bit M=96 69.3 against 65.4, M=128 73-91 against 57-69)
+  if (use_qmvm && qmvm_split && x_dtype == MI_DTYPE_BFLOAT16 && M > 32 && M <= split_max) {
+    const int64_t mlast = M - 32 * ((M - 1) / 32);  // rows of the last launch
     mi::QmvmPlan q1{}, q2{};
     // only when a 32-row launch fills the GPU by itself (on narrow shapes, e.g. the
     // DeepSeek-V3 shared expert, it has 56..112 blocks and the split measured slower)
     if (mi::qmvm_plan(32, (int)N, (int)K, gs, nb, 1, &q1) && q1.tiles * q1.ks >= 192 &&
-        mi::qmvm_plan((int)m2, (int)N, (int)K, gs, nb, 1, &q2)) {
-      if ((rc = run_qmvm(x, y, 32, q1)) != MI_OK) return rc;
-      return run_qmvm((const uint16_t*)x + 32 * K, (uint16_t*)y + 32 * N, m2, q2);
+        mi::qmvm_plan((int)mlast, (int)N, (int)K, gs, nb, 1, &q2)) {
+      for (int64_t m0 = 0; m0 < M; m0 += 32) {
+        const int64_t mc = std::min<int64_t>(32, M - m0);
+        rc = run_qmvm((const uint16_t*)x + m0 * K, (uint16_t*)y + m0 * N, mc, mc == 32 ? q1 : q2);
+        if (rc != MI_OK) return rc;
+      }
+      return MI_OK;
     }
   }
   if (use_qmvm && x_dtype == MI_DTYPE_BFLOAT16 && M >= 2 && M <= qmvm_max &&
