@@ -14,8 +14,8 @@
 // tile (8 KB) and one dword of scales and of biases per weight row.
 // Per 16-wide k-step a lane supplies 8 consecutive k of one weight row: word ks of the 16
 // packed bytes it owns (k in [32h, 32h+32) of the step, h = lane/32), dequantized as
-// bf16(s*q + b) with q's fp32 value 128+q built by v_perm (fma(s, 128+q, b - 128 s), one
-// rounding to bf16 by v_cvt_pk_bf16_f32, as MLX's GPU qmm rounds the weights it stages).
+// bf16(s*q + b): q from a scaled fp8 conversion, fma(s, q, b), one rounding to bf16 by
+// v_cvt_pk_bf16_f32, as MLX's GPU qmm rounds the weights it stages.
 // The x fragment of the same k-step is the natural 16-byte slot 4h+ks of the row.
 // One barrier per step, placed inside k-step 2 after the stage's last fragment reads: it
 // publishes the next stage (its DMA waited on with an exact vmcnt) and frees this one for
@@ -49,19 +49,22 @@ MI_DEV uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
-// 8 nibbles q0..q7 (k order) -> four bf16 pairs (q0,q1)..(q6,q7) of s*q + b. The byte of
-// each nibble is moved under the exponent bits 0x43 by v_perm, giving fp32 128 + q.
-MI_DEV u32x4_t dequant8(uint32_t w, float s, float bp) {
+// 8 nibbles q0..q7 (k order) -> four bf16 pairs (q0,q1)..(q6,q7) of s*q + b. The masks put
+// each nibble in a byte of its own; a byte 0..15 read as an e4m3 code is exactly q * 2^-9
+// (codes 0..7 are the subnormals q/8 * 2^-6, 8..15 the binade 1 + (q-8)/8 times 2^-6), so
+// v_cvt_scalef32_pk_f32_fp8 with the power-of-two scale 2^9 gives q itself, two per
+// instruction; then fma(s, q, b), one rounding to fp32, and one to bf16 (v_cvt_pk_bf16_f32).
+MI_DEV u32x4_t dequant8(uint32_t w, float s, float b) {
   const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-  constexpr uint32_t c43 = 0x43434343u;
-  auto v = [](uint32_t src, uint32_t byte) {
-    return __uint_as_float(perm_b32(c43, src, 0x04000C0Cu | (byte << 16)));
-  };
+  const f32x2_t l0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.0f, false);  // q0, q2
+  const f32x2_t l1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.0f, true);   // q4, q6
+  const f32x2_t h0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.0f, false);  // q1, q3
+  const f32x2_t h1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.0f, true);   // q5, q7
   u32x4_t o;
-  o.x = pack_bf16x2(fmaf(s, v(lo, 0), bp), fmaf(s, v(hi, 0), bp));
-  o.y = pack_bf16x2(fmaf(s, v(lo, 1), bp), fmaf(s, v(hi, 1), bp));
-  o.z = pack_bf16x2(fmaf(s, v(lo, 2), bp), fmaf(s, v(hi, 2), bp));
-  o.w = pack_bf16x2(fmaf(s, v(lo, 3), bp), fmaf(s, v(hi, 3), bp));
+  o.x = pack_bf16x2(fmaf(s, l0.x, b), fmaf(s, h0.x, b));
+  o.y = pack_bf16x2(fmaf(s, l0.y, b), fmaf(s, h0.y, b));
+  o.z = pack_bf16x2(fmaf(s, l1.x, b), fmaf(s, h1.x, b));
+  o.w = pack_bf16x2(fmaf(s, l1.y, b), fmaf(s, h1.y, b));
   return o;
 }
 
@@ -174,8 +177,7 @@ prefill_kernel(PrefillParams P) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       sc[j] = __uint_as_float(hi ? (w.s[j] & 0xFFFF0000u) : (w.s[j] << 16));
-      const float b = __uint_as_float(hi ? (w.b[j] & 0xFFFF0000u) : (w.b[j] << 16));
-      bp[j] = fmaf(-128.f, sc[j], b);
+      bp[j] = __uint_as_float(hi ? (w.b[j] & 0xFFFF0000u) : (w.b[j] << 16));
     }
   };
 
