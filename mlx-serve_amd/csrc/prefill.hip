@@ -21,6 +21,7 @@
 // publishes the next stage (its DMA waited on with an exact vmcnt) and frees this one for
 // the DMA of step s+3. Loads past the last step repeat it, so the control flow is uniform
 // and the compiler's wait counts stay exact.
+#include <algorithm>
 #include <cstdlib>
 
 #include "mi_common.h"
@@ -337,10 +338,27 @@ size_t prefill_plan(PrefillParams& P) {
   }();
   const int steps = P.K / kBK;
   const int64_t tiles = (int64_t)((P.M + kBM - 1) / kBM) * ((P.N + kBN - 1) / kBN);
-  // Split K when the tiles fill less than the GPU's 256 CUs, keeping >= 8 steps a split.
+  // K splits: the fewest estimated microseconds over rounds of 256 blocks (one per CU) x
+  // 64-wide steps a split (~2.15 us a step for a 256 x 256 tile), plus each split's fp32
+  // partials written and read back once (~5 TB/s); at least 8 steps a split. Measured at
+  // M=512: gate [14336,4096] 2 splits 27.5% of the bf16 peak (3 splits 20.5%), down
+  // [4096,14336] 8 splits 29.2%.
   int ks = 1;
-  if (forced_ks > 0) ks = forced_ks;
-  else if (tiles < 192) ks = (int)std::min<int64_t>((256 + tiles - 1) / tiles, steps / 8);
+  if (forced_ks > 0) {
+    ks = forced_ks;
+  } else {
+    double best = 1e30;
+    for (int k = 1; k <= std::max(1, steps / 8); ++k) {
+      const int64_t rounds = (tiles * k + 255) / 256;
+      const int sps = (steps + k - 1) / k;
+      const double part_us = k > 1 ? (double)k * P.M * P.N * 8 / 5e6 : 0.0;
+      const double cost = (double)rounds * sps * 2.15 + part_us;
+      if (cost < best - 1e-9) {
+        best = cost;
+        ks = k;
+      }
+    }
+  }
   ks = std::max(1, std::min(ks, steps));
   P.sps = (steps + ks - 1) / ks;
   P.ks = (steps + P.sps - 1) / P.sps;
