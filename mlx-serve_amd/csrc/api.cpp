@@ -822,8 +822,9 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
       return MI_OK;
     }
   }
-  if (use_qmvm && x_dtype == MI_DTYPE_BFLOAT16 && M >= 2 && M <= qmvm_max &&
-      mi::qmvm_plan((int)M, (int)N, (int)K, gs, nb, 1, &qp))
+  static const int q8_one = env_int("MI_QMM_Q8_QMVM1", 1);
+  if (use_qmvm && x_dtype == MI_DTYPE_BFLOAT16 && M >= (nb == 8 && q8_one ? 1 : 2) &&
+      M <= qmvm_max && mi::qmvm_plan((int)M, (int)N, (int)K, gs, nb, 1, &qp))
     return run_qmvm(x, y, M, qp);
   if (x_dtype == MI_DTYPE_BFLOAT16 && M > 32 && mi::qmm_supported((int)M, (int)N, (int)K, nb, gs)) {
     mi::QmmParams Q{w, (const uint16_t*)scales, (const uint16_t*)biases, (const uint16_t*)x,

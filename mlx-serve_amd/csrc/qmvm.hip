@@ -168,7 +168,7 @@ namespace {
 // 5, 6 bits on the 4-bit layout (bits = 4 here), staged like the affine 4-bit plans.
 bool plan_impl(int M, int N, int K, int gs, int bits, int64_t n_items, int fpm, QmvmPlan* out) {
   const bool fp = fpm >= 0 && fpm < 100, odd = fpm >= 100;
-  if ((bits != 4 && bits != 8) || M < (fp || odd ? 1 : 2) || M > (fp || odd ? 32 : 64))
+  if ((bits != 4 && bits != 8) || M < (fp || odd || bits == 8 ? 1 : 2) || M > (fp || odd ? 32 : 64))
     return false;
   if (odd && (int64_t)N * (K * (fpm - 100) / 8) >= ((int64_t)1 << 31)) return false;
   const int cv = 512 / bits;  // values per 64-byte chunk of a row
