@@ -194,7 +194,14 @@ bool plan_impl(int M, int N, int K, int gs, int bits, int64_t n_items, int fpm, 
   const int wr0 = env_wr ? env_wr : M <= 2 ? 1 : M <= 16 ? 4 : M <= 32 ? 8 : 4;
   QmvmPlan best{};
   double best_cost = 1e30;
-  for (int wr = wr0; wr >= 1 && !best.nc; wr >>= 1) {
+  // Up to 16 rows, a plan under 192 blocks (narrow shapes: N = 2048 or 7168 at K = 7168 or
+  // 2048) also weighs fewer tiles per block: more blocks outweigh the extra activation reads
+  // there (configs[4] shared expert, 8-bit M=8: 27.7 us at one tile against 36.4 at four).
+  auto few_blocks = [&]() {
+    return mt == 16 && !env_wr &&
+           (int64_t)best.tiles * best.ks * std::max<int64_t>(1, n_items) < 192;
+  };
+  for (int wr = wr0; wr >= 1 && (!best.nc || few_blocks()); wr >>= 1) {
     const int tiles = (N + 16 * wr - 1) / (16 * wr);
     for (int ks = 1; ks <= nch; ++ks) {
       if (nch % ks) continue;
