@@ -675,6 +675,39 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
     if (N > (int64_t)1 << 30 || M > (int64_t)1 << 30 || N * K * 2 > ((int64_t)1 << 34))
       return fail(MI_ERR_INVALID, "N, M or N*K too large");
     hipStream_t s = (hipStream_t)stream;
+    // one row of nvfp4 / mxfp4: the one-row streaming kernel's fp instances
+    static const int fp_qmv1 = env_int("MI_QMM_FP_QMV1", 1);
+    if (fp_qmv1 && M == 1 && fm <= 1 && mi::qmv1_supported((int)N, (int)K, 64, 4, 0)) {
+      const mi::Qmv1Plan pl = mi::qmv1_plan((int)N, (int)K, 64, 1);
+      mi::QmvParams P{};
+      P.w = w;
+      P.scales = (const uint16_t*)scales;
+      P.x = x;
+      P.y = y;
+      P.n_pairs = 1;
+      P.lhs_div = 1;
+      P.x_batch = 1;
+      P.n_experts = 1;
+      P.M = 1;
+      P.N = (int)N;
+      P.K = (int)K;
+      P.bits = 4;
+      P.group_size = 64;
+      P.rpi = 1;
+      P.items_per_pair = 1;
+      P.n_items_fixed = 1;
+      P.ks = pl.ks;
+      P.gps = pl.gps;
+      P.row_blocks = pl.tiles;
+      if (pl.ks > 1) {
+        void* data = nullptr;
+        rc = workspace(s, (size_t)pl.ks * N * 4, &data);
+        if (rc) return rc;
+        P.part = (float*)data;
+      }
+      hipError_t e = mi::launch_qmv1_fp(P, pl, fm, s);
+      return e == hipSuccess ? MI_OK : hip_fail(e, "qmv1 fp launch");
+    }
     // 1..32 rows: the few-row MFMA kernel (code x scale exact in bf16)
     static const int fp_mfma = env_int("MI_QMM_FP_MFMA", 1);
     static const int fp_mfma_min = env_int("MI_QMM_FP_MFMA_MIN", 1);

@@ -1,0 +1,49 @@
+// Decoders of the bias-less 4-bit modes to exact bf16 pairs, shared by the one-row and
+// few-row decode kernels: nvfp4 (e2m1 codes, 16-value groups, e4m3 scales) and mxfp4
+// (e2m1 codes, 32-value groups, e8m0 scales). A code times its group scale is exact in bf16
+// (at most 2 x 4 significant bits).
+#pragma once
+#include "mi_common.h"
+
+namespace mi {
+namespace fp_codes {
+
+// e4m3 (nvfp4 scales) with the reference's reading of every code as finite, as fp32.
+MI_DEV float fp_e4m3(uint32_t b) {
+  const uint32_t m = b & 0x7Fu, e = m >> 3, f = m & 7u;
+  const float mag = e ? __uint_as_float(((e + 120u) << 23) | (f << 20)) : (float)f * 0.001953125f;
+  return (b & 0x80u) ? -mag : mag;
+}
+
+// 8 e2m1 codes (one per nibble, low nibble first) times one power-of-two scale -> 4 bf16
+// pairs. v_cvt_scalef32_pk_bf16_fp4 reads only the exponent field of its fp32 scale, as an
+// e8m0 byte (0 -> 2^-127), which is exactly mxfp4's scale: pass the byte as the exponent.
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+MI_DEV u32x4_t fp4_run(uint32_t codes, float sc) {
+  return u32x4_t{
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, sc, 0)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, sc, 1)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, sc, 2)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, sc, 3))};
+}
+// nvfp4: e4m3 scales are not powers of two. The code converts to fp32 with the scale's
+// power of two, is multiplied by the scale's signed mantissa factor (exact: at most 2 x 4
+// significant bits) and rounds to bf16 without loss.
+MI_DEV u32x4_t fp4_run_e4m3(uint32_t codes, float sc) {
+  const uint32_t sb = __float_as_uint(sc);
+  const float p = __uint_as_float(sb & 0x7F800000u);
+  const float m = sc == 0.f ? 0.f : __uint_as_float((sb & 0x807FFFFFu) | 0x3F800000u);
+  auto pair = [&](f32x2v v) {
+    const f32x2v w = {v.x * m, v.y * m};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(w, bf16x2v));
+  };
+  return u32x4_t{pair(__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, p, 0)),
+                 pair(__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, p, 1)),
+                 pair(__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, p, 2)),
+                 pair(__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, p, 3))};
+}
+
+
+}  // namespace fp_codes
+}  // namespace mi

@@ -20,6 +20,7 @@
 #include "mi_internal.h"
 #include "qmv_common.h"
 #include "moe_route.h"
+#include "fp_codes.h"
 
 #include <type_traits>
 
@@ -88,8 +89,15 @@ constexpr int groups_per_chunk() {
 }
 
 // Up to 16 waves per block when a wave holds <= 8 chunks (<= 128 VGPRs), else 8.
-template <int GS, int NC, int XU, int DEPTH, bool DENSE, bool DUAL = false>
+// FPM 0 / 1 (dense only): bias-less nvfp4 / mxfp4 weights in the same chunk layout, P.scales
+// then uint8 [N, K / FGS] (e4m3 for nvfp4's 16-value groups, e8m0 for mxfp4's 32). Each 8-code
+// word becomes exact bf16 pairs of code x scale (the few-row kernel's decoders), dotted with
+// the activations in natural order; no affine terms, so no per-slice sums.
+template <int GS, int NC, int XU, int DEPTH, bool DENSE, bool DUAL = false, int FPM = -1>
 __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P) {
+  constexpr bool FP = FPM >= 0;
+  static_assert(!FP || (DENSE && !DUAL && (FPM == 0 || FPM == 1)), "fp4 modes: dense calls");
+  constexpr int FGS = FPM == 0 ? 16 : 32;
   constexpr int GPC = groups_per_chunk<GS>();
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, BD = blockDim.x, W = BD >> 6;
@@ -128,6 +136,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     __amdgpu_buffer_rsrc_t wres;
     uint32_t wo;
     uint32_t sd[GPC >= 2 ? NSL : NC], bd[GPC >= 2 ? NSL : NC];
+    u32x2_t fs[FP ? NC : 1];  // fp modes: the row's scale bytes of each chunk
     u32x4_t wv[NC];
   };
   // 1. every global load of this item, before anything waits, as buffer loads from
@@ -160,7 +169,22 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     // of the row's quad loads dwords g, g+4, ... and chunks take theirs by a quad
     // broadcast. gs 128: one bf16 per chunk.
     const uint32_t so = nn * (uint32_t)(G * 2) + (uint32_t)((kb0 + c0 * kChunkVals) / GS) * 2;
-    if constexpr (GPC >= 2) {
+    if constexpr (FP) {
+      // the chunk's 8 (nvfp4) or 4 (mxfp4) scale bytes of the row; the row's 4 lanes read
+      // the same bytes and each takes its own slice's
+      const int Gf = K / FGS;
+      const __amdgpu_buffer_rsrc_t fres = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)((const unsigned char*)Ps + mat * (uint32_t)Gf), (short)0, N * Gf, kBufFlags);
+      const uint32_t fo = nn * (uint32_t)Gf + (uint32_t)(kb0 + c0 * kChunkVals) / FGS;
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        if constexpr (FPM == 0)
+          L.fs[j] = __builtin_bit_cast(
+              u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(fres, fo + 8 * j, 0, 0));
+        else
+          L.fs[j].x = __builtin_amdgcn_raw_buffer_load_b32(fres, fo + 4 * j, 0, 0);
+      }
+    } else if constexpr (GPC >= 2) {
 #pragma unroll
       for (int i = 0; i < NSL; ++i) {
         L.sd[i] = __builtin_amdgcn_raw_buffer_load_b32(sres, so + 4 * g + 16 * i, 0, 0);
@@ -192,13 +216,17 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
       s8 += quad_xor1(s8);
       s8 += quad_xor2(s8);
       if (u < nunits) {
-        u32x4_t o;
-        o.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
-        o.y = perm_b32(X.w, X.z, 0x05040100u);  // (x4, x6)
-        o.z = perm_b32(X.y, X.x, 0x07060302u);  // (x1, x3)
-        o.w = perm_b32(X.w, X.z, 0x07060302u);  // (x5, x7)
-        *reinterpret_cast<u32x4_t*>(xs + u * 4) = o;
-        if ((u & 3) == 0) xsum[u >> 2] = s8;
+        if constexpr (FP) {  // natural order: the fp decoders emit (q0, q1), (q2, q3), ..
+          *reinterpret_cast<u32x4_t*>(xs + u * 4) = X;
+        } else {
+          u32x4_t o;
+          o.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
+          o.y = perm_b32(X.w, X.z, 0x05040100u);  // (x4, x6)
+          o.z = perm_b32(X.y, X.x, 0x07060302u);  // (x1, x3)
+          o.w = perm_b32(X.w, X.z, 0x07060302u);  // (x5, x7)
+          *reinterpret_cast<u32x4_t*>(xs + u * 4) = o;
+          if ((u & 3) == 0) xsum[u >> 2] = s8;
+        }
       }
     }
     // LDS-only barrier: the weight loads stay in flight.
@@ -219,6 +247,35 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
       const int jj = min(j, nload - 1);
       const int off = (c0 + jj) * kChunkVals + 32 * g;  // within the block range
       const u32x4_t* xp = reinterpret_cast<const u32x4_t*>(xs + off / 2);
+      if constexpr (FP) {
+        // lane slice g of chunk j: codes 32g .. 32g + 31, word t = codes 32g + 8t ..
+        float acc = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t codes = t == 0 ? L.wv[j].x : t == 1 ? L.wv[j].y : t == 2 ? L.wv[j].z
+                                                                              : L.wv[j].w;
+          u32x4_t a;
+          if constexpr (FPM == 1) {  // one e8m0 byte per 32 codes: byte g
+            a = fp_codes::fp4_run(codes, __uint_as_float(((L.fs[j].x >> (8 * g)) & 0xFFu) << 23));
+          } else {  // one e4m3 byte per 16 codes: byte 2g + t/2 of the chunk's 8
+            const int b = 2 * g + (t >> 1);
+            const uint32_t wd = b < 4 ? L.fs[j].x : L.fs[j].y;
+            a = fp_codes::fp4_run_e4m3(codes, fp_codes::fp_e4m3((wd >> (8 * (b & 3))) & 0xFFu));
+          }
+          const u32x4_t xv4 = xp[t];
+          acc = dot2(a.x, xv4.x, acc);
+          acc = dot2(a.y, xv4.y, acc);
+          acc = dot2(a.z, xv4.z, acc);
+          acc = dot2(a.w, xv4.w, acc);
+          // one word's pairs live at a time (the compiler otherwise decodes ahead and
+          // spills)
+          asm volatile("" : "+v"(acc));
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        y = fmaf(j < nmine ? 1.f : 0.f, acc, y);
+        if constexpr (D < NC) __builtin_amdgcn_sched_barrier(0);
+        continue;
+      }
       float acc = 0.f;
       acc = dot8(L.wv[j].x, xp[0], acc);
       acc = dot8(L.wv[j].y, xp[1], acc);

@@ -372,11 +372,29 @@ def test_qmm_fp4_mfma(dev, mode, M, N, K):
 
 
 @pytest.mark.parametrize("mode", ["nvfp4", "mxfp4"])
-def test_qmm_fp4_mfma_scale_edges(dev, mode):
+@pytest.mark.parametrize("M,N,K", [(1, 320, 14336), (1, 64, 2176), (1, 4096, 1024),
+                                   (1, 100, 4096)])
+def test_qmm_fp4_one_row(dev, mode, M, N, K):
+    """One row of nvfp4 / mxfp4 on the one-row streaming kernel's fp instances (K = 2176:
+    17 chunks, a K-split plan and the fixed-order reduce)."""
+    _print_case(t="qmm_fp4_one_row", mode=mode, N=N, K=K)
+    wq, sc = _fp_weight(mode, N, K, 90 + N)
+    x = O.make_x_bf16(M, K, 91 + K)
+    y = mi_qmm.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(wq, dev),
+                                torch.from_numpy(sc).to(dev), None, True, mode=mode)
+    truth = O.bf16_to_f32(x).astype(np.float64) @ O.dequantize_fp(wq, sc, mode).astype(np.float64).T
+    assert y.shape == (M, N)
+    assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+
+
+@pytest.mark.parametrize("mode", ["nvfp4", "mxfp4"])
+@pytest.mark.parametrize("M", [1, 8])
+def test_qmm_fp4_mfma_scale_edges(dev, mode, M):
     """Scale bytes at the ends of their formats: e4m3 0x7F (480 in the reference's
-    reading) and 0x01 (2^-9), e8m0 1 and 254 groups mixed with ordinary ones."""
-    _print_case(t="qmm_fp4_edges", mode=mode)
-    N, K, M = 64, 512, 8
+    reading) and 0x01 (2^-9), e8m0 1 and 254 groups mixed with ordinary ones (one row:
+    the one-row kernel; eight: the few-row MFMA kernel)."""
+    _print_case(t="qmm_fp4_edges", mode=mode, M=M)
+    N, K = 64, 512
     wq, sc = _fp_weight(mode, N, K, 77)
     if mode == "nvfp4":
         sc[0, :] = 0x7F
