@@ -91,8 +91,9 @@ constexpr int groups_per_chunk() {
 // Up to 16 waves per block when a wave holds <= 8 chunks (<= 128 VGPRs), else 8.
 // FPM 0 / 1 (dense only): bias-less nvfp4 / mxfp4 weights in the same chunk layout, P.scales
 // then uint8 [N, K / FGS] (e4m3 for nvfp4's 16-value groups, e8m0 for mxfp4's 32). Each 8-code
-// word becomes exact bf16 pairs of code x scale (the few-row kernel's decoders), dotted with
-// the activations in natural order; no affine terms, so no per-slice sums.
+// word becomes exact bf16 pairs (mxfp4: code x scale; nvfp4: the code, its group's scale
+// applied to the group's fp32 dot sum), dotted with the activations in natural order; no
+// affine terms, so no per-slice sums.
 template <int GS, int NC, int XU, int DEPTH, bool DENSE, bool DUAL = false, int FPM = -1>
 __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P) {
   constexpr bool FP = FPM >= 0;
@@ -249,27 +250,33 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
       const u32x4_t* xp = reinterpret_cast<const u32x4_t*>(xs + off / 2);
       if constexpr (FP) {
         // lane slice g of chunk j: codes 32g .. 32g + 31, word t = codes 32g + 8t ..
-        float acc = 0.f;
+        // mxfp4: one e8m0 scale (byte g) for the slice, applied exactly in the conversion.
+        // nvfp4: two e4m3 scales (bytes 2g, 2g+1), one per 16 codes: the codes convert
+        // exactly (scale 1), each group's dot sum is scaled in fp32, the groups in order.
+        float acc = 0.f, grp = 0.f;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const uint32_t codes = t == 0 ? L.wv[j].x : t == 1 ? L.wv[j].y : t == 2 ? L.wv[j].z
                                                                               : L.wv[j].w;
-          u32x4_t a;
-          if constexpr (FPM == 1) {  // one e8m0 byte per 32 codes: byte g
-            a = fp_codes::fp4_run(codes, __uint_as_float(((L.fs[j].x >> (8 * g)) & 0xFFu) << 23));
-          } else {  // one e4m3 byte per 16 codes: byte 2g + t/2 of the chunk's 8
-            const int b = 2 * g + (t >> 1);
-            const uint32_t wd = b < 4 ? L.fs[j].x : L.fs[j].y;
-            a = fp_codes::fp4_run_e4m3(codes, fp_codes::fp_e4m3((wd >> (8 * (b & 3))) & 0xFFu));
-          }
+          const u32x4_t a = fp_codes::fp4_run(
+              codes, FPM == 1 ? __uint_as_float(((L.fs[j].x >> (8 * g)) & 0xFFu) << 23) : 1.f);
           const u32x4_t xv4 = xp[t];
-          acc = dot2(a.x, xv4.x, acc);
-          acc = dot2(a.y, xv4.y, acc);
-          acc = dot2(a.z, xv4.z, acc);
-          acc = dot2(a.w, xv4.w, acc);
+          float& d = FPM == 1 ? acc : grp;
+          d = dot2(a.x, xv4.x, d);
+          d = dot2(a.y, xv4.y, d);
+          d = dot2(a.z, xv4.z, d);
+          d = dot2(a.w, xv4.w, d);
+          if constexpr (FPM == 0) {
+            if (t & 1) {  // a 16-code group is complete
+              const int b = 2 * g + (t >> 1);
+              const uint32_t wd = b < 4 ? L.fs[j].x : L.fs[j].y;
+              acc = fmaf(fp_codes::fp_e4m3((wd >> (8 * (b & 3))) & 0xFFu), grp, acc);
+              grp = 0.f;
+            }
+          }
           // one word's pairs live at a time (the compiler otherwise decodes ahead and
           // spills)
-          asm volatile("" : "+v"(acc));
+          asm volatile("" : "+v"(acc), "+v"(grp));
           __builtin_amdgcn_sched_barrier(0);
         }
         y = fmaf(j < nmine ? 1.f : 0.f, acc, y);
