@@ -779,6 +779,41 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   const bool odd_width = nb != 4 && nb != 8;
   if (odd_width && (x_dtype != MI_DTYPE_BFLOAT16 || N * K * 2 > ((int64_t)1 << 34)))
     return fail(MI_ERR_UNSUPPORTED, "bits=%d: bf16 activations only", nb);
+  // one row at gs 64: the one-row streaming kernel's odd-width instances
+  static const int odd_qmv1 = env_int("MI_QMM_ODD_QMV1", 1);
+  if (odd_width && odd_qmv1 && M == 1 && gs == 64 && x_dtype == MI_DTYPE_BFLOAT16 &&
+      K % 128 == 0 && N * (K / 8 * nb) < ((int64_t)1 << 31)) {
+    const mi::Qmv1Plan pl = mi::qmv1_plan((int)N, (int)K, 64, 1);
+    mi::QmvParams P{};
+    P.w = w;
+    P.scales = (const uint16_t*)scales;
+    P.biases = (const uint16_t*)biases;
+    P.x = x;
+    P.y = y;
+    P.n_pairs = 1;
+    P.lhs_div = 1;
+    P.x_batch = 1;
+    P.n_experts = 1;
+    P.M = 1;
+    P.N = (int)N;
+    P.K = (int)K;
+    P.bits = nb;
+    P.group_size = 64;
+    P.rpi = 1;
+    P.items_per_pair = 1;
+    P.n_items_fixed = 1;
+    P.ks = pl.ks;
+    P.gps = pl.gps;
+    P.row_blocks = pl.tiles;
+    if (pl.ks > 1) {
+      void* data = nullptr;
+      rc = workspace(s, (size_t)pl.ks * N * 4, &data);
+      if (rc) return rc;
+      P.part = (float*)data;
+    }
+    hipError_t e = mi::launch_qmv1_fp(P, pl, 100 + nb, s);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "qmv1 odd-width launch");
+  }
   static const int odd_mfma = env_int("MI_QMM_ODD_MFMA", 1);
   mi::QmvmPlan op{};
   // 2..32 rows, gs 64 (and one row at 2 bits, where the per-code kernel is VALU-bound)

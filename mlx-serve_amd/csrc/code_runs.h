@@ -1,12 +1,12 @@
-// Decoders of the bias-less 4-bit modes to exact bf16 pairs, shared by the one-row and
-// few-row decode kernels: nvfp4 (e2m1 codes, 16-value groups, e4m3 scales) and mxfp4
-// (e2m1 codes, 32-value groups, e8m0 scales). A code times its group scale is exact in bf16
-// (at most 2 x 4 significant bits).
+// Decoders of 8-code runs to exact bf16 pairs, shared by the one-row and few-row decode
+// kernels: the bias-less 4-bit modes nvfp4 (e2m1 codes, 16-value groups, e4m3 scales) and
+// mxfp4 (e2m1 codes, 32-value groups, e8m0 scales), where a code times its group scale is
+// exact in bf16 (at most 2 x 4 significant bits); and affine 2/3/5/6-bit codes as 128 + q.
 #pragma once
 #include "mi_common.h"
 
 namespace mi {
-namespace fp_codes {
+namespace code_runs {
 
 // e4m3 (nvfp4 scales) with the reference's reading of every code as finite, as fp32.
 MI_DEV float fp_e4m3(uint32_t b) {
@@ -44,6 +44,19 @@ MI_DEV u32x4_t fp4_run_e4m3(uint32_t codes, float sc) {
                  pair(__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, p, 3))};
 }
 
+// 8 codes of `OB` bits (LSB-first, starting `sh` bits into the 64-bit pair d1:d0) ->
+// bf16 pairs (128 + q0, 128 + q1) .. (128 + q6, 128 + q7).
+template <int OB>
+MI_DEV u32x4_t odd_run(uint32_t d0, uint32_t d1, uint32_t sh) {
+  const uint64_t v = ((((uint64_t)d1) << 32) | d0) >> sh;
+  constexpr uint32_t mask = (1u << OB) - 1u;
+  auto pr = [&](int p) {
+    const uint32_t c0 = (uint32_t)(v >> (2 * p * OB)) & mask;
+    const uint32_t c1 = (uint32_t)(v >> ((2 * p + 1) * OB)) & mask;
+    return (c0 | (c1 << 16)) | 0x43004300u;
+  };
+  return u32x4_t{pr(0), pr(1), pr(2), pr(3)};
+}
 
-}  // namespace fp_codes
+}  // namespace code_runs
 }  // namespace mi

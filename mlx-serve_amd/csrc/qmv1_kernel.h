@@ -20,7 +20,7 @@
 #include "mi_internal.h"
 #include "qmv_common.h"
 #include "moe_route.h"
-#include "fp_codes.h"
+#include "code_runs.h"
 
 #include <type_traits>
 
@@ -96,8 +96,14 @@ constexpr int groups_per_chunk() {
 // affine terms, so no per-slice sums.
 template <int GS, int NC, int XU, int DEPTH, bool DENSE, bool DUAL = false, int FPM = -1>
 __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P) {
-  constexpr bool FP = FPM >= 0;
+  constexpr bool FP = FPM >= 0 && FPM < 100;
+  // FPM 100 + b: affine b = 2, 3, 5, 6 bits, one LSB-first bitstream per row; a lane's 32
+  // codes of a chunk are 4b bytes at byte 4bg of the chunk's 16b (dword-aligned)
+  constexpr bool ODD = FPM >= 100;
+  constexpr int OB = ODD ? FPM - 100 : 4;
   static_assert(!FP || (DENSE && !DUAL && (FPM == 0 || FPM == 1)), "fp4 modes: dense calls");
+  static_assert(!ODD || (DENSE && !DUAL && GS == 64 && (OB == 2 || OB == 3 || OB == 5 || OB == 6)),
+                "odd widths: dense calls at group size 64");
   constexpr int FGS = FPM == 0 ? 16 : 32;
   constexpr int GPC = groups_per_chunk<GS>();
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -139,6 +145,30 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     uint32_t sd[GPC >= 2 ? NSL : NC], bd[GPC >= 2 ? NSL : NC];
     u32x2_t fs[FP ? NC : 1];  // fp modes: the row's scale bytes of each chunk
     u32x4_t wv[NC];
+    u32x2_t wv2[ODD ? NC : 1];  // odd widths: dwords 4, 5 of a lane's 5- or 6-dword slice
+  };
+  // One chunk's weights of this lane: 16 B at 4 bits, OB dwords at the odd widths.
+  auto load_chunk = [&](BankLoads& L, int j) __attribute__((always_inline)) {
+    if constexpr (ODD) {
+      const uint32_t o = L.wo + 16 * OB * j;
+      if constexpr (OB == 2) {
+        const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(L.wres, o, 0, 0));
+        L.wv[j] = u32x4_t{v.x, v.y, 0u, 0u};
+      } else if constexpr (OB == 3) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b96(L.wres, o, 0, 0);
+        L.wv[j] = u32x4_t{v[0], v[1], v[2], 0u};
+      } else {
+        L.wv[j] = __builtin_amdgcn_raw_buffer_load_b128(L.wres, o, 0, 0);
+        if constexpr (OB == 5) {
+          L.wv2[j] = u32x2_t{__builtin_amdgcn_raw_buffer_load_b32(L.wres, o + 16, 0, 0), 0u};
+        } else {
+          L.wv2[j] = __builtin_bit_cast(u32x2_t,
+                                        __builtin_amdgcn_raw_buffer_load_b64(L.wres, o + 16, 0, 0));
+        }
+      }
+    } else {
+      L.wv[j] = __builtin_amdgcn_raw_buffer_load_b128(L.wres, L.wo + 64 * j, 0, 0);
+    }
   };
   // 1. every global load of this item, before anything waits, as buffer loads from
   //    per-matrix resources: 32-bit lane offsets, chunk / slot strides folded into the
@@ -159,13 +189,17 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     const uint16_t* Pb = BANK ? P.biases2 : P.biases;
     const uint32_t e = __builtin_amdgcn_readfirstlane(it.expert_ok ? it.expert : 0u);
     const size_t mat = (size_t)e * (uint32_t)N;
-    L.wres = __builtin_amdgcn_make_buffer_rsrc((void*)(Pw + mat * (uint32_t)(K / 8)), (short)0,
-                                               N * (K / 2), kBufFlags);
+    L.wres = ODD ? __builtin_amdgcn_make_buffer_rsrc(
+                       (void*)((const unsigned char*)Pw + mat * (uint32_t)(K / 8 * OB)), (short)0,
+                       N * (K / 8 * OB), kBufFlags)
+                 : __builtin_amdgcn_make_buffer_rsrc((void*)(Pw + mat * (uint32_t)(K / 8)), (short)0,
+                                                     N * (K / 2), kBufFlags);
     const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(Ps + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
     const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(Pb + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
-    L.wo = nn * (uint32_t)(K / 2) + (uint32_t)(kb0 + c0 * kChunkVals) / 2 + 16 * g;
+    L.wo = ODD ? nn * (uint32_t)(K / 8 * OB) + (uint32_t)(kb0 + c0 * kChunkVals) / 8 * OB + 4 * OB * g
+               : nn * (uint32_t)(K / 2) + (uint32_t)(kb0 + c0 * kChunkVals) / 2 + 16 * g;
     // Scales/biases. gs 64/32: the wave's groups of a row are contiguous dwords; lane g
     // of the row's quad loads dwords g, g+4, ... and chunks take theirs by a quad
     // broadcast. gs 128: one bf16 per chunk.
@@ -201,8 +235,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     // Weights: the first D chunks now, then one more as each chunk is consumed, so a
     // wave's data arrives in the order it is used.
 #pragma unroll
-    for (int j = 0; j < D; ++j)
-      L.wv[j] = __builtin_amdgcn_raw_buffer_load_b128(L.wres, L.wo + 64 * j, 0, 0);
+    for (int j = 0; j < D; ++j) load_chunk(L, j);
   };
   // 2. stage the activations in dot8's pair order, with per-32-value sums.
   auto stage_x = [&](const u32x4_t (&xv)[XU]) {
@@ -217,8 +250,9 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
       s8 += quad_xor1(s8);
       s8 += quad_xor2(s8);
       if (u < nunits) {
-        if constexpr (FP) {  // natural order: the fp decoders emit (q0, q1), (q2, q3), ..
+        if constexpr (FP || ODD) {  // natural order: these decoders emit (q0, q1), (q2, q3), ..
           *reinterpret_cast<u32x4_t*>(xs + u * 4) = X;
+          if (ODD && (u & 3) == 0) xsum[u >> 2] = s8;
         } else {
           u32x4_t o;
           o.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
@@ -242,8 +276,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
       if constexpr (D < NC) {
-        if (j + D < NC)
-          L.wv[j + D] = __builtin_amdgcn_raw_buffer_load_b128(L.wres, L.wo + 64 * (j + D), 0, 0);
+        if (j + D < NC) load_chunk(L, j + D);
       }
       const int jj = min(j, nload - 1);
       const int off = (c0 + jj) * kChunkVals + 32 * g;  // within the block range
@@ -258,7 +291,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
         for (int t = 0; t < 4; ++t) {
           const uint32_t codes = t == 0 ? L.wv[j].x : t == 1 ? L.wv[j].y : t == 2 ? L.wv[j].z
                                                                               : L.wv[j].w;
-          const u32x4_t a = fp_codes::fp4_run(
+          const u32x4_t a = code_runs::fp4_run(
               codes, FPM == 1 ? __uint_as_float(((L.fs[j].x >> (8 * g)) & 0xFFu) << 23) : 1.f);
           const u32x4_t xv4 = xp[t];
           float& d = FPM == 1 ? acc : grp;
@@ -270,7 +303,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
             if (t & 1) {  // a 16-code group is complete
               const int b = 2 * g + (t >> 1);
               const uint32_t wd = b < 4 ? L.fs[j].x : L.fs[j].y;
-              acc = fmaf(fp_codes::fp_e4m3((wd >> (8 * (b & 3))) & 0xFFu), grp, acc);
+              acc = fmaf(code_runs::fp_e4m3((wd >> (8 * (b & 3))) & 0xFFu), grp, acc);
               grp = 0.f;
             }
           }
@@ -284,10 +317,28 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
         continue;
       }
       float acc = 0.f;
-      acc = dot8(L.wv[j].x, xp[0], acc);
-      acc = dot8(L.wv[j].y, xp[1], acc);
-      acc = dot8(L.wv[j].z, xp[2], acc);
-      acc = dot8(L.wv[j].w, xp[3], acc);
+      if constexpr (ODD) {
+        // run t (codes 8t .. 8t+7 of the slice) starts at byte t*OB of the lane's dwords
+        auto dw = [&](int i) -> uint32_t {
+          return i == 0 ? L.wv[j].x : i == 1 ? L.wv[j].y : i == 2 ? L.wv[j].z : i == 3 ? L.wv[j].w
+                 : i == 4 ? L.wv2[j].x : i == 5 ? L.wv2[j].y : 0u;
+        };
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int i = (t * OB) >> 2, sh = 8 * ((t * OB) & 3);
+          const u32x4_t a = code_runs::odd_run<OB>(dw(i), i + 1 < OB ? dw(i + 1) : 0u, sh);
+          const u32x4_t xv4 = xp[t];
+          acc = dot2(a.x, xv4.x, acc);
+          acc = dot2(a.y, xv4.y, acc);
+          acc = dot2(a.z, xv4.z, acc);
+          acc = dot2(a.w, xv4.w, acc);
+        }
+      } else {
+        acc = dot8(L.wv[j].x, xp[0], acc);
+        acc = dot8(L.wv[j].y, xp[1], acc);
+        acc = dot8(L.wv[j].z, xp[2], acc);
+        acc = dot8(L.wv[j].w, xp[3], acc);
+      }
       const float use = j < nmine ? 1.f : 0.f;
       float s, b;
       if constexpr (GPC == 2) {
@@ -438,6 +489,44 @@ hipError_t launch_nc(const QmvParams& P, dim3 grid, int waves, int xu, int depth
   if (dense) launch_depth<GS, NC, true>(P, grid, block, xu, depth, lds, s);
   else launch_depth<GS, NC, false>(P, grid, block, xu, depth, lds, s);
   return hipGetLastError();
+}
+
+// Dense one-row launches of the other weight formats (fp4 modes, odd widths): the
+// instances for one format, dispatched on the plan's chunks per wave, loads and depth.
+template <int NC, int DEPTH, int FPM>
+void launch_xu_fmt(const QmvParams& P, dim3 grid, dim3 block, int xu, size_t lds, hipStream_t s) {
+  switch (xu) {
+    case 1: hipLaunchKernelGGL((qmv1_kernel<64, NC, 1, DEPTH, true, false, FPM>), grid, block, lds, s, P); break;
+    case 2: hipLaunchKernelGGL((qmv1_kernel<64, NC, 2, DEPTH, true, false, FPM>), grid, block, lds, s, P); break;
+    case 4: hipLaunchKernelGGL((qmv1_kernel<64, NC, 4, DEPTH, true, false, FPM>), grid, block, lds, s, P); break;
+    default: hipLaunchKernelGGL((qmv1_kernel<64, NC, 8, DEPTH, true, false, FPM>), grid, block, lds, s, P); break;
+  }
+}
+
+template <int NC, int FPM>
+void launch_nc_fmt(const QmvParams& P, dim3 grid, dim3 block, int xu, int depth, size_t lds,
+                  hipStream_t s) {
+  if (NC > 2 && depth == 2) launch_xu_fmt<NC, 2, FPM>(P, grid, block, xu, lds, s);
+  else launch_xu_fmt<NC, 4, FPM>(P, grid, block, xu, lds, s);
+}
+
+template <int FPM>
+void launch_fmt(const QmvParams& P, const Qmv1Plan& pl, hipStream_t s) {
+  const dim3 grid((unsigned)pl.tiles, (unsigned)P.ks, 1), block(64 * pl.waves);
+  switch (pl.nc) {
+    case 1: launch_nc_fmt<1, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
+    case 2: launch_nc_fmt<2, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
+    case 3: launch_nc_fmt<3, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
+    case 4: launch_nc_fmt<4, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
+    case 5: launch_nc_fmt<5, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
+    case 6: launch_nc_fmt<6, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
+    case 7: launch_nc_fmt<7, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
+    case 8: launch_nc_fmt<8, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
+    case 10: launch_nc_fmt<10, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
+    case 12: launch_nc_fmt<12, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
+    case 14: launch_nc_fmt<14, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
+    default: launch_nc_fmt<16, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
+  }
 }
 
 }  // namespace qmv1_detail

@@ -46,7 +46,7 @@
 // range order. Every sum has a fixed order: results are deterministic.
 #pragma once
 #include "qmv_common.h"
-#include "fp_codes.h"
+#include "code_runs.h"
 
 #include <cstdint>
 #include <type_traits>
@@ -59,11 +59,12 @@ using qmv_detail::item_x_row;
 using qmv_detail::Item;
 using qmv_detail::lds_barrier;
 
-using fp_codes::bf16x2v;
-using fp_codes::f32x2v;
-using fp_codes::fp4_run;
-using fp_codes::fp4_run_e4m3;
-using fp_codes::fp_e4m3;
+using code_runs::bf16x2v;
+using code_runs::f32x2v;
+using code_runs::fp4_run;
+using code_runs::fp4_run_e4m3;
+using code_runs::fp_e4m3;
+using code_runs::odd_run;
 
 typedef __bf16 bf16x8m __attribute__((ext_vector_type(8)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -163,20 +164,6 @@ MI_DEV u32x4_t fp8_run(uint32_t w0, uint32_t w1, float sc) {
       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, true)),
       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, false)),
       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, true))};
-}
-
-// 8 codes of `OB` bits (LSB-first, starting `sh` bits into the 64-bit pair d1:d0) ->
-// bf16 pairs (128 + q0, 128 + q1) .. (128 + q6, 128 + q7).
-template <int OB>
-MI_DEV u32x4_t odd_run(uint32_t d0, uint32_t d1, uint32_t sh) {
-  const uint64_t v = ((((uint64_t)d1) << 32) | d0) >> sh;
-  constexpr uint32_t mask = (1u << OB) - 1u;
-  auto pr = [&](int p) {
-    const uint32_t c0 = (uint32_t)(v >> (2 * p * OB)) & mask;
-    const uint32_t c1 = (uint32_t)(v >> ((2 * p + 1) * OB)) & mask;
-    return (c0 | (c1 << 16)) | 0x43004300u;
-  };
-  return u32x4_t{pr(0), pr(1), pr(2), pr(3)};
 }
 
 template <int BITS, int GS, int NC, int XU, int DEPTH, int MT, bool SBF32, bool GATHER, int FPM = -1>

@@ -92,6 +92,20 @@ def test_qmm_other_widths(dev, M, N, K, bits, gs):
     assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
 
 
+@pytest.mark.parametrize("bits", [2, 3, 5, 6])
+@pytest.mark.parametrize("N,K", [(320, 14336), (64, 2176), (4096, 1024), (100, 4096)])
+def test_qmm_other_widths_one_row(dev, bits, N, K):
+    """One row of 2/3/5/6-bit gs 64 on the one-row streaming kernel's odd-width instances
+    (K = 2176: 17 chunks, a K-split plan and the fixed-order reduce)."""
+    _print_case(t="qmm_odd_one_row", bits=bits, N=N, K=K)
+    wq, s, b = weights(1, N, K, bits, 64, 4000 + bits)
+    x = O.make_x_bf16(1, K, 4100 + N)
+    y = mi_qmm.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(wq[0], dev),
+                                to_dev_bf16(s[0], dev), to_dev_bf16(b[0], dev), True, 64, bits)
+    truth = O.qmm_f64(x, wq[0], s[0], b[0], 64, bits)
+    assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+
+
 @pytest.mark.parametrize("bits", [3, 5, 6])
 def test_gather_other_widths(dev, bits):
     """2/3/5/6-bit gathers: one token broadcast over its slots, one slot out of range
