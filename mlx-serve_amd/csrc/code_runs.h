@@ -1,7 +1,8 @@
 // Decoders of 8-code runs to exact bf16 pairs, shared by the one-row and few-row decode
 // kernels: the bias-less 4-bit modes nvfp4 (e2m1 codes, 16-value groups, e4m3 scales) and
 // mxfp4 (e2m1 codes, 32-value groups, e8m0 scales), where a code times its group scale is
-// exact in bf16 (at most 2 x 4 significant bits); and affine 2/3/5/6-bit codes as 128 + q.
+// exact in bf16 (at most 2 x 4 significant bits); mxfp8 (e4m3 codes, 32-value groups, e8m0
+// scales, exact as well); and affine 2/3/5/6-bit codes as 128 + q.
 #pragma once
 #include "mi_common.h"
 
@@ -42,6 +43,30 @@ MI_DEV u32x4_t fp4_run_e4m3(uint32_t codes, float sc) {
                  pair(__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, p, 1)),
                  pair(__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, p, 2)),
                  pair(__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, p, 3))};
+}
+
+// 8 e4m3 codes (two words, low byte first) times an e8m0 scale -> 4 bf16 pairs.
+// v_cvt_scalef32_pk_bf16_fp8 reads 0x7F / 0xFF as NaN; the reference reads them as +-480
+// (2^8 x 1.875), so a word holding one takes the exact per-code route (rare: the
+// largest magnitude of the format).
+MI_DEV uint32_t fp8_pair_exact(uint32_t w, int hi, float sc) {
+  const f32x2v v = {fp_e4m3((w >> (16 * hi)) & 0xFFu) * sc,
+                    fp_e4m3((w >> (16 * hi + 8)) & 0xFFu) * sc};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
+}
+MI_DEV u32x4_t fp8_run(uint32_t w0, uint32_t w1, float sc) {
+  const uint32_t m7 = 0x7F7F7F7Fu, c1 = 0x01010101u, top = 0x80808080u;
+  const bool odd = (((w0 & m7) + c1) | ((w1 & m7) + c1)) & top;
+  if (__builtin_expect(odd, 0)) {
+    const float s = sc == 0.f ? __uint_as_float(0x00400000u) : sc;  // e8m0 byte 0: 2^-127
+    return u32x4_t{fp8_pair_exact(w0, 0, s), fp8_pair_exact(w0, 1, s),
+                   fp8_pair_exact(w1, 0, s), fp8_pair_exact(w1, 1, s)};
+  }
+  return u32x4_t{
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, false)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, true)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, false)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, true))};
 }
 
 // 8 codes of `OB` bits (LSB-first, starting `sh` bits into the 64-bit pair d1:d0) ->

@@ -65,6 +65,7 @@ using code_runs::fp4_run;
 using code_runs::fp4_run_e4m3;
 using code_runs::fp_e4m3;
 using code_runs::odd_run;
+using code_runs::fp8_run;
 
 typedef __bf16 bf16x8m __attribute__((ext_vector_type(8)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -142,30 +143,6 @@ __host__ __device__ inline QmvmLds qmvm_lds(int M, int nvals, int gs, int rows, 
 
 // G is read only by gathers (work items, index arrays, expert bank); dense calls pass
 // their shapes in P.
-// 8 e4m3 codes (two words, low byte first) times an e8m0 scale -> 4 bf16 pairs.
-// v_cvt_scalef32_pk_bf16_fp8 reads 0x7F / 0xFF as NaN; the reference reads them as +-480
-// (2^8 x 1.875), so a word holding one takes the exact per-code route (rare: the
-// largest magnitude of the format).
-MI_DEV uint32_t fp8_pair_exact(uint32_t w, int hi, float sc) {
-  const f32x2v v = {fp_e4m3((w >> (16 * hi)) & 0xFFu) * sc,
-                    fp_e4m3((w >> (16 * hi + 8)) & 0xFFu) * sc};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
-}
-MI_DEV u32x4_t fp8_run(uint32_t w0, uint32_t w1, float sc) {
-  const uint32_t m7 = 0x7F7F7F7Fu, c1 = 0x01010101u, top = 0x80808080u;
-  const bool odd = (((w0 & m7) + c1) | ((w1 & m7) + c1)) & top;
-  if (__builtin_expect(odd, 0)) {
-    const float s = sc == 0.f ? __uint_as_float(0x00400000u) : sc;  // e8m0 byte 0: 2^-127
-    return u32x4_t{fp8_pair_exact(w0, 0, s), fp8_pair_exact(w0, 1, s),
-                   fp8_pair_exact(w1, 0, s), fp8_pair_exact(w1, 1, s)};
-  }
-  return u32x4_t{
-      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, false)),
-      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, true)),
-      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, false)),
-      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, true))};
-}
-
 template <int BITS, int GS, int NC, int XU, int DEPTH, int MT, bool SBF32, bool GATHER, int FPM = -1>
 // MT 64 keeps four accumulator tiles and the second pass's activations in registers:
 // blocks of up to 8 waves (256 VGPRs per lane) instead of 16.
