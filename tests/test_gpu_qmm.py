@@ -205,7 +205,8 @@ def test_gather_decode_broadcast(dev):
                                           (1, 512, 64, 20, 2), (1, 512, 40, 30, 2),
                                           (1, 1024, 32, 40, 3), (2, 512, 16, 24, 2),
                                           (1, 512, 4, 64, 4), (1, 8192, 4, 64, 4),
-                                          (1, 256, 16, 3000, 4), (2, 256, 300, 2600, 2)])
+                                          (1, 256, 16, 3000, 4), (2, 256, 300, 2600, 2),
+                                          (1, 768, 6, 120, 4)])
 def test_gather_sorted_matches_unsorted(dev, M, K, E, T, topk):
     """Sorted (grouped) path and unsorted path both match truth; the shapes cover work
     items of 1 row (one-row kernel), 2..32 rows (few-row MFMA kernel, K split across
@@ -269,6 +270,32 @@ def test_gather_sorted_multirow_nan_rows(dev):
         assert np.isnan(yf[r]).all()
     ok = np.array([0, 1, 3, 4])
     truth = O.gather_qmm_f64(x, wq, s, b, lhs[ok], rhs[ok], len(ok))
+    assert max_err_ratio(yf[ok], truth) <= BF16_TOL
+
+
+def test_gather_sorted_long_runs(dev):
+    """Sorted runs longer than one work item (32 rows), at a configs[3]-like width: a run of
+    50 rows (one lhs out of range -> NaN row), a run of 70 (three items), a run on an unknown
+    expert (NaN rows); every other row against the oracle."""
+    _print_case(t="gather_sorted_long")
+    E, N, K = 3, 768, 768
+    wq, s, b = weights(E, N, K, 4, 64, 94)
+    n0, n1, n9 = 50, 70, 10
+    x = O.make_x_bf16(n0 + n1 + n9, K, 95).reshape(-1, 1, K)
+    rhs = np.array([0] * n0 + [1] * n1 + [9] * n9, np.uint32)
+    lhs = np.arange(n0 + n1 + n9, dtype=np.uint32)
+    lhs[7] = 100000
+    y = mi_qmm.gather_qmm(to_dev_bf16(x, dev), to_dev_u32(wq, dev), to_dev_bf16(s, dev),
+                          to_dev_bf16(b, dev), lhs_indices=to_dev_u32(lhs, dev),
+                          rhs_indices=to_dev_u32(rhs, dev), group_size=64, bits=4,
+                          sorted_indices=True)
+    yf = to_f64(y).reshape(len(rhs), N)
+    bad = np.zeros(len(rhs), bool)
+    bad[7] = True
+    bad[n0 + n1:] = True
+    assert np.isnan(yf[bad]).all()
+    ok = np.nonzero(~bad)[0]
+    truth = O.gather_qmm_f64(x, wq, s, b, lhs[ok], rhs[ok], len(ok)).reshape(len(ok), N)
     assert max_err_ratio(yf[ok], truth) <= BF16_TOL
 
 
