@@ -61,7 +61,7 @@ hipError_t launch_reduce_splits(const QmvParams& P, hipStream_t s);
 
 // One-row decode kernel (qmv1.hip): 4-bit, bf16 x, items of exactly one row.
 struct Qmv1Plan {
-  int ks, gps, waves, nc, xu, depth, tiles;
+  int ks, gps, waves, nc, depth, tiles;
   size_t lds;
 };
 bool qmv1_supported(int N, int K, int gs, int bits, int x_f32);
@@ -70,8 +70,8 @@ hipError_t launch_qmv1(const QmvParams& P, const Qmv1Plan& plan, int grid_z, hip
 // dense one-row nvfp4 (fpm 0) / mxfp4 (fpm 1): the one-row kernel's fp instances
 hipError_t launch_qmv1_fp(const QmvParams& P, const Qmv1Plan& plan, int fpm, hipStream_t s);
 template <int GS>
-hipError_t launch_qmv1_gs(const QmvParams& P, dim3 grid, int waves, int nc, int xu, int depth,
-                          size_t lds, hipStream_t s);
+hipError_t launch_qmv1_gs(const QmvParams& P, dim3 grid, int waves, int nc, int depth, size_t lds,
+                          hipStream_t s);
 
 // Few-row decode kernel (qmvm*.hip): 2 <= M <= 32 rows, gs 64, bf16 x and y; dense 4-/8-bit,
 // gathers 4-bit.

@@ -119,9 +119,6 @@ Qmv1Plan qmv1_plan(int N, int K, int gs, int64_t n_items) {
   p.depth = env_depth ? env_depth
             : (p.nc <= 4 && waves_total >= 16 * kCUs) ? 4
             : p.nc <= 8 ? 2 : 4;
-  const int units = ch_split * kChunkVals / 8;
-  const int xu = (units + 64 * p.waves - 1) / (64 * p.waves);
-  p.xu = xu <= 2 ? xu : xu <= 4 ? 4 : 8;
   p.lds = qmv1_lds_bytes(ch_split * kChunkVals, p.waves);
   p.tiles = (int)tiles;
   return p;
@@ -131,9 +128,9 @@ hipError_t launch_qmv1(const QmvParams& P, const Qmv1Plan& plan, int grid_z, hip
   dim3 grid((unsigned)plan.tiles, (unsigned)P.ks, (unsigned)grid_z);
   hipError_t e;
   switch (P.group_size) {
-    case 32: e = launch_qmv1_gs<32>(P, grid, plan.waves, plan.nc, plan.xu, plan.depth, plan.lds, s); break;
-    case 64: e = launch_qmv1_gs<64>(P, grid, plan.waves, plan.nc, plan.xu, plan.depth, plan.lds, s); break;
-    default: e = launch_qmv1_gs<128>(P, grid, plan.waves, plan.nc, plan.xu, plan.depth, plan.lds, s); break;
+    case 32: e = launch_qmv1_gs<32>(P, grid, plan.waves, plan.nc, plan.depth, plan.lds, s); break;
+    case 64: e = launch_qmv1_gs<64>(P, grid, plan.waves, plan.nc, plan.depth, plan.lds, s); break;
+    default: e = launch_qmv1_gs<128>(P, grid, plan.waves, plan.nc, plan.depth, plan.lds, s); break;
   }
   if (e != hipSuccess || P.ks == 1) return e;
   return launch_reduce_splits(P, s);

@@ -2,6 +2,5 @@
 #include "qmv1_kernel.h"
 
 namespace mi {
-template hipError_t launch_qmv1_gs<32>(const QmvParams&, dim3, int, int, int, int, size_t,
-                                       hipStream_t);
+template hipError_t launch_qmv1_gs<32>(const QmvParams&, dim3, int, int, int, size_t, hipStream_t);
 }  // namespace mi

@@ -5,8 +5,9 @@
 // owns row l/4 and the 32-value slice l%4 of every 128-value chunk, so the 4 lanes of a
 // row read its 64 contiguous bytes per chunk. A wave first issues its activation loads
 // and its scale/bias loads, then its weight loads (16 B per chunk per lane): DEPTH
-// chunks up front and one more as each chunk is consumed. The activation row is staged
-// into LDS while the weights are in flight.
+// chunks up front and one more as each chunk is consumed. Each wave stages the activations
+// of its own chunks into LDS while the weights are in flight, so no block barrier precedes
+// the dot products.
 //
 // Per 8 packed values: two masks split even/odd nibbles, v_perm builds bf16 pairs
 // 0x43qq (= 128 + q exactly) and v_dot2_f32_bf16 multiplies them with the activations,
@@ -94,7 +95,7 @@ constexpr int groups_per_chunk() {
 // word becomes exact bf16 pairs (mxfp4: code x scale; nvfp4: the code, its group's scale
 // applied to the group's fp32 dot sum), dotted with the activations in natural order; no
 // affine terms, so no per-slice sums.
-template <int GS, int NC, int XU, int DEPTH, bool DENSE, bool DUAL = false, int FPM = -1>
+template <int GS, int NC, int DEPTH, bool DENSE, bool DUAL = false, int FPM = -1>
 __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P) {
   constexpr bool FP = FPM >= 0 && FPM < 100;
   // FPM 100 + b: affine b = 2, 3, 5, 6 bits, one LSB-first bitstream per row; a lane's 32
@@ -139,6 +140,9 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
   constexpr int ND = GPC >= 2 ? NC * GPC / 2 : 1;
   constexpr int NSL = (ND + 3) / 4;
   constexpr int D = DEPTH < NC ? DEPTH : NC;
+  // Each wave stages the activations of its own chunks (ceil(NC/4) 16-byte units per lane)
+  // and waits only for its own LDS writes, not for the whole block's.
+  constexpr int XN = (NC + 3) / 4;
   struct BankLoads {
     __amdgpu_buffer_rsrc_t wres;
     uint32_t wo;
@@ -174,13 +178,14 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
   //    per-matrix resources: 32-bit lane offsets, chunk / slot strides folded into the
   //    instructions' immediate offsets. Reads past a wave's range only feed chunks that
   //    weigh 0, and reads past a resource's end return 0.
-  auto issue_x = [&](int64_t xr, u32x4_t (&xv)[XU]) {
+  auto issue_x = [&](int64_t xr, u32x4_t (&xv)[XN]) {
     const uint16_t* xb = reinterpret_cast<const uint16_t*>(P.x) + (xr < 0 ? 0 : xr) + kb0;
     const __amdgpu_buffer_rsrc_t xres =
         __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, nvals * 2, kBufFlags);
 #pragma unroll
-    for (int i = 0; i < XU; ++i)
-      xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xres, (tid + i * BD) * 16, 0, 0);
+    for (int i = 0; i < XN; ++i)
+      xv[i] = __builtin_amdgcn_raw_buffer_load_b128(
+          xres, (c0 * 16 + lane + 64 * i) * 16, 0, 0);
   };
   auto issue_bank = [&](const Item& it, auto bank_c, BankLoads& L) {
     constexpr int BANK = decltype(bank_c)::value;
@@ -238,10 +243,10 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     for (int j = 0; j < D; ++j) load_chunk(L, j);
   };
   // 2. stage the activations in dot8's pair order, with per-32-value sums.
-  auto stage_x = [&](const u32x4_t (&xv)[XU]) {
+  auto stage_x = [&](const u32x4_t (&xv)[XN]) {
 #pragma unroll
-    for (int i = 0; i < XU; ++i) {
-      const int u = tid + i * BD;
+    for (int i = 0; i < XN; ++i) {
+      const int u = c0 * 16 + lane + 64 * i;  // 16-byte unit of the block range
       const u32x4_t X = xv[i];
       float s8 = ((bf16_bits_to_f32(X.x & 0xFFFFu) + bf16_bits_to_f32(X.x >> 16)) +
                   (bf16_bits_to_f32(X.y & 0xFFFFu) + bf16_bits_to_f32(X.y >> 16))) +
@@ -249,7 +254,9 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
                   (bf16_bits_to_f32(X.w & 0xFFFFu) + bf16_bits_to_f32(X.w >> 16)));
       s8 += quad_xor1(s8);
       s8 += quad_xor2(s8);
-      if (u < nunits) {
+      // (a wave whose range was clamped onto the last chunk writes the same values as that
+      // chunk's own wave)
+      if (u < nunits && u < (c0 + NC) * 16) {
         if constexpr (FP || ODD) {  // natural order: these decoders emit (q0, q1), (q2, q3), ..
           *reinterpret_cast<u32x4_t*>(xs + u * 4) = X;
           if (ODD && (u & 3) == 0) xsum[u >> 2] = s8;
@@ -264,8 +271,11 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
         }
       }
     }
-    // LDS-only barrier: the weight loads stay in flight.
-    lds_barrier();
+    // The wave reads only what its own lanes wrote: a wave-level fence, no block barrier
+    // (the weight loads stay in flight).
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
   // 3. dot products, chunk by chunk as the loads land (chunks past the range weigh 0),
   // 4. reduce the row's 4 lanes, then the waves in order, and write.
@@ -390,7 +400,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
   };
   using bank0_t = std::integral_constant<int, 0>;
   using bank1_t = std::integral_constant<int, 1>;
-  auto process = [&](const Item& it, int64_t xr, u32x4_t (&xv)[XU]) {
+  auto process = [&](const Item& it, int64_t xr, u32x4_t (&xv)[XN]) {
     BankLoads L0;
     issue_bank(it, bank0_t{}, L0);
     if constexpr (DUAL) {
@@ -412,7 +422,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     it.cnt = 1;
     it.expert = 0;
     it.expert_ok = true;
-    u32x4_t xv[XU];
+    u32x4_t xv[XN];
     issue_x(0, xv);
     process(it, 0, xv);
   } else {
@@ -424,7 +434,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
       // the activation row does not depend on the expert: its loads go out first
       const int64_t xr = item_x_row(P, it, 0);
       if (xr == -1) continue;  // block-uniform
-      u32x4_t xv[XU];
+      u32x4_t xv[XN];
       issue_x(xr, xv);
       if constexpr (DUAL) {
         if (P.route_logits) {
@@ -454,78 +464,63 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
   }
 }
 
-template <int GS, int NC, int DEPTH, bool DENSE, bool DUAL>
-void launch_xu2(const QmvParams& P, dim3 grid, dim3 block, int xu, size_t lds, hipStream_t s) {
-  switch (xu) {
-    case 1: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 1, DEPTH, DENSE, DUAL>), grid, block, lds, s, P); break;
-    case 2: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 2, DEPTH, DENSE, DUAL>), grid, block, lds, s, P); break;
-    case 4: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 4, DEPTH, DENSE, DUAL>), grid, block, lds, s, P); break;
-    default: hipLaunchKernelGGL((qmv1_kernel<GS, NC, 8, DEPTH, DENSE, DUAL>), grid, block, lds, s, P); break;
-  }
-}
-
 template <int GS, int NC, int DEPTH, bool DENSE>
-void launch_xu(const QmvParams& P, dim3 grid, dim3 block, int xu, size_t lds, hipStream_t s) {
+void launch_k(const QmvParams& P, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
   // gate + up + SwiGLU in one launch: group size 64 work items only
   if constexpr (GS == 64 && !DENSE) {
-    if (P.dual) return launch_xu2<GS, NC, DEPTH, false, true>(P, grid, block, xu, lds, s);
+    if (P.dual) {
+      hipLaunchKernelGGL((qmv1_kernel<GS, NC, DEPTH, false, true>), grid, block, lds, s, P);
+      return;
+    }
   }
-  launch_xu2<GS, NC, DEPTH, DENSE, false>(P, grid, block, xu, lds, s);
+  hipLaunchKernelGGL((qmv1_kernel<GS, NC, DEPTH, DENSE, false>), grid, block, lds, s, P);
 }
 
 template <int GS, int NC, bool DENSE>
-void launch_depth(const QmvParams& P, dim3 grid, dim3 block, int xu, int depth, size_t lds,
+void launch_depth(const QmvParams& P, dim3 grid, dim3 block, int depth, size_t lds,
                   hipStream_t s) {
   // depth 4 covers "all loads up front" for NC <= 4; NC <= 2 has a single schedule
-  if (NC > 2 && depth == 2) launch_xu<GS, NC, 2, DENSE>(P, grid, block, xu, lds, s);
-  else launch_xu<GS, NC, 4, DENSE>(P, grid, block, xu, lds, s);
+  if (NC > 2 && depth == 2) launch_k<GS, NC, 2, DENSE>(P, grid, block, lds, s);
+  else launch_k<GS, NC, 4, DENSE>(P, grid, block, lds, s);
 }
 
 template <int GS, int NC>
-hipError_t launch_nc(const QmvParams& P, dim3 grid, int waves, int xu, int depth, size_t lds,
+hipError_t launch_nc(const QmvParams& P, dim3 grid, int waves, int depth, size_t lds,
                      hipStream_t s) {
   const dim3 block(64 * waves);
   const bool dense = !P.items && !P.lhs && !P.rhs && P.n_pairs == 1 && P.M == 1;
-  if (dense) launch_depth<GS, NC, true>(P, grid, block, xu, depth, lds, s);
-  else launch_depth<GS, NC, false>(P, grid, block, xu, depth, lds, s);
+  if (dense) launch_depth<GS, NC, true>(P, grid, block, depth, lds, s);
+  else launch_depth<GS, NC, false>(P, grid, block, depth, lds, s);
   return hipGetLastError();
 }
 
 // Dense one-row launches of the other weight formats (fp4 modes, odd widths): the
-// instances for one format, dispatched on the plan's chunks per wave, loads and depth.
-template <int NC, int DEPTH, int FPM>
-void launch_xu_fmt(const QmvParams& P, dim3 grid, dim3 block, int xu, size_t lds, hipStream_t s) {
-  switch (xu) {
-    case 1: hipLaunchKernelGGL((qmv1_kernel<64, NC, 1, DEPTH, true, false, FPM>), grid, block, lds, s, P); break;
-    case 2: hipLaunchKernelGGL((qmv1_kernel<64, NC, 2, DEPTH, true, false, FPM>), grid, block, lds, s, P); break;
-    case 4: hipLaunchKernelGGL((qmv1_kernel<64, NC, 4, DEPTH, true, false, FPM>), grid, block, lds, s, P); break;
-    default: hipLaunchKernelGGL((qmv1_kernel<64, NC, 8, DEPTH, true, false, FPM>), grid, block, lds, s, P); break;
-  }
-}
-
+// instances for one format, dispatched on the plan's chunks per wave and depth.
 template <int NC, int FPM>
-void launch_nc_fmt(const QmvParams& P, dim3 grid, dim3 block, int xu, int depth, size_t lds,
-                  hipStream_t s) {
-  if (NC > 2 && depth == 2) launch_xu_fmt<NC, 2, FPM>(P, grid, block, xu, lds, s);
-  else launch_xu_fmt<NC, 4, FPM>(P, grid, block, xu, lds, s);
+void launch_nc_fmt(const QmvParams& P, dim3 grid, dim3 block, int depth, size_t lds,
+                   hipStream_t s) {
+  if (NC > 2 && depth == 2)
+    hipLaunchKernelGGL((qmv1_kernel<64, NC, 2, true, false, FPM>), grid, block, lds, s, P);
+  else
+    hipLaunchKernelGGL((qmv1_kernel<64, NC, 4, true, false, FPM>), grid, block, lds, s, P);
 }
 
 template <int FPM>
 void launch_fmt(const QmvParams& P, const Qmv1Plan& pl, hipStream_t s) {
   const dim3 grid((unsigned)pl.tiles, (unsigned)P.ks, 1), block(64 * pl.waves);
   switch (pl.nc) {
-    case 1: launch_nc_fmt<1, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
-    case 2: launch_nc_fmt<2, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
-    case 3: launch_nc_fmt<3, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
-    case 4: launch_nc_fmt<4, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
-    case 5: launch_nc_fmt<5, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
-    case 6: launch_nc_fmt<6, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
-    case 7: launch_nc_fmt<7, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
-    case 8: launch_nc_fmt<8, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
-    case 10: launch_nc_fmt<10, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
-    case 12: launch_nc_fmt<12, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
-    case 14: launch_nc_fmt<14, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
-    default: launch_nc_fmt<16, FPM>(P, grid, block, pl.xu, pl.depth, pl.lds, s); break;
+    case 1: launch_nc_fmt<1, FPM>(P, grid, block, pl.depth, pl.lds, s); break;
+    case 2: launch_nc_fmt<2, FPM>(P, grid, block, pl.depth, pl.lds, s); break;
+    case 3: launch_nc_fmt<3, FPM>(P, grid, block, pl.depth, pl.lds, s); break;
+    case 4: launch_nc_fmt<4, FPM>(P, grid, block, pl.depth, pl.lds, s); break;
+    case 5: launch_nc_fmt<5, FPM>(P, grid, block, pl.depth, pl.lds, s); break;
+    case 6: launch_nc_fmt<6, FPM>(P, grid, block, pl.depth, pl.lds, s); break;
+    case 7: launch_nc_fmt<7, FPM>(P, grid, block, pl.depth, pl.lds, s); break;
+    case 8: launch_nc_fmt<8, FPM>(P, grid, block, pl.depth, pl.lds, s); break;
+    case 10: launch_nc_fmt<10, FPM>(P, grid, block, pl.depth, pl.lds, s); break;
+    case 12: launch_nc_fmt<12, FPM>(P, grid, block, pl.depth, pl.lds, s); break;
+    case 14: launch_nc_fmt<14, FPM>(P, grid, block, pl.depth, pl.lds, s); break;
+    default: launch_nc_fmt<16, FPM>(P, grid, block, pl.depth, pl.lds, s); break;
   }
 }
 
@@ -534,22 +529,22 @@ void launch_fmt(const QmvParams& P, const Qmv1Plan& pl, hipStream_t s) {
 // Launch for one group size; each group size is instantiated in its own translation unit
 // (qmv1_g32.hip, qmv1_g64.hip, qmv1_g128.hip) so the kernel instances compile in parallel.
 template <int GS>
-hipError_t launch_qmv1_gs(const QmvParams& P, dim3 grid, int waves, int nc, int xu, int depth,
+hipError_t launch_qmv1_gs(const QmvParams& P, dim3 grid, int waves, int nc, int depth,
                           size_t lds, hipStream_t s) {
   using namespace qmv1_detail;
   switch (nc) {
-    case 1: return launch_nc<GS, 1>(P, grid, waves, xu, depth, lds, s);
-    case 2: return launch_nc<GS, 2>(P, grid, waves, xu, depth, lds, s);
-    case 3: return launch_nc<GS, 3>(P, grid, waves, xu, depth, lds, s);
-    case 4: return launch_nc<GS, 4>(P, grid, waves, xu, depth, lds, s);
-    case 5: return launch_nc<GS, 5>(P, grid, waves, xu, depth, lds, s);
-    case 6: return launch_nc<GS, 6>(P, grid, waves, xu, depth, lds, s);
-    case 7: return launch_nc<GS, 7>(P, grid, waves, xu, depth, lds, s);
-    case 8: return launch_nc<GS, 8>(P, grid, waves, xu, depth, lds, s);
-    case 10: return launch_nc<GS, 10>(P, grid, waves, xu, depth, lds, s);
-    case 12: return launch_nc<GS, 12>(P, grid, waves, xu, depth, lds, s);
-    case 14: return launch_nc<GS, 14>(P, grid, waves, xu, depth, lds, s);
-    default: return launch_nc<GS, 16>(P, grid, waves, xu, depth, lds, s);
+    case 1: return launch_nc<GS, 1>(P, grid, waves, depth, lds, s);
+    case 2: return launch_nc<GS, 2>(P, grid, waves, depth, lds, s);
+    case 3: return launch_nc<GS, 3>(P, grid, waves, depth, lds, s);
+    case 4: return launch_nc<GS, 4>(P, grid, waves, depth, lds, s);
+    case 5: return launch_nc<GS, 5>(P, grid, waves, depth, lds, s);
+    case 6: return launch_nc<GS, 6>(P, grid, waves, depth, lds, s);
+    case 7: return launch_nc<GS, 7>(P, grid, waves, depth, lds, s);
+    case 8: return launch_nc<GS, 8>(P, grid, waves, depth, lds, s);
+    case 10: return launch_nc<GS, 10>(P, grid, waves, depth, lds, s);
+    case 12: return launch_nc<GS, 12>(P, grid, waves, depth, lds, s);
+    case 14: return launch_nc<GS, 14>(P, grid, waves, depth, lds, s);
+    default: return launch_nc<GS, 16>(P, grid, waves, depth, lds, s);
   }
 }
 
