@@ -2,8 +2,9 @@
 // (the reference's gatherQmvDownReduce, src/transformer.zig:20675-20761): one launch
 // instead of a gather and a reduce, same results bit for bit.
 //
-// Block = 16 output rows of one token; its waves are k slots x WS waves per slot. The
-// waves of slot s stage that pair's activation row into their own LDS region and stream
+// Block = 16 output rows of one token; its waves are k slots x WS waves per slot. Each
+// wave of slot s stages its own chunks of that pair's activation row into the slot's LDS
+// region (a wave-level fence, no block barrier, before its dot products) and streams
 // the 16-row tile of expert inds[t*k + s] over K (WS x NC chunks of 128 values), with
 // the one-row kernel's arithmetic (bf16 0x43qq nibbles, v_dot2_f32_bf16, affine terms per
 // 32-value slice). The 16 writer threads then take the slots in ascending order:
@@ -31,9 +32,10 @@ MI_DEV uint16_t bf16_add_bits(uint16_t a, uint16_t b) {
   return (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(a) + bf16_bits_to_f32(b));
 }
 
-template <int NC, int XU>
+template <int NC>
 __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDownParams P) {
   constexpr int GS = 64;
+  constexpr int XN = (NC + 3) / 4;  // 16-byte activation units per lane (its own chunks)
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ int okf[16];
   __shared__ uint16_t score_l[16];
@@ -70,12 +72,11 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDownParams P) {
       (void*)(P.scales + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
   const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(P.biases + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
-  const int ts = kp * 64 + lane, TS = WS * 64;  // thread within the slot's waves
   const int nunits = K / 8;
-  u32x4_t xv[XU];
+  u32x4_t xv[XN];
 #pragma unroll
-  for (int i = 0; i < XU; ++i)
-    xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xres, (ts + i * TS) * 16, 0, 0);
+  for (int i = 0; i < XN; ++i)
+    xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xres, (c0 * 16 + lane + 64 * i) * 16, 0, 0);
   constexpr int NSL = (NC + 3) / 4;  // gs 64: a dword holds the two groups of a chunk
   const uint32_t so = nn * (uint32_t)(G * 2) + (uint32_t)c0 * 4;
   uint32_t sd[NSL], bd[NSL];
@@ -89,10 +90,10 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDownParams P) {
 #pragma unroll
   for (int j = 0; j < NC; ++j) wv[j] = __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 64 * j, 0, 0);
 
-  // 2. stage the slot's activations in dot8's pair order with per-32-value sums.
+  // 2. stage the wave's activations in dot8's pair order with per-32-value sums.
 #pragma unroll
-  for (int i = 0; i < XU; ++i) {
-    const int u = ts + i * TS;
+  for (int i = 0; i < XN; ++i) {
+    const int u = c0 * 16 + lane + 64 * i;
     const u32x4_t X = xv[i];
     float s8 = ((bf16_bits_to_f32(X.x & 0xFFFFu) + bf16_bits_to_f32(X.x >> 16)) +
                 (bf16_bits_to_f32(X.y & 0xFFFFu) + bf16_bits_to_f32(X.y >> 16))) +
@@ -100,7 +101,7 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDownParams P) {
                 (bf16_bits_to_f32(X.w & 0xFFFFu) + bf16_bits_to_f32(X.w >> 16)));
     s8 += quad_xor1(s8);
     s8 += quad_xor2(s8);
-    if (u < nunits) {
+    if (u < nunits && u < (c0 + NC) * 16) {
       u32x4_t o;
       o.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
       o.y = perm_b32(X.w, X.z, 0x05040100u);  // (x4, x6)
@@ -110,9 +111,12 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDownParams P) {
       if ((u & 3) == 0) xsum[u >> 2] = s8;
     }
   }
-  if (kp == 0 && lane == 0) okf[s] = ok;
+  if (kp == 0 && lane == 0) okf[s] = ok;  // read after the reduction barrier below
   if (tid < k) score_l[tid] = my_score;
-  lds_barrier();
+  // the wave reads only what its own lanes staged
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
   // 3. dot products of the wave's chunks.
   float yv = 0.f;
@@ -156,23 +160,13 @@ __global__ void __launch_bounds__(1024) moe_down_kernel(MoeDownParams P) {
   (void)W;
 }
 
-template <int NC, int XU>
+template <int NC>
 void launch_one(const MoeDownParams& P, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
   static const bool big_lds = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&moe_down_kernel<NC, XU>),
+      reinterpret_cast<const void*>(&moe_down_kernel<NC>),
       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024) == hipSuccess;
   (void)big_lds;  // a failure shows as a launch error for plans above 64 KiB
-  hipLaunchKernelGGL((moe_down_kernel<NC, XU>), grid, block, lds, s, P);
-}
-
-template <int NC>
-void launch_xu(const MoeDownParams& P, dim3 grid, dim3 block, int xu, size_t lds, hipStream_t s) {
-  switch (xu) {
-    case 1: launch_one<NC, 1>(P, grid, block, lds, s); break;
-    case 2: launch_one<NC, 2>(P, grid, block, lds, s); break;
-    case 4: launch_one<NC, 4>(P, grid, block, lds, s); break;
-    default: launch_one<NC, 8>(P, grid, block, lds, s); break;
-  }
+  hipLaunchKernelGGL((moe_down_kernel<NC>), grid, block, lds, s, P);
 }
 
 }  // namespace
@@ -185,7 +179,7 @@ bool moe_down_supported(int64_t T, int k, int64_t N, int64_t K, int gs, int bits
   if (N * (K / 2) >= ((int64_t)1 << 31) || k * ws > 16 || ws * nc != K / 128) return false;
   if (!((nc >= 1 && nc <= 8) || nc == 10 || nc == 12 || nc == 14 || nc == 16)) return false;
   const size_t lds = (size_t)k * (K * 2 + (K / 32) * 4) + (size_t)k * ws * 16 * 4;
-  return (K / 8 + 64 * ws - 1) / (64 * ws) <= 8 && lds <= 160 * 1024 - 1024;
+  return lds <= 160 * 1024 - 1024;
 }
 
 hipError_t launch_moe_down(uint16_t* y, const uint16_t* act, const uint32_t* w,
@@ -193,26 +187,23 @@ hipError_t launch_moe_down(uint16_t* y, const uint16_t* act, const uint32_t* w,
                            const uint16_t* scores, int64_t T, int k, int64_t N, int64_t K,
                            int64_t E, int ws, int nc, hipStream_t s) {
   if (!moe_down_supported(T, k, N, K, 64, 4, ws, nc)) return hipErrorInvalidValue;
-  const int units = (int)(K / 8);
-  const int xu0 = (units + 64 * ws - 1) / (64 * ws);
-  const int xu = xu0 <= 1 ? 1 : xu0 <= 2 ? 2 : xu0 <= 4 ? 4 : 8;
   MoeDownParams P{act, w, scales, biases, inds, scores, y, (int)N, (int)K, (int)E, k, ws};
   const dim3 grid((unsigned)((N + 15) / 16), (unsigned)T);
   const dim3 block(64 * k * ws);
   const size_t lds = (size_t)k * (K * 2 + (K / 32) * 4) + (size_t)k * ws * 16 * 4;
   switch (nc) {
-    case 1: launch_xu<1>(P, grid, block, xu, lds, s); break;
-    case 2: launch_xu<2>(P, grid, block, xu, lds, s); break;
-    case 3: launch_xu<3>(P, grid, block, xu, lds, s); break;
-    case 4: launch_xu<4>(P, grid, block, xu, lds, s); break;
-    case 5: launch_xu<5>(P, grid, block, xu, lds, s); break;
-    case 6: launch_xu<6>(P, grid, block, xu, lds, s); break;
-    case 7: launch_xu<7>(P, grid, block, xu, lds, s); break;
-    case 8: launch_xu<8>(P, grid, block, xu, lds, s); break;
-    case 10: launch_xu<10>(P, grid, block, xu, lds, s); break;
-    case 12: launch_xu<12>(P, grid, block, xu, lds, s); break;
-    case 14: launch_xu<14>(P, grid, block, xu, lds, s); break;
-    default: launch_xu<16>(P, grid, block, xu, lds, s); break;
+    case 1: launch_one<1>(P, grid, block, lds, s); break;
+    case 2: launch_one<2>(P, grid, block, lds, s); break;
+    case 3: launch_one<3>(P, grid, block, lds, s); break;
+    case 4: launch_one<4>(P, grid, block, lds, s); break;
+    case 5: launch_one<5>(P, grid, block, lds, s); break;
+    case 6: launch_one<6>(P, grid, block, lds, s); break;
+    case 7: launch_one<7>(P, grid, block, lds, s); break;
+    case 8: launch_one<8>(P, grid, block, lds, s); break;
+    case 10: launch_one<10>(P, grid, block, lds, s); break;
+    case 12: launch_one<12>(P, grid, block, lds, s); break;
+    case 14: launch_one<14>(P, grid, block, lds, s); break;
+    default: launch_one<16>(P, grid, block, lds, s); break;
   }
   return hipGetLastError();
 }
