@@ -517,7 +517,7 @@ def main():
                    "gate_rel_err_vs_oracle": float(f"{gate_err:.3e}")},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": pmc_traffic(), "kernel": "mi::qmv1_kernel<64, NC, XU, true> (dense M=1 instances)",
+                     "traffic": pmc_traffic(), "kernel": "mi::qmv1_kernel<64, NC, DEPTH, true> (dense M=1 instances)",
                      "bytes_per_launch": head["bytes_per_launch"],
                      "avg_launch_us": round(head["avg_launch_us"], 3)},
         "cpu_baseline": cpu,
