@@ -47,26 +47,36 @@ MI_DEV u32x4_t fp4_run_e4m3(uint32_t codes, float sc) {
 
 // 8 e4m3 codes (two words, low byte first) times an e8m0 scale -> 4 bf16 pairs.
 // v_cvt_scalef32_pk_bf16_fp8 reads 0x7F / 0xFF as NaN; the reference reads them as +-480
-// (2^8 x 1.875), so a word holding one takes the exact per-code route (rare: the
-// largest magnitude of the format).
-MI_DEV uint32_t fp8_pair_exact(uint32_t w, int hi, float sc) {
-  const f32x2v v = {fp_e4m3((w >> (16 * hi)) & 0xFFu) * sc,
-                    fp_e4m3((w >> (16 * hi + 8)) & 0xFFu) * sc};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
-}
+// (2^8 x 1.875). A run holding one (never in weights the format's quantizer writes, but
+// any byte is a valid code) keeps the conversion's other values and patches those codes
+// with +-bf16(480 x scale), exact: the scale is a power of two (2^-127 for scale byte 0).
 MI_DEV u32x4_t fp8_run(uint32_t w0, uint32_t w1, float sc) {
   const uint32_t m7 = 0x7F7F7F7Fu, c1 = 0x01010101u, top = 0x80808080u;
-  const bool odd = (((w0 & m7) + c1) | ((w1 & m7) + c1)) & top;
-  if (__builtin_expect(odd, 0)) {
-    const float s = sc == 0.f ? __uint_as_float(0x00400000u) : sc;  // e8m0 byte 0: 2^-127
-    return u32x4_t{fp8_pair_exact(w0, 0, s), fp8_pair_exact(w0, 1, s),
-                   fp8_pair_exact(w1, 0, s), fp8_pair_exact(w1, 1, s)};
-  }
-  return u32x4_t{
+  // bit 7 of each byte: the code's low 7 bits are all ones
+  const uint32_t e0 = ((w0 & m7) + c1) & top, e1 = ((w1 & m7) + c1) & top;
+  u32x4_t r{
       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, false)),
       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, true)),
       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, false)),
       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, true))};
+  if (__builtin_expect((e0 | e1) != 0u, 0)) {
+    const float s = sc == 0.f ? __uint_as_float(0x00400000u) : sc;  // e8m0 byte 0: 2^-127
+    const uint32_t mag = __float_as_uint(480.f * s) >> 16;           // exact in bf16
+    const uint32_t mp = mag | (mag << 16);
+    // dword d of word w holds codes 2d, 2d+1: v_perm's sign-extending selectors spread their
+    // flags (e bits 7, 15 / 23, 31, reached as bits 15 / 31 of e << 8 and of e) over the two
+    // bf16 halves, and byte selectors move the codes' sign bits to bits 15 and 31
+    auto fix = [&](uint32_t res, uint32_t w, uint32_t e, int d) {
+      const uint32_t m = perm_b32(e, e << 8, d ? 0x0B0B0909u : 0x0A0A0808u);
+      const uint32_t sg = perm_b32(w, w, d ? 0x030C020Cu : 0x010C000Cu) & 0x80008000u;
+      return (m & (sg | mp)) | (~m & res);
+    };
+    r.x = fix(r.x, w0, e0, 0);
+    r.y = fix(r.y, w0, e0, 1);
+    r.z = fix(r.z, w1, e1, 0);
+    r.w = fix(r.w, w1, e1, 1);
+  }
+  return r;
 }
 
 // 8 codes of `OB` bits (LSB-first, starting `sh` bits into the 64-bit pair d1:d0) ->

@@ -429,12 +429,14 @@ def test_qmm_fp4_one_row(dev, mode, M, N, K):
     assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
 
 
-@pytest.mark.parametrize("mode", ["nvfp4", "mxfp4"])
+@pytest.mark.parametrize("mode", ["nvfp4", "mxfp4", "mxfp8"])
 @pytest.mark.parametrize("M", [1, 8])
 def test_qmm_fp4_mfma_scale_edges(dev, mode, M):
     """Scale bytes at the ends of their formats: e4m3 0x7F (480 in the reference's
-    reading) and 0x01 (2^-9), e8m0 1 and 254 groups mixed with ordinary ones (one row:
-    the one-row kernel; eight: the few-row MFMA kernel)."""
+    reading) and 0x01 (2^-9), e8m0 0 (2^-127), 1 and 140 groups mixed with ordinary ones;
+    for mxfp8 also dense runs of the codes 0x7F / 0xFF (+-480, which the hardware
+    conversion reads as NaN) in those groups (one row: the one-row kernel or, for mxfp8,
+    the few-row MFMA kernel; eight: the few-row MFMA kernel)."""
     _print_case(t="qmm_fp4_edges", mode=mode, M=M)
     N, K = 64, 512
     wq, sc = _fp_weight(mode, N, K, 77)
@@ -445,6 +447,15 @@ def test_qmm_fp4_mfma_scale_edges(dev, mode, M):
     else:
         sc[0, 1] = 1
         sc[1, :] = 140  # 2^13
+    if mode == "mxfp8":
+        sc[2, :] = 0  # 2^-127
+        b = wq.view(np.uint8).reshape(N, K)
+        b[2, ::5] = 0x7F
+        b[2, 1::7] = 0xFF
+        b[1, 3::11] = 0xFF
+        b[4, ::2] = 0x7F
+        b[4, 1::2] = 0xFF
+        b[5, 64:96] = 0x7E  # the largest finite code of the hardware's reading
     x = O.make_x_bf16(M, K, 78)
     y = mi_qmm.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(wq, dev),
                                 torch.from_numpy(sc).to(dev), None, True, mode=mode)
