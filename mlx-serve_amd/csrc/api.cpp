@@ -676,9 +676,9 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
     if (N > (int64_t)1 << 30 || M > (int64_t)1 << 30 || N * K * 2 > ((int64_t)1 << 34))
       return fail(MI_ERR_INVALID, "N, M or N*K too large");
     hipStream_t s = (hipStream_t)stream;
-    // one row of nvfp4 / mxfp4: the one-row streaming kernel's fp instances
+    // one row of nvfp4 / mxfp4 / mxfp8: the one-row streaming kernel's fp instances
     static const int fp_qmv1 = env_int("MI_QMM_FP_QMV1", 1);
-    if (fp_qmv1 && M == 1 && fm <= 1 && mi::qmv1_supported((int)N, (int)K, 64, 4, 0)) {
+    if (fp_qmv1 && M == 1 && K % 128 == 0 && N * K * (fm == 2 ? 2 : 1) / 2 < ((int64_t)1 << 31)) {
       const mi::Qmv1Plan pl = mi::qmv1_plan((int)N, (int)K, 64, 1);
       mi::QmvParams P{};
       P.w = w;
@@ -692,7 +692,7 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
       P.M = 1;
       P.N = (int)N;
       P.K = (int)K;
-      P.bits = 4;
+      P.bits = fm == 2 ? 8 : 4;
       P.group_size = 64;
       P.rpi = 1;
       P.items_per_pair = 1;

@@ -90,8 +90,9 @@ constexpr int groups_per_chunk() {
 }
 
 // Up to 16 waves per block when a wave holds <= 8 chunks (<= 128 VGPRs), else 8.
-// FPM 0 / 1 (dense only): bias-less nvfp4 / mxfp4 weights in the same chunk layout, P.scales
-// then uint8 [N, K / FGS] (e4m3 for nvfp4's 16-value groups, e8m0 for mxfp4's 32). Each 8-code
+// FPM 0 / 1 / 2 (dense only): bias-less nvfp4 / mxfp4 / mxfp8 weights (mxfp8: one byte a
+// code, a chunk is 128 bytes of a row), P.scales then uint8 [N, K / FGS] (e4m3 for nvfp4's
+// 16-value groups, e8m0 for the mx modes' 32). Each 8-code
 // word becomes exact bf16 pairs (mxfp4: code x scale; nvfp4: the code, its group's scale
 // applied to the group's fp32 dot sum), dotted with the activations in natural order; no
 // affine terms, so no per-slice sums.
@@ -102,7 +103,8 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
   // codes of a chunk are 4b bytes at byte 4bg of the chunk's 16b (dword-aligned)
   constexpr bool ODD = FPM >= 100;
   constexpr int OB = ODD ? FPM - 100 : 4;
-  static_assert(!FP || (DENSE && !DUAL && (FPM == 0 || FPM == 1)), "fp4 modes: dense calls");
+  static_assert(!FP || (DENSE && !DUAL && FPM <= 2), "fp modes: dense calls");
+  constexpr bool FP8 = FPM == 2;
   static_assert(!ODD || (DENSE && !DUAL && GS == 64 && (OB == 2 || OB == 3 || OB == 5 || OB == 6)),
                 "odd widths: dense calls at group size 64");
   constexpr int FGS = FPM == 0 ? 16 : 32;
@@ -150,6 +152,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     u32x2_t fs[FP ? NC : 1];  // fp modes: the row's scale bytes of each chunk
     u32x4_t wv[NC];
     u32x2_t wv2[ODD ? NC : 1];  // odd widths: dwords 4, 5 of a lane's 5- or 6-dword slice
+    u32x4_t wv8[FP8 ? NC : 1];  // mxfp8: bytes 16..31 of a lane's 32-byte slice
   };
   // One chunk's weights of this lane: 16 B at 4 bits, OB dwords at the odd widths.
   auto load_chunk = [&](BankLoads& L, int j) __attribute__((always_inline)) {
@@ -170,6 +173,9 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
                                         __builtin_amdgcn_raw_buffer_load_b64(L.wres, o + 16, 0, 0));
         }
       }
+    } else if constexpr (FP8) {
+      L.wv[j] = __builtin_amdgcn_raw_buffer_load_b128(L.wres, L.wo + 128 * j, 0, 0);
+      L.wv8[j] = __builtin_amdgcn_raw_buffer_load_b128(L.wres, L.wo + 128 * j + 16, 0, 0);
     } else {
       L.wv[j] = __builtin_amdgcn_raw_buffer_load_b128(L.wres, L.wo + 64 * j, 0, 0);
     }
@@ -197,14 +203,17 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     L.wres = ODD ? __builtin_amdgcn_make_buffer_rsrc(
                        (void*)((const unsigned char*)Pw + mat * (uint32_t)(K / 8 * OB)), (short)0,
                        N * (K / 8 * OB), kBufFlags)
+                 : FP8 ? __builtin_amdgcn_make_buffer_rsrc((void*)(Pw + mat * (uint32_t)(K / 4)),
+                                                           (short)0, N * K, kBufFlags)
                  : __builtin_amdgcn_make_buffer_rsrc((void*)(Pw + mat * (uint32_t)(K / 8)), (short)0,
                                                      N * (K / 2), kBufFlags);
     const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(Ps + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
     const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(Pb + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
-    L.wo = ODD ? nn * (uint32_t)(K / 8 * OB) + (uint32_t)(kb0 + c0 * kChunkVals) / 8 * OB + 4 * OB * g
-               : nn * (uint32_t)(K / 2) + (uint32_t)(kb0 + c0 * kChunkVals) / 2 + 16 * g;
+    L.wo = ODD   ? nn * (uint32_t)(K / 8 * OB) + (uint32_t)(kb0 + c0 * kChunkVals) / 8 * OB + 4 * OB * g
+           : FP8 ? nn * (uint32_t)K + (uint32_t)(kb0 + c0 * kChunkVals) + 32 * g
+                 : nn * (uint32_t)(K / 2) + (uint32_t)(kb0 + c0 * kChunkVals) / 2 + 16 * g;
     // Scales/biases. gs 64/32: the wave's groups of a row are contiguous dwords; lane g
     // of the row's quad loads dwords g, g+4, ... and chunks take theirs by a quad
     // broadcast. gs 128: one bf16 per chunk.
@@ -293,18 +302,24 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
       const u32x4_t* xp = reinterpret_cast<const u32x4_t*>(xs + off / 2);
       if constexpr (FP) {
         // lane slice g of chunk j: codes 32g .. 32g + 31, word t = codes 32g + 8t ..
-        // mxfp4: one e8m0 scale (byte g) for the slice, applied exactly in the conversion.
+        // mxfp4 / mxfp8: one e8m0 scale (byte g) for the slice, applied in the conversion.
         // nvfp4: two e4m3 scales (bytes 2g, 2g+1), one per 16 codes: the codes convert
         // exactly (scale 1), each group's dot sum is scaled in fp32, the groups in order.
         float acc = 0.f, grp = 0.f;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const uint32_t codes = t == 0 ? L.wv[j].x : t == 1 ? L.wv[j].y : t == 2 ? L.wv[j].z
-                                                                              : L.wv[j].w;
-          const u32x4_t a = code_runs::fp4_run(
-              codes, FPM == 1 ? __uint_as_float(((L.fs[j].x >> (8 * g)) & 0xFFu) << 23) : 1.f);
+          const float e8 = __uint_as_float(((L.fs[j].x >> (8 * g)) & 0xFFu) << 23);
+          u32x4_t a;
+          if constexpr (FP8) {  // codes 8t .. 8t+7: two dwords of the lane's 32 bytes
+            const u32x4_t h = t < 2 ? L.wv[j] : L.wv8[j];
+            a = (t & 1) ? code_runs::fp8_run(h.z, h.w, e8) : code_runs::fp8_run(h.x, h.y, e8);
+          } else {
+            const uint32_t codes = t == 0 ? L.wv[j].x : t == 1 ? L.wv[j].y : t == 2 ? L.wv[j].z
+                                                                                : L.wv[j].w;
+            a = code_runs::fp4_run(codes, FPM == 1 ? e8 : 1.f);
+          }
           const u32x4_t xv4 = xp[t];
-          float& d = FPM == 1 ? acc : grp;
+          float& d = FPM == 0 ? grp : acc;
           d = dot2(a.x, xv4.x, d);
           d = dot2(a.y, xv4.y, d);
           d = dot2(a.z, xv4.z, d);

@@ -416,9 +416,9 @@ def test_qmm_fp4_mfma(dev, mode, M, N, K):
 @pytest.mark.parametrize("M,N,K", [(1, 320, 14336), (1, 64, 2176), (1, 4096, 1024),
                                    (1, 100, 4096)])
 def test_qmm_fp4_one_row(dev, mode, M, N, K):
-    """One row of nvfp4 / mxfp4 on the one-row streaming kernel's fp instances (K = 2176:
-    17 chunks, a K-split plan and the fixed-order reduce); one row of mxfp8 on qmvm, whose
-    0x7F / 0xFF codes take the exact per-code route."""
+    """One row of nvfp4 / mxfp4 / mxfp8 on the one-row streaming kernel's fp instances
+    (K = 2176: 17 chunks, a K-split plan and the fixed-order reduce; mxfp8's 0x7F / 0xFF
+    codes patched to +-480 x scale)."""
     _print_case(t="qmm_fp4_one_row", mode=mode, N=N, K=K)
     wq, sc = _fp_weight(mode, N, K, 90 + N)
     x = O.make_x_bf16(M, K, 91 + K)
