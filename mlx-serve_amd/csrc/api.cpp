@@ -777,13 +777,10 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
     hipError_t e = mi::launch_prefill(Q, s);
     return e == hipSuccess ? MI_OK : hip_fail(e, "prefill launch");
   }
-  const bool odd_width = nb != 4 && nb != 8;
-  if (odd_width && (x_dtype != MI_DTYPE_BFLOAT16 || N * K * 2 > ((int64_t)1 << 34)))
-    return fail(MI_ERR_UNSUPPORTED, "bits=%d: bf16 activations only", nb);
-  // one row at gs 64: the one-row streaming kernel's odd-width instances
-  static const int odd_qmv1 = env_int("MI_QMM_ODD_QMV1", 1);
-  if (odd_width && odd_qmv1 && M == 1 && gs == 64 && x_dtype == MI_DTYPE_BFLOAT16 &&
-      K % 128 == 0 && N * (K / 8 * nb) < ((int64_t)1 << 31)) {
+  // Dense one row of gs-64 affine weights in a format the one-row streaming kernel has
+  // instances for (fpm 100 + bits: 2/3/5/6/8 bits), with its plan and fixed-order K-split
+  // reduce.
+  auto run_qmv1_fmt = [&](int fpm) -> int {
     const mi::Qmv1Plan pl = mi::qmv1_plan((int)N, (int)K, 64, 1);
     mi::QmvParams P{};
     P.w = w;
@@ -808,13 +805,21 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
     P.row_blocks = pl.tiles;
     if (pl.ks > 1) {
       void* data = nullptr;
-      rc = workspace(s, (size_t)pl.ks * N * 4, &data);
-      if (rc) return rc;
+      const int rc2 = workspace(s, (size_t)pl.ks * N * 4, &data);
+      if (rc2) return rc2;
       P.part = (float*)data;
     }
-    hipError_t e = mi::launch_qmv1_fp(P, pl, 100 + nb, s);
-    return e == hipSuccess ? MI_OK : hip_fail(e, "qmv1 odd-width launch");
-  }
+    hipError_t e = mi::launch_qmv1_fp(P, pl, fpm, s);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "qmv1 format launch");
+  };
+  const bool odd_width = nb != 4 && nb != 8;
+  if (odd_width && (x_dtype != MI_DTYPE_BFLOAT16 || N * K * 2 > ((int64_t)1 << 34)))
+    return fail(MI_ERR_UNSUPPORTED, "bits=%d: bf16 activations only", nb);
+  // one row at gs 64: the one-row streaming kernel's odd-width instances
+  static const int odd_qmv1 = env_int("MI_QMM_ODD_QMV1", 1);
+  if (odd_width && odd_qmv1 && M == 1 && gs == 64 && x_dtype == MI_DTYPE_BFLOAT16 &&
+      K % 128 == 0 && N * (K / 8 * nb) < ((int64_t)1 << 31))
+    return run_qmv1_fmt(100 + nb);
   static const int odd_mfma = env_int("MI_QMM_ODD_MFMA", 1);
   mi::QmvmPlan op{};
   // 2..32 rows, gs 64 (and one row at 2 bits, where the per-code kernel is VALU-bound)
@@ -891,6 +896,11 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
       return MI_OK;
     }
   }
+  // one row of 8-bit at gs 64: the one-row streaming kernel's 8-bit instances
+  static const int q8_qmv1 = env_int("MI_QMM_Q8_QMV1", 1);
+  if (q8_qmv1 && nb == 8 && M == 1 && gs == 64 && x_dtype == MI_DTYPE_BFLOAT16 &&
+      K % 128 == 0 && N * K < ((int64_t)1 << 31))
+    return run_qmv1_fmt(108);
   static const int q8_one = env_int("MI_QMM_Q8_QMVM1", 1);
   if (use_qmvm && x_dtype == MI_DTYPE_BFLOAT16 && M >= (nb == 8 && q8_one ? 1 : 2) &&
       M <= qmvm_max && mi::qmvm_plan((int)M, (int)N, (int)K, gs, nb, 1, &qp))

@@ -101,10 +101,16 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
   constexpr bool FP = FPM >= 0 && FPM < 100;
   // FPM 100 + b: affine b = 2, 3, 5, 6 bits, one LSB-first bitstream per row; a lane's 32
   // codes of a chunk are 4b bytes at byte 4bg of the chunk's 16b (dword-aligned)
-  constexpr bool ODD = FPM >= 100;
+  // FPM 108: affine 8 bits at gs 64, one byte a code (a chunk is 128 bytes of a row); each
+  // code converts exactly to bf16 (v_cvt_f32_ubyte, v_cvt_pk_bf16_f32) and the epilogue adds
+  // b * sum(x) (no 128 offset)
+  constexpr bool B8 = FPM == 108;
+  constexpr bool ODD = FPM >= 100 && !B8;
   constexpr int OB = ODD ? FPM - 100 : 4;
   static_assert(!FP || (DENSE && !DUAL && FPM <= 2), "fp modes: dense calls");
   constexpr bool FP8 = FPM == 2;
+  static_assert(!B8 || (DENSE && !DUAL && GS == 64), "8-bit one-row: dense calls at gs 64");
+  constexpr bool BYTES = FP8 || B8;  // one byte a code: two 16-byte loads per lane and chunk
   static_assert(!ODD || (DENSE && !DUAL && GS == 64 && (OB == 2 || OB == 3 || OB == 5 || OB == 6)),
                 "odd widths: dense calls at group size 64");
   constexpr int FGS = FPM == 0 ? 16 : 32;
@@ -152,7 +158,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     u32x2_t fs[FP ? NC : 1];  // fp modes: the row's scale bytes of each chunk
     u32x4_t wv[NC];
     u32x2_t wv2[ODD ? NC : 1];  // odd widths: dwords 4, 5 of a lane's 5- or 6-dword slice
-    u32x4_t wv8[FP8 ? NC : 1];  // mxfp8: bytes 16..31 of a lane's 32-byte slice
+    u32x4_t wv8[BYTES ? NC : 1];  // one byte a code: bytes 16..31 of a lane's 32-byte slice
   };
   // One chunk's weights of this lane: 16 B at 4 bits, OB dwords at the odd widths.
   auto load_chunk = [&](BankLoads& L, int j) __attribute__((always_inline)) {
@@ -173,7 +179,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
                                         __builtin_amdgcn_raw_buffer_load_b64(L.wres, o + 16, 0, 0));
         }
       }
-    } else if constexpr (FP8) {
+    } else if constexpr (BYTES) {
       L.wv[j] = __builtin_amdgcn_raw_buffer_load_b128(L.wres, L.wo + 128 * j, 0, 0);
       L.wv8[j] = __builtin_amdgcn_raw_buffer_load_b128(L.wres, L.wo + 128 * j + 16, 0, 0);
     } else {
@@ -203,7 +209,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     L.wres = ODD ? __builtin_amdgcn_make_buffer_rsrc(
                        (void*)((const unsigned char*)Pw + mat * (uint32_t)(K / 8 * OB)), (short)0,
                        N * (K / 8 * OB), kBufFlags)
-                 : FP8 ? __builtin_amdgcn_make_buffer_rsrc((void*)(Pw + mat * (uint32_t)(K / 4)),
+                 : BYTES ? __builtin_amdgcn_make_buffer_rsrc((void*)(Pw + mat * (uint32_t)(K / 4)),
                                                            (short)0, N * K, kBufFlags)
                  : __builtin_amdgcn_make_buffer_rsrc((void*)(Pw + mat * (uint32_t)(K / 8)), (short)0,
                                                      N * (K / 2), kBufFlags);
@@ -212,7 +218,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
     const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(Pb + mat * (uint32_t)G), (short)0, N * G * 2, kBufFlags);
     L.wo = ODD   ? nn * (uint32_t)(K / 8 * OB) + (uint32_t)(kb0 + c0 * kChunkVals) / 8 * OB + 4 * OB * g
-           : FP8 ? nn * (uint32_t)K + (uint32_t)(kb0 + c0 * kChunkVals) + 32 * g
+           : BYTES ? nn * (uint32_t)K + (uint32_t)(kb0 + c0 * kChunkVals) + 32 * g
                  : nn * (uint32_t)(K / 2) + (uint32_t)(kb0 + c0 * kChunkVals) / 2 + 16 * g;
     // Scales/biases. gs 64/32: the wave's groups of a row are contiguous dwords; lane g
     // of the row's quad loads dwords g, g+4, ... and chunks take theirs by a quad
@@ -266,9 +272,9 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
       // (a wave whose range was clamped onto the last chunk writes the same values as that
       // chunk's own wave)
       if (u < nunits && u < (c0 + NC) * 16) {
-        if constexpr (FP || ODD) {  // natural order: these decoders emit (q0, q1), (q2, q3), ..
+        if constexpr (FP || ODD || B8) {  // natural order: these decoders emit (q0, q1), (q2, q3), ..
           *reinterpret_cast<u32x4_t*>(xs + u * 4) = X;
-          if (ODD && (u & 3) == 0) xsum[u >> 2] = s8;
+          if ((ODD || B8) && (u & 3) == 0) xsum[u >> 2] = s8;
         } else {
           u32x4_t o;
           o.x = perm_b32(X.y, X.x, 0x05040100u);  // (x0, x2)
@@ -358,6 +364,23 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
           acc = dot2(a.z, xv4.z, acc);
           acc = dot2(a.w, xv4.w, acc);
         }
+      } else if constexpr (B8) {
+        // codes 8t .. 8t+7 of the slice: two dwords of the lane's 32 bytes, each byte an
+        // exact bf16 (0..255 needs 8 significant bits)
+        auto pk = [](uint32_t d, int b) {
+          const float lo = (float)((d >> (8 * b)) & 0xFFu), hi = (float)((d >> (8 * b + 8)) & 0xFFu);
+          return __builtin_bit_cast(uint32_t, __builtin_convertvector((code_runs::f32x2v){lo, hi}, bf16x2_t));
+        };
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const u32x4_t h = t < 2 ? L.wv[j] : L.wv8[j];
+          const uint32_t d0 = (t & 1) ? h.z : h.x, d1 = (t & 1) ? h.w : h.y;
+          const u32x4_t xv4 = xp[t];
+          acc = dot2(pk(d0, 0), xv4.x, acc);
+          acc = dot2(pk(d0, 2), xv4.y, acc);
+          acc = dot2(pk(d1, 0), xv4.z, acc);
+          acc = dot2(pk(d1, 2), xv4.w, acc);
+        }
       } else {
         acc = dot8(L.wv[j].x, xp[0], acc);
         acc = dot8(L.wv[j].y, xp[1], acc);
@@ -386,7 +409,7 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
       s *= use;
       b *= use;
       y = fmaf(s, acc, y);
-      y = fmaf(fmaf(-128.f, s, b), xsum[off >> 5], y);
+      y = fmaf(fmaf(B8 ? 0.f : -128.f, s, b), xsum[off >> 5], y);
       if constexpr (D < NC) __builtin_amdgcn_sched_barrier(0);  // keep the issue order
     }
     y += quad_xor1(y);

@@ -1,4 +1,4 @@
-// Instances of the one-row decode kernel for affine 2/3/5/6-bit weights at group size 64:
+// Instances of the one-row decode kernel for affine 2/3/5/6/8-bit weights at group size 64:
 // dense calls of one activation row, the same plan as the 4-bit instances.
 #include "qmv1_kernel.h"
 
@@ -10,6 +10,7 @@ hipError_t launch_qmv1_odd(const QmvParams& P, const Qmv1Plan& pl, int fpm, hipS
     case 103: qmv1_detail::launch_fmt<103>(P, pl, s); break;
     case 105: qmv1_detail::launch_fmt<105>(P, pl, s); break;
     case 106: qmv1_detail::launch_fmt<106>(P, pl, s); break;
+    case 108: qmv1_detail::launch_fmt<108>(P, pl, s); break;
     default: return hipErrorInvalidValue;
   }
   return hipSuccess;

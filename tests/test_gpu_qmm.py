@@ -92,10 +92,10 @@ def test_qmm_other_widths(dev, M, N, K, bits, gs):
     assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
 
 
-@pytest.mark.parametrize("bits", [2, 3, 5, 6])
+@pytest.mark.parametrize("bits", [2, 3, 5, 6, 8])
 @pytest.mark.parametrize("N,K", [(320, 14336), (64, 2176), (4096, 1024), (100, 4096)])
 def test_qmm_other_widths_one_row(dev, bits, N, K):
-    """One row of 2/3/5/6-bit gs 64 on the one-row streaming kernel's odd-width instances
+    """One row of 2/3/5/6/8-bit gs 64 on the one-row streaming kernel's other-width instances
     (K = 2176: 17 chunks, a K-split plan and the fixed-order reduce)."""
     _print_case(t="qmm_odd_one_row", bits=bits, N=N, K=K)
     wq, s, b = weights(1, N, K, bits, 64, 4000 + bits)
