@@ -79,6 +79,21 @@ MI_DEV u32x4_t fp8_run(uint32_t w0, uint32_t w1, float sc) {
   return r;
 }
 
+// 16 two-bit codes (LSB-first in d) -> bf16 pairs (128 + q) in natural order, codes 0..7 in
+// r0 and 8..15 in r1. Four masked shifts put codes k, k+4, k+8, k+12 in the bytes of one
+// word; v_perm pairs code 2p with code 2p+1 between zero bytes, and the OR adds the 0x43
+// high bytes (the same pairs as odd_run<2>, with fewer instructions).
+MI_DEV void two_bit_runs(uint32_t d, u32x4_t& r0, u32x4_t& r1) {
+  const uint32_t m = 0x03030303u, c43 = 0x43004300u;
+  const uint32_t a = d & m, b = (d >> 2) & m, c = (d >> 4) & m, e = (d >> 6) & m;
+  // [lo byte k, 0, hi byte k, 0]
+  auto pr = [&](uint32_t hi, uint32_t lo, uint32_t k) {
+    return perm_b32(hi, lo, 0x0C000C00u | k | ((4u + k) << 16)) | c43;
+  };
+  r0 = u32x4_t{pr(b, a, 0), pr(e, c, 0), pr(b, a, 1), pr(e, c, 1)};
+  r1 = u32x4_t{pr(b, a, 2), pr(e, c, 2), pr(b, a, 3), pr(e, c, 3)};
+}
+
 // 8 codes of `OB` bits (LSB-first, starting `sh` bits into the 64-bit pair d1:d0) ->
 // bf16 pairs (128 + q0, 128 + q1) .. (128 + q6, 128 + q7).
 template <int OB>

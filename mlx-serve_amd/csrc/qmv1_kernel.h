@@ -354,15 +354,32 @@ __global__ void __launch_bounds__(NC <= 8 ? 1024 : 512) qmv1_kernel(QmvParams P)
           return i == 0 ? L.wv[j].x : i == 1 ? L.wv[j].y : i == 2 ? L.wv[j].z : i == 3 ? L.wv[j].w
                  : i == 4 ? L.wv2[j].x : i == 5 ? L.wv2[j].y : 0u;
         };
+        if constexpr (OB == 2) {  // a dword is two runs
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int i = (t * OB) >> 2, sh = 8 * ((t * OB) & 3);
-          const u32x4_t a = code_runs::odd_run<OB>(dw(i), i + 1 < OB ? dw(i + 1) : 0u, sh);
-          const u32x4_t xv4 = xp[t];
-          acc = dot2(a.x, xv4.x, acc);
-          acc = dot2(a.y, xv4.y, acc);
-          acc = dot2(a.z, xv4.z, acc);
-          acc = dot2(a.w, xv4.w, acc);
+          for (int h = 0; h < 2; ++h) {
+            u32x4_t a0, a1;
+            code_runs::two_bit_runs(dw(h), a0, a1);
+            const u32x4_t x0 = xp[2 * h], x1 = xp[2 * h + 1];
+            acc = dot2(a0.x, x0.x, acc);
+            acc = dot2(a0.y, x0.y, acc);
+            acc = dot2(a0.z, x0.z, acc);
+            acc = dot2(a0.w, x0.w, acc);
+            acc = dot2(a1.x, x1.x, acc);
+            acc = dot2(a1.y, x1.y, acc);
+            acc = dot2(a1.z, x1.z, acc);
+            acc = dot2(a1.w, x1.w, acc);
+          }
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int i = (t * OB) >> 2, sh = 8 * ((t * OB) & 3);
+            const u32x4_t a = code_runs::odd_run<OB>(dw(i), i + 1 < OB ? dw(i + 1) : 0u, sh);
+            const u32x4_t xv4 = xp[t];
+            acc = dot2(a.x, xv4.x, acc);
+            acc = dot2(a.y, xv4.y, acc);
+            acc = dot2(a.z, xv4.z, acc);
+            acc = dot2(a.w, xv4.w, acc);
+          }
         }
       } else if constexpr (B8) {
         // codes 8t .. 8t+7 of the slice: two dwords of the lane's 32 bytes, each byte an
