@@ -754,12 +754,16 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   if (!y || !x || !w || !scales || !biases) return fail(MI_ERR_INVALID, "null tensor pointer");
   if (N > (int64_t)1 << 30 || M > (int64_t)1 << 30) return fail(MI_ERR_INVALID, "N or M too large");
   hipStream_t s = (hipStream_t)stream;
-  // M >= 256: dequantize once into the workspace and run a dense bf16 GEMM (the reference's
-  // prefillDqGemm shape, src/transformer.zig:20987-21011); below the threshold the fused
-  // dequant-in-register kernel is faster.
-  // 2/3/5/6-bit weights take this path at every M (no fused kernel for those widths).
-  // 4-bit weights at M >= MI_QMM_PREFILL_MIN (default 128): the fused prefill kernel
-  // (prefill.hip). Dequantize + hipBLASLt is opt-in (MI_QMM_DQGEMM=1) for 4/8 bits.
+  // Dispatch, in order:
+  //  - 4-bit weights at M >= MI_QMM_PREFILL_MIN (default 128): the fused prefill kernel
+  //    (prefill.hip), which replaces the reference's prefillDqGemm route
+  //    (src/transformer.zig:20987-21011) without a bf16 copy of the weight;
+  //  - one row of gs-64 2/3/5/6/8-bit weights: the one-row streaming kernel;
+  //  - 2/3/5/6 bits: the few-row MFMA kernel (2..32 rows, gs 64), qmv_any (up to
+  //    MI_QMM_ANY_MAX rows), else dequantize + hipBLASLt;
+  //  - 4/8 bits: the few-row MFMA kernel (up to 64 rows), else the fused qmm kernel.
+  //    Dequantize + hipBLASLt for 4/8 bits is opt-in (MI_QMM_DQGEMM=1, from
+  //    MI_QMM_DQGEMM_MIN rows).
   static const int dq_min = env_int("MI_QMM_DQGEMM_MIN", 256);
   static const int use_dqgemm = env_int("MI_QMM_DQGEMM", 0);
   static const int prefill_min = env_int("MI_QMM_PREFILL_MIN", 128);
