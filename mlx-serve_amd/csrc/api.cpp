@@ -888,9 +888,10 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   if (use_qmvm && qmvm_split && x_dtype == MI_DTYPE_BFLOAT16 && M > 32 && M <= split_max) {
     const int64_t mlast = M - 32 * ((M - 1) / 32);  // rows of the last launch
     mi::QmvmPlan q1{}, q2{};
-    // only when a 32-row launch fills the GPU by itself (on narrow shapes, e.g. the
-    // DeepSeek-V3 shared expert, it has 56..112 blocks and the split measured slower)
-    if (mi::qmvm_plan(32, (int)N, (int)K, gs, nb, 1, &q1) && q1.tiles * q1.ks >= 192 &&
+    // only when a 32-row launch fills the GPU by itself at 8 weight tiles a block (on
+    // narrow shapes, e.g. the DeepSeek-V3 shared expert, the 32-row plan needs fewer tiles
+    // a block to fill the GPU, and two such launches measured slower than one 64-row one)
+    if (mi::qmvm_plan(32, (int)N, (int)K, gs, nb, 1, &q1) && q1.wr >= 8 && q1.tiles * q1.ks >= 192 &&
         mi::qmvm_plan((int)mlast, (int)N, (int)K, gs, nb, 1, &q2)) {
       for (int64_t m0 = 0; m0 < M; m0 += 32) {
         const int64_t mc = std::min<int64_t>(32, M - m0);

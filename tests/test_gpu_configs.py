@@ -311,3 +311,19 @@ def test_config4_shared_expert_8bit(dev, T):
         truth = O.qmm_f64(bf16_bits(x), *host(*W), 64, 8)
         err = max_err_ratio(to_f64(y), truth)
         assert err <= BF16_TOL, (N, K, err)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [17, 32])
+@pytest.mark.parametrize("N,K", [(2048, 7168), (7168, 2048), (1536, 2048), (2048, 768)])
+def test_narrow_few_row_plans(dev, N, K, M, bits):
+    """17..32 rows on the MoE / shared-expert projection shapes of configs[3] and [4],
+    where the few-row plan walks down to 1 or 2 weight tiles per block: the whole output
+    against the oracle."""
+    _case(t="narrow_few_row", N=N, K=K, M=M, bits=bits)
+    W = dev_weight(dev, N, K, bits, seed(7, 1, N + K + bits))
+    x = dev_x(dev, M, K, seed(7, 0, M + N))
+    y = mi_qmm.quantized_matmul(x, *W, True, 64, bits)
+    truth = O.qmm_f64(bf16_bits(x), *host(*W), 64, bits)
+    err = max_err_ratio(to_f64(y), truth)
+    assert err <= BF16_TOL, (N, K, M, bits, err)
