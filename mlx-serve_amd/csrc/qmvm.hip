@@ -194,21 +194,21 @@ bool plan_impl(int M, int N, int K, int gs, int bits, int64_t n_items, int fpm, 
   const int wr0 = env_wr ? env_wr : M <= 2 ? 1 : M <= 16 ? 4 : M <= 32 ? 8 : 4;
   QmvmPlan best{};
   double best_cost = 1e30;
-  // Up to 16 rows, a plan under 192 blocks (narrow shapes: N = 2048 or 7168 at K = 7168 or
-  // 2048) also weighs fewer tiles per block: more blocks outweigh the extra activation reads
-  // there (configs[4] shared expert, 8-bit M=8: 27.7 us at one tile against 36.4 at four).
-  // At 17..32 rows the same walk takes the plan of the first tile count that reaches 192
-  // blocks (else the last, one tile): the cost model's K-split and chunk-count terms
-  // otherwise keep 8 tiles a block and leave most CUs idle (8-bit, 32 rows: [2048,7168]
-  // 14.5 -> 11.6 us at 2 tiles, [7168,2048] 13.0 -> 7.8, [1536,2048] 12.0 -> 6.2 and
-  // [2048,768] 8.6 -> 5.1 at one; wide shapes such as [14336,4096] keep their plan).
-  static const int narrow32 = env_or("MI_QMVM_NARROW32", 1);
+  // Up to 32 rows, a plan under 192 blocks (narrow shapes: N = 1536..7168 at K = 768..7168)
+  // walks down the tile counts and takes the plan of the first that reaches 192 blocks
+  // (else the last, one tile): more blocks outweigh the extra activation reads there, and
+  // the cost model's K-split and chunk-count terms alone keep too many tiles a block.
+  // Measured per launch, 8-bit: [2048,7168] 32 rows 14.5 -> 11.4 us (2 tiles), 16 rows
+  // 10.6 -> 9.6 (1 tile); [1536,2048] 32 rows 12.0 -> 6.2, 16 rows 7.5 -> 4.8 (1 tile);
+  // [7168,2048] 32 rows 13.0 -> 7.8 (2 tiles). Wide shapes such as [14336,4096] reach 192
+  // blocks at the first tile count and keep their plan.
+  static const int narrow = env_or("MI_QMVM_NARROW", 1);
   auto few_blocks = [&]() {
-    return (mt == 16 || (mt == 32 && narrow32)) && !env_wr &&
+    return mt <= 32 && narrow && !env_wr &&
            (int64_t)best.tiles * best.ks * std::max<int64_t>(1, n_items) < 192;
   };
   for (int wr = wr0; wr >= 1 && (!best.nc || few_blocks()); wr >>= 1) {
-    if (mt == 32 && best.nc) best_cost = 1e30;  // a plan found at this tile count replaces it
+    if (best.nc) best_cost = 1e30;  // a plan found at this tile count replaces it
     const int tiles = (N + 16 * wr - 1) / (16 * wr);
     for (int ks = 1; ks <= nch; ++ks) {
       if (nch % ks) continue;

@@ -314,10 +314,10 @@ def test_config4_shared_expert_8bit(dev, T):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("M", [17, 32])
+@pytest.mark.parametrize("M", [4, 8, 16, 17, 32])
 @pytest.mark.parametrize("N,K", [(2048, 7168), (7168, 2048), (1536, 2048), (2048, 768)])
 def test_narrow_few_row_plans(dev, N, K, M, bits):
-    """17..32 rows on the MoE / shared-expert projection shapes of configs[3] and [4],
+    """4..32 rows on the MoE / shared-expert projection shapes of configs[3] and [4],
     where the few-row plan walks down to 1 or 2 weight tiles per block: the whole output
     against the oracle."""
     _case(t="narrow_few_row", N=N, K=K, M=M, bits=bits)
