@@ -394,6 +394,8 @@ def main():
     ap.add_argument("--moe-only", type=int, default=0, choices=(0, 3, 4), metavar="CFG",
                     help="only run the MoE layer of configs[CFG] (3 or 4; for rocprofv3)")
     ap.add_argument("--tokens", type=int, default=0, help="T of --moe-only (default: all)")
+    ap.add_argument("--shared-only", type=int, default=0, metavar="T",
+                    help="time only configs[4]'s 8-bit shared expert at T tokens")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 4 device copies of 256 MiB (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes)")
@@ -431,6 +433,9 @@ def main():
     if args.prefill_only:
         print(json.dumps(prefill(torch, mi, dev, (args.prefill_only,), steps=args.steps,
                                  warmup=args.warmup)))
+        return
+    if args.shared_only:
+        print(json.dumps(shared_expert_8bit(torch, mi, dev, (args.shared_only,))))
         return
     if args.moe_only:
         if args.moe_only == 3:
