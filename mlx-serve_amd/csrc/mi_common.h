@@ -13,6 +13,24 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 MI_DEV float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
+// acc + p[r0*stride] + p[(r0+1)*stride] + ... + p[(ks-1)*stride], added in that order (the
+// fixed split order that keeps K-split results deterministic). The loads of U partials go
+// out before their adds, so their memory latencies overlap instead of adding up one
+// partial at a time (a runtime-count loop otherwise waits on each load before the next).
+template <int U, typename T>
+MI_DEV T add_splits(T acc, const T* __restrict__ p, int64_t stride, int r0, int ks) {
+  for (int r = r0; r < ks; r += U) {
+    T t[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (r + u < ks) t[u] = p[(int64_t)(r + u) * stride];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (r + u < ks) acc += t[u];
+  }
+  return acc;
+}
+
 // Round-to-nearest-even fp32 -> bf16 bits; NaN stays a quiet NaN.
 MI_DEV uint32_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);

@@ -291,8 +291,8 @@ __global__ void prefill_reduce_kernel(const float* __restrict__ part, uint16_t* 
                                       int64_t mn4, int ks) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn4;
        i += (int64_t)gridDim.x * blockDim.x) {
-    f32x4_t acc = reinterpret_cast<const f32x4_t*>(part)[i];
-    for (int s = 1; s < ks; ++s) acc += reinterpret_cast<const f32x4_t*>(part)[s * mn4 + i];
+    const f32x4_t* p4 = reinterpret_cast<const f32x4_t*>(part) + i;
+    const f32x4_t acc = add_splits<8>(p4[0], p4, mn4, 1, ks);
     u32x2_t o;
     o.x = pack_bf16x2(acc[0], acc[1]);
     o.y = pack_bf16x2(acc[2], acc[3]);

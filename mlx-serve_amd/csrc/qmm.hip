@@ -329,8 +329,7 @@ __global__ void qmm_reduce_kernel(const float* __restrict__ part, uint16_t* __re
                                   int64_t mn, int ks) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn;
        i += (int64_t)gridDim.x * blockDim.x) {
-    float acc = part[i];
-    for (int s = 1; s < ks; ++s) acc += part[(int64_t)s * mn + i];
+    const float acc = add_splits<8>(part[i], part + i, mn, 1, ks);
     y[i] = (uint16_t)f32_to_bf16_bits(acc);
   }
 }

@@ -355,8 +355,7 @@ __global__ void reduce_splits_kernel(QmvParams P) {
   const uint32_t total = PT * N;
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += gridDim.x * blockDim.x) {
-    float v = 0.f;
-    for (int k2 = 0; k2 < P.ks; ++k2) v += P.part[(size_t)k2 * total + i];
+    float v = add_splits<8>(0.f, P.part + i, (int64_t)total, 0, P.ks);
     const uint32_t p = i / N;
     const uint32_t pair = P.M == 1 ? p : p / (uint32_t)P.M;
     const uint32_t e = P.rhs ? P.rhs[pair] : pair;

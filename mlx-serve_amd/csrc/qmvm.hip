@@ -96,8 +96,7 @@ __global__ void qmvm_reduce_kernel(const float* __restrict__ part, uint16_t* __r
                                    int ks, int64_t mn) {
   const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (o >= mn) return;
-  float v = 0.f;
-  for (int r = 0; r < ks; ++r) v += part[(int64_t)r * mn + o];
+  const float v = add_splits<8>(0.f, part + o, mn, 0, ks);
   y[o] = (uint16_t)f32_to_bf16_bits(v);
 }
 
