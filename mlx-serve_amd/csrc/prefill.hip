@@ -5,22 +5,13 @@
 // copy in memory before a dense GEMM; here each weight tile is dequantized in registers on
 // its way into the matrix cores and never exists in bf16 outside them.
 //
-// Block: 256 (M) x 256 (N) outputs, 4 waves, one per SIMD. Wave w owns weight rows
-// [64w, 64w+64) of the tile (two 32-row MFMA tiles) against all 256 x rows (eight 32-row
-// tiles): 16 accumulators of v_mfma_f32_32x32x16_bf16, D[n][m] = W[n][k] x[m][k].
-// K advances in 64-wide steps through a 3-stage LDS ring. Every stage is filled by
-// buffer_load ... lds (no VGPR round trip): the 256 x 64 x tile (32 KB, 16-byte slots XOR-
-// swizzled by row so fragment reads are bank-conflict free), the 256 x 32 B packed weight
-// tile (8 KB) and one dword of scales and of biases per weight row.
-// Per 16-wide k-step a lane supplies 8 consecutive k of one weight row: word ks of the 16
-// packed bytes it owns (k in [32h, 32h+32) of the step, h = lane/32), dequantized as
+// Block: 256 (M) x 256 (N) outputs, 8 waves (two per SIMD), v_mfma_f32_32x32x16_bf16 with
+// D[n][m] = W[n][k] x[m][k]. Per 16-wide k-step a lane supplies 8 consecutive k of one
+// weight row (k in [32h, 32h+32) of the 64-wide step, h = lane/32), dequantized as
 // bf16(s*q + b): q from a scaled fp8 conversion, fma(s, q, b), one rounding to bf16 by
-// v_cvt_pk_bf16_f32, as MLX's GPU qmm rounds the weights it stages.
-// The x fragment of the same k-step is the natural 16-byte slot 4h+ks of the row.
-// One barrier per step, placed inside k-step 2 after the stage's last fragment reads: it
-// publishes the next stage (its DMA waited on with an exact vmcnt) and frees this one for
-// the DMA of step s+3. Loads past the last step repeat it, so the control flow is uniform
-// and the compiler's wait counts stay exact.
+// v_cvt_pk_bf16_f32, as MLX's GPU qmm rounds the weights it stages. The x fragment of the
+// same k-step is the 16-byte slot 4h+ks of the row. All staging is buffer_load ... lds DMA
+// (no VGPR round trip); the schedule is described at prefill_pp_kernel.
 #include <algorithm>
 #include <cstdlib>
 
@@ -34,13 +25,9 @@ namespace {
 using qmv_detail::mfma32;
 using qmv_detail::vmcnt_imm;
 
-constexpr int kBM = 256, kBN = 256, kBK = 64, kThreads = 256, kRing = 3;
+constexpr int kBM = 256, kBN = 256, kBK = 64, kRing = 3;
 constexpr int kXBytes = kBM * kBK * 2;  // x tile: 256 rows x 128 B
-constexpr int kWBytes = kBN * kBK / 2;  // packed 4-bit tile: 256 rows x 32 B
-constexpr int kSBytes = kBN * 4;        // one dword of scales (or biases) per row
-constexpr int kStage = kXBytes + kWBytes + 2 * kSBytes;
 constexpr int kBufFlags = 0x00020000;   // raw dword access
-constexpr int kLoadsPerStep = 12;       // DMA instructions per thread per step
 
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -73,28 +60,66 @@ MI_DEV u32x4_t dequant8(uint32_t w, float s, float b) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds((rsrc), (__attribute__((address_space(3))) void*)(lds), \
                                            SIZE, (voff), (soff), 0, 0)
 
-// Scale dword of step st: the dword holding group g = (64 st + 32 h) / GS of the row.
-template <int GS>
-MI_DEV uint32_t sb_dword(int st) {
-  return GS == 32 ? 4u * st : GS == 64 ? 4u * (st >> 1) : 4u * (st >> 2);
-}
-template <int GS>
-MI_DEV bool sb_high(int st, int h) {
-  return GS == 32 ? h != 0 : GS == 64 ? (st & 1) != 0 : ((st >> 1) & 1) != 0;
+// Ping-pong variant: 8 waves, two per SIMD. Wave w owns weight rows [32w, 32w + 32) (one
+// 32-row tile) against all 256 x rows (eight 32-row tiles): 8 accumulators (128
+// registers), so two waves fit a SIMD, and every weight of the block is dequantized by
+// exactly one wave. (VALU work issued beside another wave's MFMAs delays them, so the
+// dequantize count per MFMA is what this layout minimizes; the price is one 1 KB x
+// fragment read per MFMA, half the LDS read bandwidth of a CU.) Each wave's work on a
+// 64-wide step is two units: "mem" (its packed weights, scales and biases from LDS,
+// dequantized to the 16 bf16 operand registers of the whole step, and the first x
+// fragments) and "mfma" (the step's 32 MFMAs, the remaining x fragments read as they go).
+// The two groups run the same units half a step apart on staggered barriers: while group
+// 0 issues the matrix ops of step t, group 1 dequantizes step t, then the roles swap, so
+// each SIMD always has one wave feeding the matrix core and one doing the VALU/LDS work.
+// Timeline of half-steps h (a block barrier after each):
+//   h = 2t:    group 0 mem(t),     group 1 mfma(t-1)
+//   h = 2t+1:  group 0 mfma(t),    group 1 mem(t);  every wave issues the DMA of step t+2
+//
+// Staging is shaped by the number of memory requests, not bytes: the DMA path serves a
+// bounded number of requests per CU per cycle, and a request per 4-byte scale was the
+// largest cost. So LDS holds
+//   - x: a 3-stage ring of 256 x 64 tiles (32 KB each; 128-byte rows, one request each),
+//   - packed weights: 2 buffers of 2-step chunks (256 rows x 64 B: one request per row
+//     per two steps, against one per step for 32-byte rows),
+//   - scales and biases: 2 buffers of 8-group chunks (256 rows x 16 B each, moved as
+//     4 dwords per row: one request per row per 8 groups).
+// A chunk goes out with the x tile of its first step and lands one step ahead of use.
+// Step t's x stage is last read in half 2t+2; the DMA that reuses it (step t+3) goes out
+// in half 2t+3. Each wave waits (exact vmcnt) at the end of half 2t+1 for everything
+// issued before the DMA of step t+2, so the barrier publishes step t+1 before group 0
+// reads it in half 2t+2. The weight and scale buffers are reused two chunks later, after
+// the last read of the chunk they held.
+constexpr int kPPThreads = 512;
+constexpr int kPPXStage = kXBytes;                   // 32 KB
+constexpr int kPPWChunk = kBN * 64;                  // 256 rows x 64 B
+constexpr int kPPSChunk = kBN * 16;                  // 256 rows x 16 B (scales or biases)
+constexpr int kPPWOff = kRing * kPPXStage;           // 96 KB
+constexpr int kPPSOff = kPPWOff + 2 * kPPWChunk;     // 128 KB
+constexpr int kPPLds = kPPSOff + 4 * kPPSChunk;      // 144 KB
+
+MI_DEV void wait_vm(int n) {  // s_waitcnt vmcnt(n) for the counts one step can issue
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4)); break;
+    case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6)); break;
+    case 8: __builtin_amdgcn_s_waitcnt(vmcnt_imm(8)); break;
+    default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(10)); break;
+  }
 }
 
-// SPLIT: this block covers K steps [split * sps, +sps) and writes fp32 partials.
 template <int GS, bool SPLIT>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
-prefill_kernel(PrefillParams P) {
+__global__ void __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+prefill_pp_kernel(PrefillParams P) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  // steps per scale chunk (8 groups): 4, 8 or 16
+  constexpr int kSP = GS / 8;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, nq = wave & 3;
   const int fr = lane & 31, h = lane >> 5;
   const int M = P.M, N = P.N, K = P.K, G = K / GS;
   const int mtiles = (M + kBM - 1) / kBM;
-  // Consecutive blocks land on different XCDs: walking M fastest gives each XCD a fixed
-  // set of x tiles while the weight tiles stream past.
   const int mt = blockIdx.x % mtiles, nt = blockIdx.x / mtiles;
   const int m0 = mt * kBM, n0 = nt * kBN;
   const int split = blockIdx.y;
@@ -102,187 +127,165 @@ prefill_kernel(PrefillParams P) {
   const int nsteps = min(P.sps, K / kBK - s0);
   const int mrows = min(kBM, M - m0), nrows = min(kBN, N - n0);
 
-  // Buffer resources based at the block's first rows; reads past them return 0.
   const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(P.x + (size_t)m0 * K), 0, mrows * K * 2, kBufFlags);
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
       (void*)((const unsigned char*)P.w + (size_t)n0 * (K / 2)), 0, nrows * (K / 2), kBufFlags);
-  const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(P.scales + (size_t)n0 * G), 0, nrows * G * 2, kBufFlags);
-  const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(P.biases + (size_t)n0 * G), 0, nrows * G * 2, kBufFlags);
-  // x: wave w moves tile rows 64w..64w+63 as 8 instructions of 8 rows x 128 B; LDS slot p
+  // group 0 moves the scales, group 1 the biases
+  const __amdgpu_buffer_rsrc_t sbres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((grp ? P.biases : P.scales) + (size_t)n0 * G), 0, nrows * G * 2, kBufFlags);
+  // x: wave w moves tile rows 32w..32w+31 as 4 instructions of 8 rows x 128 B; LDS slot p
   // of row r holds k-slot p ^ ((r >> 1) & 7).
-  uint32_t xo[8];
+  uint32_t xo[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = 64 * wave + 8 * i + (lane >> 3);
+  for (int i = 0; i < 4; ++i) {
+    const int r = 32 * wave + 8 * i + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     xo[i] = (uint32_t)(min(r, mrows - 1) * K + 8 * c) * 2;
   }
-  // packed w: wave w moves rows 64w..64w+63 as 2 instructions of 32 rows x 32 B; LDS half
-  // p of row r holds 16-byte half p ^ ((r >> 3) & 1).
+  // packed-weight chunk: wave w moves rows 32w..32w+31 as 2 instructions of 16 rows x 64 B;
+  // LDS part p (16 B) of row r holds part p ^ ((r >> 2) & 3) of the row's 64 bytes.
   uint32_t wo[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int r = 64 * wave + 32 * i + (lane >> 1);
-    const int c = (lane & 1) ^ ((r >> 3) & 1);
+    const int r = 32 * wave + 16 * i + (lane >> 2);
+    const int c = (lane & 3) ^ ((r >> 2) & 3);
     wo[i] = (uint32_t)(min(r, nrows - 1) * (K / 2) + 16 * c);
   }
-  const uint32_t so = (uint32_t)min(64 * wave + lane, nrows - 1) * G * 2;
-  auto issue = [&](int st, int stg) {
-    unsigned char* base = smem + stg * kStage;
+  // scale (group 0) or bias (group 1) chunk: wave moves rows 64nq..64nq+63 as 4
+  // instructions of 16 rows x 4 dwords; row-major 16 B per row in LDS.
+  uint32_t so[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 64 * nq + 16 * i + (lane >> 2);
+    so[i] = (uint32_t)(min(r, nrows - 1) * G * 2 + 4 * (lane & 3));
+  }
+  // DMA of local step st (x; the weight chunk when st is even; the scale chunk when st
+  // starts one). Returns the instructions issued (0 past the last step).
+  auto issue = [&](int st) -> int {
+    if (st >= nsteps) return 0;
     const int k = s0 + st;
+    unsigned char* xb = smem + (st % kRing) * kPPXStage;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      MI_DMA_LDS(16, xres, base + 64 * wave * 128 + i * 1024, xo[i], k * kBK * 2);
+    for (int i = 0; i < 4; ++i)
+      MI_DMA_LDS(16, xres, xb + wave * 4096 + i * 1024, xo[i], k * kBK * 2);
+    int n = 4;
+    if ((st & 1) == 0) {
+      unsigned char* wb = smem + kPPWOff + ((st >> 1) & 1) * kPPWChunk;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      MI_DMA_LDS(16, wres, base + kXBytes + 64 * wave * 32 + i * 1024, wo[i], k * (kBK / 2));
-    MI_DMA_LDS(4, sres, base + kXBytes + kWBytes + 256 * wave, so, sb_dword<GS>(k));
-    MI_DMA_LDS(4, bres, base + kXBytes + kWBytes + kSBytes + 256 * wave, so, sb_dword<GS>(k));
+      for (int i = 0; i < 2; ++i)
+        MI_DMA_LDS(16, wres, wb + wave * 2048 + i * 1024, wo[i], k * (kBK / 2));
+      n += 2;
+    }
+    if (st == 0 || k % kSP == 0) {
+      const int c = k / kSP;
+      unsigned char* sb = smem + kPPSOff + (c & 1) * 2 * kPPSChunk + grp * kPPSChunk;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        MI_DMA_LDS(4, sbres, sb + nq * 1024 + i * 256, so[i], c * 16);
+      n += 4;
+    }
+    return n;
   };
 
-  f32x16_t acc[8][2];
+  f32x16_t acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+  // The accumulators go to AGPRs (the clobber makes AGPRs available to the allocator),
+  // so the MFMA C/D traffic stays out of the VGPR file the other wave's VALU work uses.
+  asm volatile("" ::: "a0");
 
-  // x fragment: tile row 32i + fr, k-slot 4h + ks of the stage.
+  // x fragment of tile i: row 32 i + fr, k-slot 4h + ks.
   auto xfrag = [&](int stg, int i, int ks) -> u32x4_t {
     const int r = 32 * i + fr, c = 4 * h + ks;
-    return *reinterpret_cast<const u32x4_t*>(smem + stg * kStage + r * 128 +
+    return *reinterpret_cast<const u32x4_t*>(smem + stg * kPPXStage + r * 128 +
                                              ((c ^ ((r >> 1) & 7)) << 4));
   };
-  struct WStep {
-    u32x4_t q[2];
-    uint32_t s[2], b[2];
-  };
-  // This wave's packed words and scale/bias dwords of weight rows 64w + 32j + fr.
-  auto wread = [&](int stg, WStep& o) {
-    const unsigned char* base = smem + stg * kStage + kXBytes;
+  u32x4_t A[4], X[2][8];
+  auto mem = [&](int st) {
+    const int k = s0 + st;
+    const unsigned char* wb = smem + kPPWOff + ((st >> 1) & 1) * kPPWChunk;
+    const unsigned char* sb = smem + kPPSOff + ((k / kSP) & 1) * 2 * kPPSChunk;
+    // group of this lane's 32 k within the chunk's 8
+    const int gi = GS == 32 ? 2 * (k % 4) + h : GS == 64 ? k % 8 : (k >> 1) % 8;
+    const int part = 2 * (st & 1) + h;
+    const int r = 32 * wave + fr;
+    const u32x4_t q =
+        *reinterpret_cast<const u32x4_t*>(wb + r * 64 + ((part ^ ((r >> 2) & 3)) << 4));
+    const uint16_t sv = *reinterpret_cast<const uint16_t*>(sb + r * 16 + 2 * gi);
+    const uint16_t bv = *reinterpret_cast<const uint16_t*>(sb + kPPSChunk + r * 16 + 2 * gi);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int r = 64 * wave + 32 * j + fr;
-      o.q[j] = *reinterpret_cast<const u32x4_t*>(base + r * 32 + ((h ^ ((r >> 3) & 1)) << 4));
-      o.s[j] = *reinterpret_cast<const uint32_t*>(base + kWBytes + 4 * r);
-      o.b[j] = *reinterpret_cast<const uint32_t*>(base + kWBytes + kSBytes + 4 * r);
-    }
-  };
-  float sc[2], bp[2];
-  auto scales_of = [&](const WStep& w, int st) {
-    const bool hi = sb_high<GS>(s0 + st, h);
+    for (int i = 0; i < 8; ++i) X[0][i] = xfrag(st % kRing, i, 0);
+    const float sc = __uint_as_float((uint32_t)sv << 16);
+    const float bp = __uint_as_float((uint32_t)bv << 16);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      sc[j] = __uint_as_float(hi ? (w.s[j] & 0xFFFF0000u) : (w.s[j] << 16));
-      bp[j] = __uint_as_float(hi ? (w.b[j] & 0xFFFF0000u) : (w.b[j] << 16));
+    for (int ks = 0; ks < 4; ++ks) A[ks] = dequant8(q[ks], sc, bp);
+  };
+  auto mfma = [&](int st) {
+    const int stg = st % kRing;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (ks < 3) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) X[(ks + 1) & 1][i] = xfrag(stg, i, ks + 1);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = mfma32(A[ks], X[ks & 1][i], acc[i]);
+      // the next k-step's fragment reads go out ahead of this k-step's MFMAs, one read
+      // per MFMA, so their latency hides under the matrix work
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        if (ks < 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // prologue: steps 0..2 in flight, step 0 published
-  issue(0, 0);
-  issue(min(1, nsteps - 1), 1);
-  issue(min(2, nsteps - 1), 2);
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kLoadsPerStep));
+  // Both groups run the same unit sequence mem(t), mfma(t) with a barrier after each unit;
+  // group 1 starts one half later (an extra barrier first), group 0 ends with an extra
+  // barrier, so the barrier counts match. The DMA of step t+2 goes out in half 2t+1 for
+  // both groups: after group 0's mfma(t) unit and after group 1's mem(t) unit.
+  issue(0);
+  wait_vm(issue(1));
   __builtin_amdgcn_s_barrier();
-  u32x4_t xb[2][8], a[2][2];
-  WStep wc, wn;
-  wread(0, wc);
-  scales_of(wc, 0);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) xb[0][i] = xfrag(0, i, 0);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) a[0][j] = dequant8(wc.q[j][0], sc[j], bp[j]);
-
-  auto mfmas = [&](int cur) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(a[cur][j], xb[cur][i], acc[i][j]);
-  };
-  // Interleave: one LDS read and three VALU ops (next k-step's operands) per MFMA.
-  auto interleave = [&](int nds) {
-#pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      if (m < nds) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-    }
+  if (grp) __builtin_amdgcn_s_barrier();
+  for (int t = 0; t < nsteps; ++t) {
+    mem(t);
     __builtin_amdgcn_sched_barrier(0);
-  };
-  auto step = [&](int st, int stage) {
-    const int ns = stage == kRing - 1 ? 0 : stage + 1;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int cur = ks & 1, nxt = cur ^ 1;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xb[nxt][i] = xfrag(stage, i, ks + 1);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) a[nxt][j] = dequant8(wc.q[j][ks + 1], sc[j], bp[j]);
-      mfmas(cur);
-      interleave(8);
-    }
-    {  // k-step 2: last fragments of this stage, barrier, DMA of step st+3, W of step st+1
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xb[1][i] = xfrag(stage, i, 3);
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLoadsPerStep));
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-      __builtin_amdgcn_s_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-      issue(min(st + 3, nsteps - 1), stage);
-      wread(ns, wn);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) a[1][j] = dequant8(wc.q[j][3], sc[j], bp[j]);
-      mfmas(0);
-      interleave(6);
-    }
-    {  // k-step 3: first fragments and operands of step st+1
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xb[0][i] = xfrag(ns, i, 0);
-      scales_of(wn, st + 1);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) a[0][j] = dequant8(wn.q[j][0], sc[j], bp[j]);
-      mfmas(1);
-      interleave(8);
-      wc = wn;
-    }
-  };
-  int st = 0;
-  for (; st + 3 <= nsteps; st += 3) {
-    step(st, 0);
-    step(st + 1, 1);
-    step(st + 2, 2);
+    if (grp) wait_vm(issue(t + 2));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    mfma(t);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!grp) wait_vm(issue(t + 2));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
   }
-  if (st < nsteps) step(st, 0);
-  if (st + 1 < nsteps) step(st + 1, 1);
+  if (!grp) __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no DMA may outlive the block
 
-  // epilogue: acc[i][j] register r is D[n = 8(r/4) + 4h + r%4][m = fr] of tile (i, j)
+  // epilogue: acc[i] register r is D[n = 32 wave + 8(r/4) + 4h + r%4][m = 32 i + fr]
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int m = m0 + 32 * i + fr;
     if (m >= M) continue;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + 64 * wave + 32 * j + 8 * g + 4 * h;
-        if (n >= N) continue;
-        if constexpr (SPLIT) {
-          f32x4_t v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                       acc[i][j][4 * g + 3]};
-          *reinterpret_cast<f32x4_t*>(P.part + ((size_t)split * M + m) * N + n) = v;
-        } else {
-          u32x2_t o;
-          o.x = pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]);
-          o.y = pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-          *reinterpret_cast<u32x2_t*>(P.y + (size_t)m * N + n) = o;
-        }
+    for (int g = 0; g < 4; ++g) {
+      const int n = n0 + 32 * wave + 8 * g + 4 * h;
+      if (n >= N) continue;
+      if constexpr (SPLIT) {
+        f32x4_t v = {acc[i][4 * g], acc[i][4 * g + 1], acc[i][4 * g + 2], acc[i][4 * g + 3]};
+        *reinterpret_cast<f32x4_t*>(P.part + ((size_t)split * M + m) * N + n) = v;
+      } else {
+        u32x2_t o;
+        o.x = pack_bf16x2(acc[i][4 * g], acc[i][4 * g + 1]);
+        o.y = pack_bf16x2(acc[i][4 * g + 2], acc[i][4 * g + 3]);
+        *reinterpret_cast<u32x2_t*>(P.y + (size_t)m * N + n) = o;
       }
+    }
   }
 }
 
@@ -300,24 +303,27 @@ __global__ void prefill_reduce_kernel(const float* __restrict__ part, uint16_t* 
   }
 }
 
+template <typename Kern>
+hipError_t set_lds(Kern k, size_t lds) {
+  return hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+}
+
 template <int GS>
 hipError_t launch_gs(const PrefillParams& P, hipStream_t s) {
   const int mtiles = (P.M + kBM - 1) / kBM, ntiles = (P.N + kBN - 1) / kBN;
-  const size_t lds = (size_t)kRing * kStage;
   static bool attr = false;
   if (!attr) {
-    for (auto k : {prefill_kernel<GS, true>, prefill_kernel<GS, false>}) {
-      hipError_t e =
-          hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return e;
-    }
+    hipError_t e = hipSuccess;
+    for (auto k : {prefill_pp_kernel<GS, true>, prefill_pp_kernel<GS, false>})
+      if (e == hipSuccess) e = set_lds(k, kPPLds);
+    if (e != hipSuccess) return e;
     attr = true;
   }
   const dim3 grid((unsigned)(mtiles * ntiles), (unsigned)P.ks);
   if (P.ks > 1)
-    hipLaunchKernelGGL((prefill_kernel<GS, true>), grid, dim3(kThreads), lds, s, P);
+    hipLaunchKernelGGL((prefill_pp_kernel<GS, true>), grid, dim3(kPPThreads), kPPLds, s, P);
   else
-    hipLaunchKernelGGL((prefill_kernel<GS, false>), grid, dim3(kThreads), lds, s, P);
+    hipLaunchKernelGGL((prefill_pp_kernel<GS, false>), grid, dim3(kPPThreads), kPPLds, s, P);
   return hipGetLastError();
 }
 
@@ -325,8 +331,10 @@ hipError_t launch_gs(const PrefillParams& P, hipStream_t s) {
 
 bool prefill_supported(int64_t M, int64_t N, int64_t K, int bits, int gs) {
   if (bits != 4 || (gs != 32 && gs != 64 && gs != 128)) return false;
-  // 32-bit buffer offsets per block; 4-output stores; whole 64-wide steps and groups
-  return M >= 1 && N >= 4 && N % 4 == 0 && K % kBK == 0 && K % gs == 0 &&
+  // 32-bit buffer offsets per block; 4-output stores; whole 64-wide steps and groups; an
+  // even group count, so every row's scales and biases start on a dword (the staging
+  // moves them as dwords)
+  return M >= 1 && N >= 4 && N % 4 == 0 && K % kBK == 0 && K % gs == 0 && (K / gs) % 2 == 0 &&
          (int64_t)kBM * K * 2 < ((int64_t)1 << 31) && (int64_t)kBN * K < ((int64_t)1 << 31) &&
          M < ((int64_t)1 << 30) && N < ((int64_t)1 << 30);
 }

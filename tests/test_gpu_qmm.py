@@ -336,6 +336,20 @@ def test_prefill_qmm(dev, M, N, K, bits, gs):
     assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
 
 
+@pytest.mark.parametrize("M,N,K,gs", [(256, 260, 960, 64), (300, 300, 1152, 128)])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_prefill_odd_group_count(dev, M, N, K, gs, bits):
+    """Odd group counts per row (K/gs = 15, 9): a row's scales then do not start on a
+    dword, so the 4-bit prefill kernel hands these shapes to another route."""
+    _print_case(t="prefill_odd_g", M=M, N=N, K=K, bits=bits, gs=gs)
+    wq, s, b = weights(1, N, K, bits, gs, 5100 + M)
+    x = O.make_x_bf16(M, K, 6100 + N)
+    y = mi_qmm.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(wq[0], dev),
+                                to_dev_bf16(s[0], dev), to_dev_bf16(b[0], dev), True, gs, bits)
+    truth = O.qmm_f64(x, wq[0], s[0], b[0], gs, bits)
+    assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+
+
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
 def test_prefill_full_size_sampled_rows(dev, N, K):
     """configs[2] shapes at M=2048: 48 sampled output rows against the oracle, and the
