@@ -15,7 +15,7 @@ BUILD = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HOST = os.path.join(HERE, "host")
 ROOT = os.path.dirname(HERE)
-SOURCES = ["csrc/qmv1_g64.hip", "csrc/qmv1_g32.hip", "csrc/qmv1_g128.hip", "csrc/qmv1.hip", "csrc/qmv1_fp.hip", "csrc/qmv1_odd.hip", "csrc/qmvm.hip", "csrc/qmvm_gather.hip", "csrc/qmvm_b8.hip", "csrc/qmvm_m64.hip", "csrc/qmvm_fp.hip", "csrc/qmvm_w2.hip", "csrc/qmvm_w3.hip", "csrc/qmvm_w5.hip", "csrc/qmvm_w6.hip", "csrc/qmvm_fp_gather.hip", "csrc/qmv.hip", "csrc/qmv16.hip", "csrc/qmm.hip", "csrc/prefill.hip", "csrc/quant.hip", "csrc/moe.hip", "csrc/moe_down.hip", "csrc/qmv_any.hip",
+SOURCES = ["csrc/qmv1_g64.hip", "csrc/qmv1_g32.hip", "csrc/qmv1_g128.hip", "csrc/qmv1.hip", "csrc/qmv1_fp.hip", "csrc/qmv1_odd.hip", "csrc/qmvm.hip", "csrc/qmvm_gather.hip", "csrc/qmvm_b8.hip", "csrc/qmvm_m64.hip", "csrc/qmvm_fp.hip", "csrc/qmvm_w2.hip", "csrc/qmvm_w3.hip", "csrc/qmvm_w5.hip", "csrc/qmvm_w6.hip", "csrc/qmvm_fp_gather.hip", "csrc/qmv.hip", "csrc/qmv16.hip", "csrc/qmm.hip", "csrc/prefill.hip", "csrc/gmm.hip", "csrc/quant.hip", "csrc/moe.hip", "csrc/moe_down.hip", "csrc/qmv_any.hip",
            "csrc/blas.cpp", "csrc/api.cpp", "host/mi_host.cpp", "host/mi_ckpt.cpp"]
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

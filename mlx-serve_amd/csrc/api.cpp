@@ -263,6 +263,8 @@ struct GatherJob {
   mi::Qmv1Plan plan1{};
   mi::QmvmPlan planm{};
   bool empty = false, narrow = false, use_items = false, one_row = false, multi_row = false;
+  bool grouped = false;  // sorted runs on the grouped kernel (gmm.hip)
+  int gmm_mt = 0;        // its 32-row tiles per item
   int64_t max_items = 0;
   size_t items_bytes = 0, part_bytes = 0;
   size_t items_region() const { return ((items_bytes + 255) / 256) * 256; }
@@ -336,12 +338,32 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
       if (mu > 1.3) avg = std::max<int64_t>(avg, (int64_t)std::ceil(mu + 3.0 * std::sqrt(mu)));
     }
     if (item_rows > 0) avg = item_rows;
+    // Runs that average several rows per distinct expert go to the grouped kernel: one
+    // block per (item, 128-row weight tile) streams the tile once for all the item's rows
+    // (up to 32 * MT), in-register dequantize into 32x32x16 MFMAs. Items are sized for
+    // mu + 3 sigma rows as above, so a run is rarely cut.
+    static const int use_gmm = env_int("MI_QMM_GMM", 1);
+    static const int gmm_min = env_int("MI_QMM_GMM_MIN_ROWS", 4);
+    if (use_gmm && item_rows <= 0 &&
+        mi::gmm_supported(P.N, P.K, nb, gs, P.x_f32, x_batch * M * K * 2)) {
+      const double e = (double)n_experts, distinct = e * (1.0 - std::pow(1.0 - 1.0 / e, (double)PT));
+      const double mu = distinct > 0 ? (double)PT / distinct : 1.0;
+      if (mu >= gmm_min) {
+        const double want = mu + 3.0 * std::sqrt(mu);
+        J.grouped = true;
+        J.gmm_mt = want <= 32 ? 1 : 2;  // longer runs are cut into 64-row items
+      }
+    }
     J.narrow = q16 && avg <= 4;
     // (64-row items on the two-pass few-row kernel measured slower than 32-row items
     // that re-read a long run's expert: with a K split at K = 2048, and also at K = 768
     // without one, configs[3] T=512 391 against 293 us per layer)
     P.rpi = avg <= 1 ? 1 : avg <= 2 ? 2 : avg <= 4 ? 4 : avg <= 8 ? 8 : avg <= 16 ? 16 : 32;
     if (!J.narrow && P.rpi < 8) P.rpi = 8;
+    if (J.grouped) {
+      J.narrow = false;
+      P.rpi = 32 * J.gmm_mt;
+    }
   } else {
     J.narrow = M <= narrow_max && q16;
     P.rpi = J.narrow ? 16 : 32;
@@ -364,6 +386,13 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
   // Items of exactly one activation row (dense M == 1, MoE decode pairs, sorted runs cut
   // into single rows) stream through the one-row kernel when it supports the layout.
   static const int use_qmv1 = env_int("MI_QMM_QMV1", 1);
+  if (J.grouped) {
+    P.ks = 1;
+    J.plan.cfg.grid_z = (int)(n_items < 65535 ? n_items : 65535);
+    J.items_bytes = (size_t)J.max_items * 16 + 256;
+    J.part_bytes = 0;
+    return MI_OK;
+  }
   J.one_row = use_qmv1 && ((J.use_items && P.rpi == 1) || (!J.use_items && M == 1));
   J.one_row = J.one_row && mi::qmv1_supported(P.N, P.K, gs, nb, P.x_f32);
   if (J.one_row) {
@@ -487,7 +516,8 @@ int gather_launch(GatherJob& J, void* ws, hipStream_t s) {
       P.item_count = count;
     }
   }
-  hipError_t e = J.one_row     ? mi::launch_qmv1(P, J.plan1, J.plan.cfg.grid_z, s)
+  hipError_t e = J.grouped     ? mi::launch_gmm(P, J.gmm_mt, J.plan.cfg.grid_z, s)
+                 : J.one_row   ? mi::launch_qmv1(P, J.plan1, J.plan.cfg.grid_z, s)
                  : J.multi_row ? mi::launch_qmvm_gather(P, J.planm, J.plan.cfg.grid_z, s)
                  : J.narrow    ? mi::launch_qmv16(P, J.plan.cfg, s)
                                : mi::launch_qmv(P, J.plan.cfg, s);

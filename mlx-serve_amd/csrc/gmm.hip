@@ -1,0 +1,267 @@
+// Grouped quantized GEMM over expert-sorted work items: the sorted gather_qmm of an MoE
+// prefill (reference: the three gather_qmm(sorted_indices = true) calls over expert
+// segments in src/transformer.zig:14961-15043, gather at :15011), 4-bit affine weights,
+// group size 64, bf16 activations.
+//
+// A work item is a run of sorted pairs with one expert, cut at 32*MT rows (build_items in
+// quant.hip). One block = one item x one 32*WV-row tile of the expert's weight: it streams
+// that weight tile from HBM exactly once and multiplies it by all the item's rows, so an
+// expert with up to 32*MT rows is read once per call whatever its segment length.
+//
+// Block: WV waves; wave w owns weight rows n0 + 32w .. +31 (one 32-row MFMA tile) against
+// the item's 32*MT rows (MT tiles) of v_mfma_f32_32x32x16_bf16, D[n][m] = W[n][k] x[m][k],
+// with two accumulator sets (even / odd k-steps) so consecutive MFMAs are independent.
+// Per 64-wide step a lane (fr = lane % 32, h = lane / 32) holds 16 packed bytes of its
+// weight row (k in [32h, 32h+32)), dequantized in registers as bf16(s*q + b)
+// (dq::dequant8: no all-ones MFMA and no per-group epilogue); the x fragment of k-step ks
+// is the 16-byte slot 4h+ks of the row.
+// Pipeline, kD steps deep: a step's weight bytes go to a register ring, its gathered x rows
+// to an LDS ring by buffer_load ... lds DMA (rows past the item's end read past the end of
+// x: zeros, no memory traffic), and every 4 steps each lane loads 8 bytes (4 groups) of its
+// row's scales (h = 0) or biases (h = 1), shared across the lane halves by a permlane swap.
+// The loads of step t are issued kD - 1 steps ahead, the x DMA last, so before step t an
+// exact vmcnt (the younger steps' loads only) publishes its x tile; the barrier waits on
+// LDS traffic only. Chunked scale loads matter: one 2-byte load per lane per step made the
+// L2 serve ~7.8 M requests per 113 MB projection and cost 10%.
+#include <algorithm>
+
+#include "dequant_bf16.h"
+#include "mi_common.h"
+#include "mi_internal.h"
+#include "qmv_common.h"
+
+namespace mi {
+namespace {
+
+using dq::dequant8;
+using dq::pack_bf16x2;
+using qmv_detail::decode_item;
+using qmv_detail::Item;
+using qmv_detail::item_x_row;
+using qmv_detail::mfma32;
+using qmv_detail::vmcnt_imm;
+
+constexpr int kOOB = 0x7FFFFFF0;  // buffer offset past any x: the load returns 0, no traffic
+constexpr int kD = 8;        // steps in flight: LDS ring of x tiles, register ring of weights
+constexpr int kBufFlags = 0x00020000;
+
+MI_DEV u32x4_t ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4_t,
+                            __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+// 16 bytes per lane from the buffer into LDS at lds + 16 * lane (LDS DMA)
+MI_DEV void dma16(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                           (int)voff, (int)soff, 0, 0);
+}
+MI_DEV u32x2_t ld8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
+
+MI_DEV uint32_t xor32_u32(uint32_t v, int lane) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (lane & 32) ? r[0] : r[1];
+}
+
+template <int MT, int WV>
+__global__ void __launch_bounds__(64 * WV, 8 / WV) gmm_kernel(QmvParams P) {
+  constexpr int R = 32 * MT, kNT = 32 * WV, kThreads = 64 * WV;
+  // x DMA instructions per thread per step: R rows x 128 B over kThreads lanes x 16 B
+  constexpr int XU = R * 8 / kThreads;
+  static_assert(XU >= 1 && XU * kThreads == R * 8, "x tile must split evenly over the lanes");
+  constexpr int kN = XU + 1;  // VMEM instructions per step: x DMA and weights (+1 per chunk)
+  // Dynamic LDS: the x ring (kD stages of R rows x 128 B), then the row table. (With a
+  // static array the compiler would drain every load before each LDS read that may alias
+  // an LDS DMA; the waits here are exact and explicit.)
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int kStage = R * 128;
+  int64_t* rowtab = reinterpret_cast<int64_t*>(smem + kD * kStage);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 31, h = lane >> 5;
+  const int N = P.N, K = P.K, G = K / 64, nsteps = K / 64;
+  const int n0 = blockIdx.x * kNT;
+  const int n_items = (int)*P.item_count;
+  const uint32_t wrow = (uint32_t)min(n0 + 32 * wave + fr, N - 1);
+  const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)P.x, 0, (int)(uint32_t)(P.x_batch * P.M * (int64_t)K * 2), kBufFlags);
+
+  for (int it_i = blockIdx.y; it_i < n_items; it_i += gridDim.y) {
+    const Item it = decode_item(P, it_i);
+    if (it.cnt <= 0) continue;  // block-uniform
+    const uint32_t e = __builtin_amdgcn_readfirstlane(it.expert_ok ? it.expert : 0u);
+    const bool eok = it.expert_ok;
+    if (tid < R) rowtab[tid] = item_x_row(P, it, tid);  // -1 skip, -2 NaN
+    __syncthreads();
+
+    const size_t mat = (size_t)e * (uint32_t)N;
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.w + mat * (uint32_t)(K / 8)), 0, N * (K / 2), kBufFlags);
+    const uint32_t wo = wrow * (uint32_t)(K / 2) + 16 * h;
+    // lane h = 0 loads its row's scales, h = 1 its biases, 4 groups (8 bytes) at a time; a
+    // lane-half swap shares them
+    const uint16_t* sbp = (h ? P.biases : P.scales) + (mat + wrow) * (uint32_t)G;
+    const int nch = (nsteps + 3) / 4;
+    // x: DMA instruction i of wave w moves rows 8 (XU w + i) .. +7 (8 x 128 B); LDS slot
+    // p of row r holds k-slot p ^ ((r >> 1) & 7). Rows outside the item read past the
+    // end of x (zeros, no memory traffic).
+    uint32_t xo[XU];
+#pragma unroll
+    for (int i = 0; i < XU; ++i) {
+      const int r = 8 * (XU * wave + i) + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      const int64_t ro = rowtab[r];
+      xo[i] = ro >= 0 ? (uint32_t)ro * 2u + 16u * c : (uint32_t)kOOB;
+    }
+
+    u32x4_t wq[kD];
+    u32x2_t sbc[4];  // scale/bias chunks: chunk c (steps 4c..4c+3) in slot c % 4
+    // Step t's loads: its scale chunk when t starts one, its weights, then (last, so the
+    // wait before a step counts only younger loads) its x DMA.
+    auto issue = [&](int t, int slot, int cslot) __attribute__((always_inline)) {
+      const uint32_t tt = (uint32_t)min(t, nsteps - 1);
+      if ((t & 3) == 0)
+        sbc[cslot] = *reinterpret_cast<const u32x2_t*>(sbp + 4 * min(t >> 2, nch - 1));
+      wq[slot] = ld16(wres, wo, tt * 32u);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < XU; ++i)
+        dma16(xres, smem + slot * kStage + (XU * wave + i) * 1024, xo[i], tt * 128u);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+
+    f32x16_t acc[2][MT];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[a][i][r] = 0.f;
+
+    if (eok) {
+      // step t: wait for its DMA (issued kD - 1 steps earlier), barrier, compute(t), then
+      // issue step t + kD - 1 into the stage step t - 1 freed. Unrolled by 16 (two rings,
+      // four scale chunks) so every register slot is static.
+#pragma unroll
+      for (int j = 0; j < kD - 1; ++j) issue(j, j, (j >> 2) & 3);
+      for (int t0 = 0; t0 < nsteps; t0 += 16) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int t = t0 + j, js = j % kD;
+          // This step's x DMA is done once only the younger steps' loads (t+1 .. t+kD-2,
+          // kN each plus one per scale chunk they start) are in flight. The barrier waits
+          // on LDS traffic only, so the register loads stay in flight.
+          constexpr int kAfter0 = (kD - 2) * kN;
+          const int starts = ((j + kD - 2) >> 2) - (j >> 2);  // multiples of 4 in j+1..j+kD-2
+          switch (starts) {
+            case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAfter0 + 1)); break;
+            default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAfter0 + 2)); break;
+          }
+          qmv_detail::lds_barrier();
+          if (t < nsteps) {
+            // this step's group: t % 4 of chunk slot (t / 4) % 4
+            const u32x2_t mine = sbc[(j >> 2) & 3];
+            const uint32_t mw = (j & 2) ? mine.y : mine.x;
+            const uint32_t ow = xor32_u32(mw, lane);
+            const uint32_t sw = h ? ow : mw, bw = h ? mw : ow;
+            const float sc = __uint_as_float((j & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
+            const float bp = __uint_as_float((j & 1) ? (bw & 0xFFFF0000u) : (bw << 16));
+            // all fragment reads first, the dequantize under their latency, then the MFMAs
+            u32x4_t X[4][MT], A[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+              for (int i = 0; i < MT; ++i) {
+                const int r = 32 * i + fr, c = 4 * h + ks;
+                X[ks][i] = *reinterpret_cast<const u32x4_t*>(
+                    smem + js * kStage + r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+              }
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) A[ks] = dequant8(wq[js][ks], sc, bp);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+              for (int i = 0; i < MT; ++i)
+                acc[ks & 1][i] = mfma32(A[ks], X[ks][i], acc[ks & 1][i]);
+            __builtin_amdgcn_sched_group_barrier(0x100, 4 * MT, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 76, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * MT, 0);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          issue(t + kD - 1, (j + kD - 1) % kD, ((j + kD - 1) >> 2) & 3);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no DMA may outlive its stage
+    }
+
+    // epilogue: acc[.][i] register r is D[n = 32 wave + 8(r/4) + 4h + r%4][m = 32 i + fr]
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int m = 32 * i + fr;
+      const int64_t ro = rowtab[m];
+      if (ro == -1) continue;
+      const int64_t pos = it.pos0 + m;
+      const bool nan = ro == -2 || !eok;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + 32 * wave + 8 * g + 4 * h;
+        if (n >= N) continue;
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          v[q] = nan ? __builtin_nanf("") : acc[0][i][4 * g + q] + acc[1][i][4 * g + q];
+        uint16_t* y = reinterpret_cast<uint16_t*>(P.y) + pos * N + n;
+        if (P.swiglu_gate) {
+          const uint16_t* gt = P.swiglu_gate + pos * N + n;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            y[q] = swiglu_bf16(gt[q], (uint16_t)f32_to_bf16_bits(v[q]));
+        } else {
+          u32x2_t o;
+          o.x = pack_bf16x2(v[0], v[1]);
+          o.y = pack_bf16x2(v[2], v[3]);
+          *reinterpret_cast<u32x2_t*>(y) = o;
+        }
+      }
+    }
+    __syncthreads();  // the row table and the x ring are reused by the next item
+  }
+}
+
+}  // namespace
+
+bool gmm_supported(int64_t N, int64_t K, int bits, int gs, int x_f32, int64_t x_bytes) {
+  // whole 64-wide steps; scale chunks of 4 groups on an 8-byte boundary; 4-output stores;
+  // 32-bit buffer offsets
+  return bits == 4 && gs == 64 && !x_f32 && K % 256 == 0 && N % 4 == 0 && N >= 4 &&
+         N * (K / 2) < ((int64_t)1 << 31) && x_bytes + 2 * K < ((int64_t)1 << 31);
+}
+
+template <int MT, int WV>
+hipError_t launch_mt(const QmvParams& P, int grid_items, hipStream_t s) {
+  const size_t lds = (size_t)kD * 32 * MT * 128 + 32 * MT * sizeof(int64_t);
+  static bool attr = false;
+  if (!attr) {
+    auto k = gmm_kernel<MT, WV>;
+    hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  const dim3 grid((unsigned)((P.N + 32 * WV - 1) / (32 * WV)), (unsigned)std::max(1, grid_items));
+  hipLaunchKernelGGL((gmm_kernel<MT, WV>), grid, dim3(64 * WV), lds, s, P);
+  return hipGetLastError();
+}
+
+hipError_t launch_gmm(const QmvParams& P, int mt, int grid_items, hipStream_t s) {
+  if (!P.items || !P.item_count) return hipErrorInvalidValue;
+  // 4 waves (128 weight rows) a block, two blocks a CU: 256-row blocks of 8 waves measured
+  // 233 against 216 us per configs[3] T=512 layer
+  switch (mt) {
+    case 1: return launch_mt<1, 4>(P, grid_items, s);
+    case 2: return launch_mt<2, 4>(P, grid_items, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace mi

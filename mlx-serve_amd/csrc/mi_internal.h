@@ -99,6 +99,11 @@ bool qmvm_plan_odd(int rows, int N, int K, int gs, int bits, int64_t n_items, Qm
 hipError_t launch_qmvm(const QmvmParams& P, const QmvmPlan& plan, hipStream_t s);
 hipError_t launch_qmvm_gather(const QmvParams& G, const QmvmPlan& plan, int grid_z, hipStream_t s);
 
+// Grouped GEMM over sorted work items (gmm.hip): 4-bit affine gs 64, bf16 x; items of up to
+// 32 * mt rows (mt = 1, 2) built by launch_build_items; grid_items blocks stride them.
+bool gmm_supported(int64_t N, int64_t K, int bits, int gs, int x_f32, int64_t x_bytes);
+hipError_t launch_gmm(const QmvParams& P, int mt, int grid_items, hipStream_t s);
+
 // Decode-width kernel (qmv16.hip): M <= 16 rows per item, 16-row weight tiles.
 int qmv16_mp_for_rows(int rows);
 int qmv16_groups_per_chunk(int bits, int gs);

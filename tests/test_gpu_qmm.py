@@ -236,6 +236,32 @@ def test_gather_sorted_matches_unsorted(dev, M, K, E, T, topk):
     assert max_err_ratio(back, t2) <= BF16_TOL
 
 
+@pytest.mark.parametrize("N,K,E,T,topk,skew", [(200, 256, 8, 64, 4, False),
+                                                 (1536, 2048, 16, 96, 4, True),
+                                                 (260, 768, 4, 100, 2, True)])
+def test_gather_sorted_grouped_kernel(dev, N, K, E, T, topk, skew):
+    """Sorted gathers that average several rows per expert run the grouped kernel (one
+    block per work item x 128-row weight tile): widths that end in a partial tile, items of
+    32 and 64 rows, and skewed routings whose hot experts are cut into several items."""
+    _print_case(t="gather_grouped", N=N, K=K, E=E, T=T, topk=topk, skew=skew)
+    wq, s, b = weights(E, N, K, 4, 64, 210 + N)
+    rng = np.random.default_rng(N + K)
+    p = np.ones(E) / E
+    if skew:
+        p = np.ones(E)
+        p[: max(1, E // 8)] = 4.0 * E / max(1, E // 8)
+        p /= p.sum()
+    flat = rng.choice(E, size=T * topk, p=p).astype(np.uint32)
+    order, inv, srt, lhs = O.sort_dispatch(flat, topk)
+    x = O.make_x_bf16(T, K, 211 + K).reshape(T, 1, K)
+    y = mi_qmm.gather_qmm(to_dev_bf16(x, dev), to_dev_u32(wq, dev), to_dev_bf16(s, dev),
+                          to_dev_bf16(b, dev), lhs_indices=to_dev_u32(lhs, dev),
+                          rhs_indices=to_dev_u32(srt, dev), group_size=64, bits=4,
+                          sorted_indices=True)
+    truth = O.gather_qmm_f64(x, wq, s, b, lhs, srt, T * topk)
+    assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+
+
 def test_gather_out_of_range_is_nan(dev):
     _print_case(t="gather_oob")
     E, N, K = 4, 32, 128
