@@ -122,8 +122,10 @@ def decode_mlp(torch, mi, layers, M, bits, gs, dev, steps, warmup, hidden=4096, 
 
 def single_qmv(torch, mi, dev, reps=50, warmup=5):
     """one 4-bit g64 qmv x [1,4096] @ W [4096,4096]^T. Reports the eager
-    single-call latency (event-timed call on an idle GPU, median) and the rate over
-    rotated copies (>= 512 MB in one graph, so each call streams its weight from HBM)."""
+    single-call latency (HIP events bracketing one Python/ctypes call on an idle GPU, median:
+    it includes the host-side enqueue, so it is a host-inclusive latency, not a kernel time)
+    and the rate over rotated copies (>= 512 MB in one graph, so each call streams its weight
+    from HBM; that is the kernel figure)."""
     N = K = 4096
     bits, gs = 4, 64
     per = qbytes(N, K, bits, gs, 1)
@@ -153,7 +155,7 @@ def single_qmv(torch, mi, dev, reps=50, warmup=5):
         for W in Ws:
             mi.quantized_matmul(x, *W, True, gs, bits)
     t = graph_time(torch, all_copies, 10, 2) / copies
-    return {"cfg0_single_call_latency_us": round(lat[len(lat) // 2], 2),
+    return {"cfg0_single_call_host_inclusive_latency_us": round(lat[len(lat) // 2], 2),
             "cfg0_rotated_us_per_call": round(t * 1e6, 3),
             "cfg0_rotated_GBs": round(per / t / 1e9, 1),
             "cfg0_rotated_copies": copies}

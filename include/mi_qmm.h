@@ -93,8 +93,10 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
  * for callers that cannot allocate (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Same arguments, results and kernels as
  * mi_gather_qmm; its work items and K-split partials live in a fixed per-device scratch
- * array of MI_GATHER_NOALLOC_SCRATCH_BYTES (64 MiB) inside the library, held until the
- * process ends. A call that would need more returns MI_ERR_WORKSPACE. Every call on a
+ * array of MI_GATHER_NOALLOC_SCRATCH_BYTES (64 MiB) inside the library: the array is
+ * part of the library's code object, so it is reserved on every device when the library
+ * loads (whether or not this entry point is called) and held until the process ends. A
+ * call that would need more returns MI_ERR_WORKSPACE. Every call on a
  * device shares that device's scratch: calls that overlap on one device (different
  * streams, or concurrent host threads) race and must not be issued. */
 #define MI_GATHER_NOALLOC_SCRATCH_BYTES ((int64_t)64 << 20)

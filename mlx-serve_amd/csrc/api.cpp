@@ -104,18 +104,28 @@ int workspace(hipStream_t s, size_t bytes, void** data) {
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   std::lock_guard<std::mutex> lk(g_ws_mu);
   mi::GrowOnlyBuffer& w = g_ws[dev];
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  const bool capturing =
+      hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
   if (w.size() < bytes || !w.data()) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+    if (capturing)
       return fail(MI_ERR_WORKSPACE, "workspace too small during stream capture "
                   "(call mi_workspace_reserve before capturing)");
     hipError_t ae = hipSuccess;
-    const int rc = w.grow(bytes, [&](void** p, size_t n) {
-      ae = hipMalloc(p, n);
-      return ae == hipSuccess ? 0 : 1;
-    });
+    const int rc = w.grow(
+        bytes,
+        [&](void** p, size_t n) {
+          ae = hipMalloc(p, n);
+          return ae == hipSuccess ? 0 : 1;
+        },
+        [](void* p) {
+          // eager work queued on any stream of the device may still use it
+          (void)hipDeviceSynchronize();
+          (void)hipFree(p);
+        });
     if (rc) return hip_fail(ae, "hipMalloc(workspace)");
   }
+  if (capturing) w.mark_captured();  // a graph now holds this generation's address
   *data = w.data();
   return MI_OK;
 }
@@ -576,6 +586,27 @@ int mi_affine_params_from_geometry(int64_t w_cols, int64_t s_cols, int64_t in_di
   return MI_OK;
 }
 
+}  // extern "C"
+
+namespace {
+// The per-pair kernel for fp-mode and affine 2/3/5/6-bit gathers (up to 8 rows per pair):
+// one block column per pair, no workspace and no device allocation.
+int gather_any(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+               const uint32_t* lhs_indices, const uint32_t* rhs_indices, int64_t n_idx,
+               int64_t lhs_div, int64_t x_batch, int64_t M, int64_t N, int64_t K,
+               int64_t n_experts, int gs, int nb, int fm, hipStream_t s) {
+  hipError_t e = mi::launch_qmv_any_gather(
+      (const uint16_t*)x, w, scales, fm < 0 ? (const uint16_t*)biases : nullptr, (uint16_t*)y,
+      M, N, K, gs, nb, fm, lhs_indices, rhs_indices, n_idx, lhs_div, x_batch, n_experts, s);
+  if (e == hipErrorNotSupported)
+    return fail(MI_ERR_UNSUPPORTED, "gather_qmm at this format: up to 8 rows per pair, "
+                "65535 pairs and K*rows*2 <= 160 KiB");
+  return e == hipSuccess ? MI_OK : hip_fail(e, "qmv_any gather launch");
+}
+}  // namespace
+
+extern "C" {
+
 int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
                   const void* biases, const uint32_t* lhs_indices, const uint32_t* rhs_indices,
                   int64_t n_idx, int64_t lhs_div, int64_t x_batch, int64_t M, int64_t N, int64_t K,
@@ -613,14 +644,8 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
         return gather_launch(J, data, s);
       }
     }
-    hipError_t e = mi::launch_qmv_any_gather(
-        (const uint16_t*)x, w, scales, fm < 0 ? (const uint16_t*)biases : nullptr, (uint16_t*)y,
-        M, N, K, gs, nb, fm, lhs_indices, rhs_indices, n_idx, lhs_div, x_batch, n_experts,
-        (hipStream_t)stream);
-    if (e == hipErrorNotSupported)
-      return fail(MI_ERR_UNSUPPORTED, "gather_qmm at this format: up to 8 rows per pair, "
-                  "65535 pairs and K*rows*2 <= 160 KiB");
-    return e == hipSuccess ? MI_OK : hip_fail(e, "qmv_any gather launch");
+    return gather_any(y, x, w, scales, biases, lhs_indices, rhs_indices, n_idx, lhs_div,
+                      x_batch, M, N, K, n_experts, gs, nb, fm, (hipStream_t)stream);
   }
   GatherJob J;
   int rc = gather_prepare(J, y, x, w, scales, biases, lhs_indices, rhs_indices, n_idx, lhs_div,
@@ -651,30 +676,33 @@ int mi_gather_qmm_noalloc(void* y, const void* x, const uint32_t* w, const void*
   const int fm = fp_mode_of(mode);
   const bool odd_w = fm == -1 && bits.has_value && bits.value != 4 && bits.value != 8;
   if (fm >= 0 || odd_w) {
-    // fp-mode and odd-width gathers run the MFMA kernel with items / partials in scratch
+    // fp-mode and odd-width gathers: the MFMA kernel with items / partials in scratch, else
+    // the per-pair kernel, which needs no workspace at all
     int gs = 0, nb = 0;
     rc = fm >= 0 ? resolve_fp(fm, group_size, bits, transpose, K, sb_dtype, &gs, &nb)
                  : resolve_common(group_size, bits, mode, transpose, K, &gs, &nb);
     if (rc) return rc;
-    if (x_dtype == MI_DTYPE_BFLOAT16 && n_idx > 0 && M > 0 && N > 0 && lhs_div > 0 && y && x &&
-        w && scales && (fm >= 0 || (biases && sb_dtype == MI_DTYPE_BFLOAT16))) {
-      GatherJob J;
-      if (gather_prepare_fp(J, fm >= 0 ? fm : 100 + nb, gs, y, x, w, scales, biases,
-                            lhs_indices, rhs_indices, n_idx, lhs_div, x_batch, M, N, K,
-                            n_experts, sorted_indices) == MI_OK) {
-        if (J.ws_bytes() > kNoAllocScratchBytes)
-          return fail(MI_ERR_WORKSPACE, "gather_qmm_noalloc: the call needs %zu bytes of "
-                      "scratch, the fixed maximum is %zu", J.ws_bytes(), kNoAllocScratchBytes);
-        return gather_launch(J, data, (hipStream_t)stream);
-      }
+    if (fm < 0 && sb_dtype != MI_DTYPE_BFLOAT16)
+      return fail(MI_ERR_UNSUPPORTED, "scales/biases dtype %d not supported", sb_dtype);
+    if (x_dtype != MI_DTYPE_BFLOAT16)
+      return fail(MI_ERR_UNSUPPORTED, "gather_qmm at this format: bf16 activations only");
+    if (n_idx < 0 || M < 0 || N < 0 || x_batch < 0 || n_experts < 0 || lhs_div <= 0)
+      return fail(MI_ERR_INVALID, "negative size or lhs_div <= 0");
+    if (n_idx == 0 || M == 0 || N == 0) return MI_OK;
+    if (!y || !x || !w || !scales || (fm < 0 && !biases))
+      return fail(MI_ERR_INVALID, "null tensor pointer");
+    GatherJob J;
+    if (gather_prepare_fp(J, fm >= 0 ? fm : 100 + nb, gs, y, x, w, scales, biases, lhs_indices,
+                          rhs_indices, n_idx, lhs_div, x_batch, M, N, K, n_experts,
+                          sorted_indices) == MI_OK) {
+      if (J.ws_bytes() > kNoAllocScratchBytes)
+        return fail(MI_ERR_WORKSPACE, "gather_qmm_noalloc: the call needs %zu bytes of "
+                    "scratch, the fixed maximum is %zu", J.ws_bytes(), kNoAllocScratchBytes);
+      return gather_launch(J, data, (hipStream_t)stream);
     }
+    return gather_any(y, x, w, scales, biases, lhs_indices, rhs_indices, n_idx, lhs_div,
+                      x_batch, M, N, K, n_experts, gs, nb, fm, (hipStream_t)stream);
   }
-  if (fm >= 0 || (bits.has_value && bits.value != 4 && bits.value != 8 && fm == -1))
-    // the other odd-width and fp-mode gathers use no scratch: the allocating entry point
-    // allocates nothing on that path
-    return mi_gather_qmm(y, x, w, scales, biases, lhs_indices, rhs_indices, n_idx, lhs_div,
-                         x_batch, M, N, K, n_experts, transpose, group_size, bits, mode,
-                         sorted_indices, x_dtype, sb_dtype, stream);
   GatherJob J;
   rc = gather_prepare(J, y, x, w, scales, biases, lhs_indices, rhs_indices, n_idx, lhs_div,
                       x_batch, M, N, K, n_experts, transpose, group_size, bits, mode,

@@ -335,6 +335,13 @@ def gather_qmv_down_reduce(act, wd, sd, bd, inds, scores, group_size=None, bits=
     return y
 
 
+def workspace_release(device=None):
+    """Free the workspace generations that graphs captured earlier kept alive
+    (mi_workspace_release). Call it once no such graph will be replayed again."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    check(lib().mi_workspace_release(ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+
+
 def workspace_reserve(nbytes, device=None):
     """Grow the library's per-device workspace ahead of HIP graph capture."""
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device

@@ -259,7 +259,10 @@ def _fp_bank(mode, E, N, K, seed):
     m, bits, gs = O.FP_MODES[mode]
     rng = np.random.default_rng(seed)
     q = rng.integers(0, 1 << bits, size=(E * N, K)).astype(np.uint8)
-    lo, hi = (0x20, 0x48) if mode == "nvfp4" else (118, 126)
+    # scales for weights of a realistic size: random e4m3 codes reach +-480, so mxfp8 takes
+    # e8m0 scales 2^-17..2^-14 (|w| <= 0.03) and the fused MLP's activations stay well inside
+    # fp32 exp range; the 4-bit modes' codes stop at +-6
+    lo, hi = {"nvfp4": (0x20, 0x48), "mxfp4": (118, 126), "mxfp8": (110, 114)}[mode]
     sc = rng.integers(lo, hi, size=(E, N, K // gs)).astype(np.uint8)
     return O.pack(q, bits).reshape(E, N, -1), sc
 

@@ -76,6 +76,59 @@ def test_noalloc_matches_gather_fp4(dev, mode):
         assert np.array_equal(bf16_bits(y0), bf16_bits(y1))
 
 
+def test_noalloc_allocates_no_device_memory(dev):
+    """Device free memory is unchanged across no-alloc calls that need scratch (a sorted
+    gather with many work items and a K-split gather), after one warm-up call so the runtime's
+    own first-use allocations are out of the picture. A library that grew its workspace or
+    called hipMalloc would lower it by at least its 1 MiB minimum generation."""
+    _case(t="noalloc_free_memory")
+    cases = [(128, 768, 2048, 512, 8), (8, 64, 8192, 64, 4)]
+    prepared = []
+    for i, (E, N, K, T, topk) in enumerate(cases):
+        wq, s, b = weights(E, N, K, 4, 64, 500 + i)
+        rng = np.random.default_rng(500 + i)
+        flat = rng.integers(0, E, size=T * topk).astype(np.uint32)
+        _, _, srt, lhs = O.sort_dispatch(flat, topk)
+        x = to_dev_bf16(O.make_x_bf16(T, K, 501 + i).reshape(T, 1, K), dev)
+        W, S, B = to_dev_u32(wq, dev), to_dev_bf16(s, dev), to_dev_bf16(b, dev)
+        kw = dict(lhs_indices=to_dev_u32(lhs, dev), rhs_indices=to_dev_u32(srt, dev),
+                  group_size=64, bits=4, sorted_indices=True, noalloc=True)
+        out = torch.empty(T * topk, 1, N, dtype=torch.bfloat16, device=dev)
+        prepared.append((x, W, S, B, kw, out))
+    for (x, W, S, B, kw, out) in prepared:  # warm-up
+        mi_qmm.gather_qmm(x, W, S, B, out=out, **kw)
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    for (x, W, S, B, kw, out) in prepared:
+        mi_qmm.gather_qmm(x, W, S, B, out=out, **kw)
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free1 == free0
+
+
+def test_noalloc_rejects_oversized_scratch_fp_mode(dev):
+    """The fp-mode path's size guard: an nvfp4 sorted gather of 4.2M pairs on one expert needs
+    4.2M + 131K work items (69 MB) of scratch: refused before any launch."""
+    _case(t="noalloc_oversize_fp")
+    n = 4_200_000
+    K, N, E = 1024, 64, 1
+    m, bits, gs = O.FP_MODES["nvfp4"]
+    rng = np.random.default_rng(11)
+    q = rng.integers(0, 1 << bits, size=(E * N, K)).astype(np.uint8)
+    wq = O.pack(q, bits).reshape(E, N, -1)
+    sc = rng.integers(0x20, 0x48, size=(E, N, K // gs)).astype(np.uint8)
+    x = torch.zeros(1, 1, K, dtype=torch.bfloat16, device=dev)
+    rhs = torch.zeros(n, dtype=torch.int32, device=dev)
+    W, S = to_dev_u32(wq, dev), torch.from_numpy(sc).to(dev)
+    y = torch.empty(n, 1, N, dtype=torch.bfloat16, device=dev)
+    rc = mi_qmm._lib.lib().mi_gather_qmm_noalloc(
+        y.data_ptr(), x.data_ptr(), W.data_ptr(), S.data_ptr(), None, None,
+        rhs.data_ptr(), n, n, 1, 1, N, K, E, True, opt(None), opt(None), b"nvfp4", True, 12, 1,
+        None)
+    assert rc == MI_ERR_WORKSPACE
+    assert "scratch" in mi_qmm._lib.last_error()
+
+
 def test_noalloc_rejects_oversized_scratch(dev):
     """4M one-row pairs need 128 MiB of work items: refused before any launch."""
     _case(t="noalloc_oversize")
