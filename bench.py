@@ -247,7 +247,9 @@ def graph_time(torch, fn, replays, warmup=2):
 
 
 def prefill(torch, mi, dev, Ms, steps=10, warmup=2, bits=4, gs=64):
-    """prefill qmm TFLOP/s for x [M, K] against 4-bit g64 W [N, K]."""
+    """prefill qmm TFLOP/s for x [M, K] against 4-bit g64 W [N, K] (other widths
+    with --bits: 8-bit on the fused prefill kernel, 2/3/5/6 through dequantize + the bf16
+    GEMM)."""
     out = {}
     for (N, K, name) in ((14336, 4096, "gate"), (4096, 14336, "down")):
         tmp = torch.empty(N * K, dtype=torch.bfloat16, device=dev).view(N, K)
@@ -260,9 +262,10 @@ def prefill(torch, mi, dev, Ms, steps=10, warmup=2, bits=4, gs=64):
             t = time_region(torch, lambda: mi.quantized_matmul(x, *W, True, gs, bits), steps,
                             warmup)
             tf = 2.0 * M * N * K * steps / t / 1e12
-            out[f"prefill_{name}_M{M}_TFLOPs"] = round(tf, 1)
-            out[f"prefill_{name}_M{M}_pct_bf16_peak"] = round(100 * tf / BF16_PEAK_TFLOPS, 2)
-            out[f"prefill_{name}_M{M}_tok_s"] = round(M * steps / t, 1)
+            tag = f"prefill_{name}_M{M}" if bits == 4 else f"prefill{bits}_{name}_M{M}"
+            out[f"{tag}_TFLOPs"] = round(tf, 1)
+            out[f"{tag}_pct_bf16_peak"] = round(100 * tf / BF16_PEAK_TFLOPS, 2)
+            out[f"{tag}_tok_s"] = round(M * steps / t, 1)
         del W
     return out
 
@@ -388,7 +391,7 @@ def main():
     ap.add_argument("--decode-only", type=int, default=0, metavar="M",
                     help="only run the configs[1] decode step at this M (for rocprofv3)")
     ap.add_argument("--bits", type=int, default=4, choices=(2, 3, 4, 5, 6, 8),
-                    help="weight bits of --decode-only")
+                    help="weight bits of --decode-only and --prefill-only")
     ap.add_argument("--mode", default="affine", choices=("affine",) + tuple(FP_MODES),
                     help="weight format of --decode-only (fp modes: random codes and scales)")
     ap.add_argument("--prefill-only", type=int, default=0, metavar="M",
@@ -434,7 +437,7 @@ def main():
         return
     if args.prefill_only:
         print(json.dumps(prefill(torch, mi, dev, (args.prefill_only,), steps=args.steps,
-                                 warmup=args.warmup)))
+                                 warmup=args.warmup, bits=args.bits)))
         return
     if args.shared_only:
         print(json.dumps(shared_expert_8bit(torch, mi, dev, (args.shared_only,))))

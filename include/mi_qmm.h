@@ -240,9 +240,9 @@ int mi_gather_qmv_down_reduce(void* y, const void* act, const uint32_t* w_down,
 
 /* Grow the per-device workspace (sorted work lists, K-split partials) to at least
  * `bytes` ahead of HIP graph capture; calls that fit never allocate. No mlx-c
- * counterpart (MLX owns its allocator). Growing allocates a new buffer and keeps the
- * outgrown one allocated (graphs captured earlier still use it) until
- * mi_workspace_release. */
+ * counterpart (MLX owns its allocator). An outgrown buffer that a call handed out during
+ * a stream capture stays allocated (graphs captured then still use it) until
+ * mi_workspace_release; one never used under capture is freed when it is outgrown. */
 int mi_workspace_reserve(int64_t bytes, void* stream);
 
 /* Free the workspace generations this device has outgrown. Growing never frees the
@@ -256,6 +256,11 @@ const char* mi_last_error(void);
 
 /* Library version string. */
 const char* mi_version(void);
+
+/* Number of GEMMs this process has run through the vendor library (hipBLASLt). No
+ * counterpart in the reference: a diagnostic for callers and tests that check no default
+ * route reaches the library GEMM (only MI_QMM_DQGEMM=1 opts into it). */
+int64_t mi_library_gemm_calls(void);
 
 #ifdef __cplusplus
 }

@@ -536,6 +536,41 @@ int gather_launch(GatherJob& J, void* ws, hipStream_t s) {
 
 size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
+// Large-M route of the formats the fused kernels do not decode: dequantize the weight into
+// the workspace as bf16 (`dequant` launches that), then the prefill kernel's bf16-weight
+// instance (prefill.hip, bits = 16). The vendor GEMM (dq_gemm) runs instead only under
+// MI_QMM_DQGEMM=1, or for shapes that instance does not take.
+template <class Dequant>
+int dequant_then_gemm(const void* x, void* y, int64_t M, int64_t N, int64_t K, hipStream_t s,
+                      Dequant dequant) {
+  static const int use_lib = env_int("MI_QMM_DQGEMM", 0);
+  const size_t wbytes = round256((size_t)N * K * 2);
+  if (!use_lib && mi::prefill_supported(M, N, K, 16, 64)) {
+    mi::PrefillParams Q{nullptr, nullptr, nullptr, (const uint16_t*)x, (uint16_t*)y, (int)M,
+                        (int)N, (int)K, 64, nullptr, 1, 0, 16};
+    const size_t pbytes = mi::prefill_plan(Q);
+    void* data = nullptr;
+    int rc = workspace(s, wbytes + pbytes, &data);
+    if (rc) return rc;
+    hipError_t e = dequant(data);
+    if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+    Q.w = (const uint32_t*)data;
+    if (pbytes) Q.part = (float*)((char*)data + wbytes);
+    e = mi::launch_prefill(Q, s);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "bf16 prefill launch");
+  }
+  void* data = nullptr;
+  int rc = workspace(s, wbytes + mi::kDqGemmBlasWs, &data);
+  if (rc) return rc;
+  hipError_t e = dequant(data);
+  if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+  const char* err = nullptr;
+  if (mi::dq_gemm((const uint16_t*)x, (const uint16_t*)data, (uint16_t*)y, (int)M, (int)N,
+                  (int)K, (int)N, (char*)data + wbytes, mi::kDqGemmBlasWs, s, &err) != 0)
+    return fail(MI_ERR_HIP, "hipBLASLt GEMM: %s", err ? err : "error");
+  return MI_OK;
+}
+
 }  // namespace
 
 namespace mi {
@@ -568,6 +603,8 @@ int mi_workspace_release(void* stream) {
 }
 
 const char* mi_version(void) { return "mi_qmm 0.1 gfx950"; }
+
+int64_t mi_library_gemm_calls(void) { return mi::g_library_gemms.load(); }
 
 int mi_affine_params_from_geometry(int64_t w_cols, int64_t s_cols, int64_t in_dim, int* bits,
                                    int* group_size) {
@@ -790,17 +827,9 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
                                         N, K, gs, nb, fm, s);
       if (e != hipErrorNotSupported) return e == hipSuccess ? MI_OK : hip_fail(e, "qmv_any launch");
     }
-    const size_t wbytes = round256((size_t)N * K * 2);
-    void* data = nullptr;
-    rc = workspace(s, wbytes + mi::kDqGemmBlasWs, &data);
-    if (rc) return rc;
-    hipError_t e = mi::launch_dequantize_fp(data, w, (const uint8_t*)scales, N, K, fm, 0, nullptr, s);
-    if (e != hipSuccess) return hip_fail(e, "dequantize launch");
-    const char* err = nullptr;
-    if (mi::dq_gemm((const uint16_t*)x, (const uint16_t*)data, (uint16_t*)y, (int)M, (int)N,
-                    (int)K, (int)N, (char*)data + wbytes, mi::kDqGemmBlasWs, s, &err) != 0)
-      return fail(MI_ERR_HIP, "hipBLASLt GEMM: %s", err ? err : "error");
-    return MI_OK;
+    return dequant_then_gemm(x, y, M, N, K, s, [&](void* wd) {
+      return mi::launch_dequantize_fp(wd, w, (const uint8_t*)scales, N, K, fm, 0, nullptr, s);
+    });
   }
   int rc = resolve_common(group_size, bits, mode, transpose, K, &gs, &nb);
   if (rc) return rc;
@@ -813,14 +842,14 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   if (N > (int64_t)1 << 30 || M > (int64_t)1 << 30) return fail(MI_ERR_INVALID, "N or M too large");
   hipStream_t s = (hipStream_t)stream;
   // Dispatch, in order:
-  //  - 4-bit weights at M >= MI_QMM_PREFILL_MIN (default 128): the fused prefill kernel
+  //  - 4- and 8-bit weights at M >= MI_QMM_PREFILL_MIN (default 128): the fused prefill kernel
   //    (prefill.hip), which replaces the reference's prefillDqGemm route
   //    (src/transformer.zig:20987-21011) without a bf16 copy of the weight;
   //  - one row of gs-64 2/3/5/6/8-bit weights: the one-row streaming kernel;
   //  - 2/3/5/6 bits: the few-row MFMA kernel (2..32 rows, gs 64), qmv_any (up to
-  //    MI_QMM_ANY_MAX rows), else dequantize + hipBLASLt;
+  //    MI_QMM_ANY_MAX rows), else dequantize to bf16 + the prefill kernel's bf16 instance;
   //  - 4/8 bits: the few-row MFMA kernel (up to 64 rows), else the fused qmm kernel.
-  //    Dequantize + hipBLASLt for 4/8 bits is opt-in (MI_QMM_DQGEMM=1, from
+  //    Dequantize + hipBLASLt is opt-in for every format (MI_QMM_DQGEMM=1; for 4/8 bits from
   //    MI_QMM_DQGEMM_MIN rows).
   static const int dq_min = env_int("MI_QMM_DQGEMM_MIN", 256);
   static const int use_dqgemm = env_int("MI_QMM_DQGEMM", 0);
@@ -828,7 +857,7 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   if (x_dtype == MI_DTYPE_BFLOAT16 && !use_dqgemm && M >= prefill_min &&
       mi::prefill_supported(M, N, K, nb, gs)) {
     mi::PrefillParams Q{w, (const uint16_t*)scales, (const uint16_t*)biases, (const uint16_t*)x,
-                        (uint16_t*)y, (int)M, (int)N, (int)K, gs, nullptr, 1, 0};
+                        (uint16_t*)y, (int)M, (int)N, (int)K, gs, nullptr, 1, 0, nb};
     const size_t ws = mi::prefill_plan(Q);
     if (ws) {
       void* data = nullptr;
@@ -906,18 +935,10 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   }
   if (x_dtype == MI_DTYPE_BFLOAT16 && (odd_width || (use_dqgemm && dq_min > 0 && M >= dq_min)) &&
       K <= INT32_MAX && N * K * 2 <= ((int64_t)1 << 34)) {
-    const size_t wbytes = round256((size_t)N * K * 2);
-    void* data = nullptr;
-    rc = workspace(s, wbytes + mi::kDqGemmBlasWs, &data);
-    if (rc) return rc;
-    hipError_t e = mi::launch_dequantize(data, w, (const uint16_t*)scales, (const uint16_t*)biases,
-                                         N, K, gs, nb, 0, 0, s);
-    if (e != hipSuccess) return hip_fail(e, "dequantize launch");
-    const char* err = nullptr;
-    if (mi::dq_gemm((const uint16_t*)x, (const uint16_t*)data, (uint16_t*)y, (int)M, (int)N,
-                    (int)K, (int)N, (char*)data + wbytes, mi::kDqGemmBlasWs, s, &err) != 0)
-      return fail(MI_ERR_HIP, "hipBLASLt GEMM: %s", err ? err : "error");
-    return MI_OK;
+    return dequant_then_gemm(x, y, M, N, K, s, [&](void* wd) {
+      return mi::launch_dequantize(wd, w, (const uint16_t*)scales, (const uint16_t*)biases, N,
+                                   K, gs, nb, 0, 0, s);
+    });
   }
   // 2..64 rows: the few-row MFMA kernel (33..64 rows as two 32-row passes per block)
   static const int use_qmvm = env_int("MI_QMM_QMVM", 1);

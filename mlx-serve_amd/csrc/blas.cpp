@@ -7,6 +7,7 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>
+#include <atomic>
 #include <mutex>
 #include <tuple>
 
@@ -43,8 +44,11 @@ const char* status_name(hipblasStatus_t st) {
 }  // namespace
 
 // Column-major view: y^T [N x M] (ld ldy) = W (col-major K x N, op T) x x^T (col-major K x M).
+std::atomic<int64_t> g_library_gemms{0};
+
 int dq_gemm(const uint16_t* x, const uint16_t* wd, uint16_t* y, int M, int N, int K, int ldy,
             void* blas_ws, size_t blas_ws_bytes, hipStream_t s, const char** err) {
+  g_library_gemms.fetch_add(1, std::memory_order_relaxed);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
     *err = "hipGetDevice failed";

@@ -1,5 +1,6 @@
 // Internal (host + device) declarations shared by the kernels and the C ABI layer.
 #pragma once
+#include <atomic>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -175,8 +176,9 @@ size_t qmm_plan(QmmParams& P);
 hipError_t launch_qmm(const QmmParams& P, hipStream_t s);
 bool qmm_supported(int M, int N, int K, int bits, int gs);
 
-// Prefill GEMM for 4-bit weights (prefill.hip): 256x256 tiles, weights dequantized in
-// registers, x through an LDS ring; ks > 1 splits K (fp32 partials [ks][M][N] in `part`,
+// Prefill GEMM for 4- and 8-bit weights, and for weights already dequantized to bf16
+// (bits = 16) (prefill.hip): 256x256 tiles, weights dequantized in registers, x through an
+// LDS ring; ks > 1 splits K (fp32 partials [ks][M][N] in `part`,
 // summed in split order by a second kernel).
 struct PrefillParams {
   const uint32_t* w;
@@ -188,10 +190,13 @@ struct PrefillParams {
   int group_size;
   float* part;
   int ks, sps;  // K splits and 64-wide steps per split
+  int bits;     // 4, 8, or 16 (w holds bf16 [N, K])
 };
 bool prefill_supported(int64_t M, int64_t N, int64_t K, int bits, int gs);
 size_t prefill_plan(PrefillParams& P);  // fills ks / sps; returns workspace bytes
 hipError_t launch_prefill(const PrefillParams& P, hipStream_t s);
+
+extern std::atomic<int64_t> g_library_gemms;  // dq_gemm calls (blas.cpp)
 
 // Dequantize + hipBLASLt bf16 GEMM for large M (blas.cpp): y = x @ wd^T with wd the
 // dequantized bf16 [N, K] weight; blas_ws is the library's scratch. 0 or -1 (err set).

@@ -14,6 +14,7 @@
 // (no VGPR round trip); the schedule is described at prefill_pp_kernel.
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "mi_common.h"
 #include "mi_internal.h"
@@ -66,13 +67,34 @@ constexpr int kBufFlags = 0x00020000;   // raw dword access
 // issued before the DMA of step t+2, so the barrier publishes step t+1 before group 0
 // reads it in half 2t+2. The weight and scale buffers are reused two chunks later, after
 // the last read of the chunk they held.
+// 8-bit weights (BITS = 8) take the same path with one step per weight chunk (64 B of a row
+// is one step's 64 codes), in 3 buffers: a 1-step chunk is last read in the half after its
+// successor's DMA would go out, so two buffers would not do.
 constexpr int kPPThreads = 512;
 constexpr int kPPXStage = kXBytes;                   // 32 KB
 constexpr int kPPWChunk = kBN * 64;                  // 256 rows x 64 B
 constexpr int kPPSChunk = kBN * 16;                  // 256 rows x 16 B (scales or biases)
 constexpr int kPPWOff = kRing * kPPXStage;           // 96 KB
-constexpr int kPPSOff = kPPWOff + 2 * kPPWChunk;     // 128 KB
-constexpr int kPPLds = kPPSOff + 4 * kPPSChunk;      // 144 KB
+// BITS = 16: weights already dequantized to bf16 (the other formats' large-M route). A
+// lane's 64 bytes of its row per step are read straight into registers (a 3-step ring), so
+// LDS holds only the x ring and the mem unit does no dequantize work.
+template <int BITS>
+constexpr int pp_wbufs() { return BITS == 4 ? 2 : BITS == 8 ? 3 : 0; }
+template <int BITS>
+constexpr int pp_soff() { return kPPWOff + pp_wbufs<BITS>() * kPPWChunk; }  // 128 / 144 KB
+template <int BITS>
+constexpr int pp_lds() { return BITS == 16 ? kPPWOff : pp_soff<BITS>() + 4 * kPPSChunk; }
+
+// 8 bytes (codes q0..q7, k order) -> four bf16 pairs of s*q + b: each byte converts exactly
+// (v_cvt_f32_ubyte), fma(s, q, b), one rounding to bf16.
+MI_DEV u32x4_t dequant8_b8(uint32_t w0, uint32_t w1, float s, float b) {
+  u32x4_t o;
+  o.x = pack_bf16x2(fmaf(s, (float)(w0 & 0xFFu), b), fmaf(s, (float)((w0 >> 8) & 0xFFu), b));
+  o.y = pack_bf16x2(fmaf(s, (float)((w0 >> 16) & 0xFFu), b), fmaf(s, (float)(w0 >> 24), b));
+  o.z = pack_bf16x2(fmaf(s, (float)(w1 & 0xFFu), b), fmaf(s, (float)((w1 >> 8) & 0xFFu), b));
+  o.w = pack_bf16x2(fmaf(s, (float)((w1 >> 16) & 0xFFu), b), fmaf(s, (float)(w1 >> 24), b));
+  return o;
+}
 
 MI_DEV void wait_vm(int n) {  // s_waitcnt vmcnt(n) for the counts one step can issue
   switch (n) {
@@ -84,9 +106,12 @@ MI_DEV void wait_vm(int n) {  // s_waitcnt vmcnt(n) for the counts one step can 
   }
 }
 
-template <int GS, bool SPLIT>
+template <int BITS, int GS, bool SPLIT>
 __global__ void __launch_bounds__(kPPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 prefill_pp_kernel(PrefillParams P) {
+  constexpr int RB = BITS * kBK / 8;  // bytes of a weight row per step: 32, 64 or 128
+  constexpr bool W16 = BITS == 16;
+  constexpr int kSOff = pp_soff<BITS>();
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   // steps per scale chunk (8 groups): 4, 8 or 16
   constexpr int kSP = GS / 8;
@@ -105,8 +130,9 @@ prefill_pp_kernel(PrefillParams P) {
 
   const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(P.x + (size_t)m0 * K), 0, mrows * K * 2, kBufFlags);
+  const int rowb = K * BITS / 8;  // bytes of a weight row
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const unsigned char*)P.w + (size_t)n0 * (K / 2)), 0, nrows * (K / 2), kBufFlags);
+      (void*)((const unsigned char*)P.w + (size_t)n0 * rowb), 0, nrows * rowb, kBufFlags);
   // group 0 moves the scales, group 1 the biases
   const __amdgpu_buffer_rsrc_t sbres = __builtin_amdgcn_make_buffer_rsrc(
       (void*)((grp ? P.biases : P.scales) + (size_t)n0 * G), 0, nrows * G * 2, kBufFlags);
@@ -119,14 +145,15 @@ prefill_pp_kernel(PrefillParams P) {
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     xo[i] = (uint32_t)(min(r, mrows - 1) * K + 8 * c) * 2;
   }
-  // packed-weight chunk: wave w moves rows 32w..32w+31 as 2 instructions of 16 rows x 64 B;
-  // LDS part p (16 B) of row r holds part p ^ ((r >> 2) & 3) of the row's 64 bytes.
+  // packed-weight chunk (2 steps at 4 bits, 1 at 8): wave w moves rows 32w..32w+31 as 2
+  // instructions of 16 rows x 64 B; LDS part p (16 B) of row r holds part p ^ ((r >> 2) & 3)
+  // of the row's 64 bytes.
   uint32_t wo[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int r = 32 * wave + 16 * i + (lane >> 2);
     const int c = (lane & 3) ^ ((r >> 2) & 3);
-    wo[i] = (uint32_t)(min(r, nrows - 1) * (K / 2) + 16 * c);
+    wo[i] = (uint32_t)(min(r, nrows - 1) * rowb + 16 * c);
   }
   // scale (group 0) or bias (group 1) chunk: wave moves rows 64nq..64nq+63 as 4
   // instructions of 16 rows x 4 dwords; row-major 16 B per row in LDS.
@@ -136,9 +163,14 @@ prefill_pp_kernel(PrefillParams P) {
     const int r = 64 * nq + 16 * i + (lane >> 2);
     so[i] = (uint32_t)(min(r, nrows - 1) * G * 2 + 4 * (lane & 3));
   }
+  // bf16 weights: lane (fr, h) reads bytes 64h .. 64h+63 of its row's 128 per step
+  u32x4_t wreg[W16 ? 3 : 1][4];
+  const uint32_t w16o = (uint32_t)min(32 * wave + fr, nrows - 1) * (uint32_t)rowb + 64 * h;
   // DMA of local step st (x; the weight chunk when st is even; the scale chunk when st
-  // starts one). Returns the instructions issued (0 past the last step).
-  auto issue = [&](int st) -> int {
+  // starts one; bf16 weights into register slot `slot`). Returns the instructions issued
+  // (0 past the last step).
+  auto issue = [&](int st, auto slot_c) -> int {
+    constexpr int slot = decltype(slot_c)::value;
     if (st >= nsteps) return 0;
     const int k = s0 + st;
     unsigned char* xb = smem + (st % kRing) * kPPXStage;
@@ -146,16 +178,22 @@ prefill_pp_kernel(PrefillParams P) {
     for (int i = 0; i < 4; ++i)
       MI_DMA_LDS(16, xres, xb + wave * 4096 + i * 1024, xo[i], k * kBK * 2);
     int n = 4;
-    if ((st & 1) == 0) {
-      unsigned char* wb = smem + kPPWOff + ((st >> 1) & 1) * kPPWChunk;
+    if constexpr (W16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        wreg[slot][i] = __builtin_amdgcn_raw_buffer_load_b128(wres, w16o + 16 * i, k * RB, 0);
+      return n + 4;
+    }
+    if (BITS == 8 || (st & 1) == 0) {
+      unsigned char* wb = smem + kPPWOff + (BITS == 4 ? (st >> 1) & 1 : st % 3) * kPPWChunk;
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        MI_DMA_LDS(16, wres, wb + wave * 2048 + i * 1024, wo[i], k * (kBK / 2));
+        MI_DMA_LDS(16, wres, wb + wave * 2048 + i * 1024, wo[i], k * RB);
       n += 2;
     }
     if (st == 0 || k % kSP == 0) {
       const int c = k / kSP;
-      unsigned char* sb = smem + kPPSOff + (c & 1) * 2 * kPPSChunk + grp * kPPSChunk;
+      unsigned char* sb = smem + kSOff + (c & 1) * 2 * kPPSChunk + grp * kPPSChunk;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         MI_DMA_LDS(4, sbres, sb + nq * 1024 + i * 256, so[i], c * 16);
@@ -180,26 +218,41 @@ prefill_pp_kernel(PrefillParams P) {
                                              ((c ^ ((r >> 1) & 7)) << 4));
   };
   u32x4_t A[4], X[2][8];
-  auto mem = [&](int st) {
-    const int k = s0 + st;
-    const unsigned char* wb = smem + kPPWOff + ((st >> 1) & 1) * kPPWChunk;
-    const unsigned char* sb = smem + kPPSOff + ((k / kSP) & 1) * 2 * kPPSChunk;
-    // group of this lane's 32 k within the chunk's 8
-    const int gi = GS == 32 ? 2 * (k % 4) + h : GS == 64 ? k % 8 : (k >> 1) % 8;
-    const int part = 2 * (st & 1) + h;
-    const int r = 32 * wave + fr;
-    const u32x4_t q =
-        *reinterpret_cast<const u32x4_t*>(wb + r * 64 + ((part ^ ((r >> 2) & 3)) << 4));
-    const uint16_t sv = *reinterpret_cast<const uint16_t*>(sb + r * 16 + 2 * gi);
-    const uint16_t bv = *reinterpret_cast<const uint16_t*>(sb + kPPSChunk + r * 16 + 2 * gi);
+  auto mem = [&](int st, auto slot_c) {
+    constexpr int slot = decltype(slot_c)::value;
 #pragma unroll
     for (int i = 0; i < 8; ++i) X[0][i] = xfrag(st % kRing, i, 0);
+    if constexpr (W16) return;  // the MFMAs read the weight registers in place
+    const int k = s0 + st;
+    const unsigned char* wb =
+        smem + kPPWOff + (BITS == 4 ? (st >> 1) & 1 : st % 3) * kPPWChunk;
+    const unsigned char* sb = smem + kSOff + ((k / kSP) & 1) * 2 * kPPSChunk;
+    // group of this lane's 32 k within the chunk's 8
+    const int gi = GS == 32 ? 2 * (k % 4) + h : GS == 64 ? k % 8 : (k >> 1) % 8;
+    const int r = 32 * wave + fr;
+    // the lane's 32 codes: 16 B (part 2(st%2) + h) at 4 bits, 32 B (parts 2h, 2h+1) at 8
+    const int part = BITS == 4 ? 2 * (st & 1) + h : 2 * h;
+    const u32x4_t q =
+        *reinterpret_cast<const u32x4_t*>(wb + r * 64 + ((part ^ ((r >> 2) & 3)) << 4));
+    u32x4_t q2 = q;
+    if constexpr (BITS == 8)
+      q2 = *reinterpret_cast<const u32x4_t*>(wb + r * 64 + (((part + 1) ^ ((r >> 2) & 3)) << 4));
+    const uint16_t sv = *reinterpret_cast<const uint16_t*>(sb + r * 16 + 2 * gi);
+    const uint16_t bv = *reinterpret_cast<const uint16_t*>(sb + kPPSChunk + r * 16 + 2 * gi);
     const float sc = __uint_as_float((uint32_t)sv << 16);
     const float bp = __uint_as_float((uint32_t)bv << 16);
+    if constexpr (BITS == 4) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) A[ks] = dequant8(q[ks], sc, bp);
+      for (int ks = 0; ks < 4; ++ks) A[ks] = dequant8(q[ks], sc, bp);
+    } else {
+      A[0] = dequant8_b8(q.x, q.y, sc, bp);
+      A[1] = dequant8_b8(q.z, q.w, sc, bp);
+      A[2] = dequant8_b8(q2.x, q2.y, sc, bp);
+      A[3] = dequant8_b8(q2.z, q2.w, sc, bp);
+    }
   };
-  auto mfma = [&](int st) {
+  auto mfma = [&](int st, auto slot_c) {
+    constexpr int slot = decltype(slot_c)::value;
     const int stg = st % kRing;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -208,7 +261,8 @@ prefill_pp_kernel(PrefillParams P) {
         for (int i = 0; i < 8; ++i) X[(ks + 1) & 1][i] = xfrag(stg, i, ks + 1);
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = mfma32(A[ks], X[ks & 1][i], acc[i]);
+      for (int i = 0; i < 8; ++i)
+        acc[i] = mfma32(W16 ? wreg[slot][ks] : A[ks], X[ks & 1][i], acc[i]);
       // the next k-step's fragment reads go out ahead of this k-step's MFMAs, one read
       // per MFMA, so their latency hides under the matrix work
 #pragma unroll
@@ -224,21 +278,35 @@ prefill_pp_kernel(PrefillParams P) {
   // group 1 starts one half later (an extra barrier first), group 0 ends with an extra
   // barrier, so the barrier counts match. The DMA of step t+2 goes out in half 2t+1 for
   // both groups: after group 0's mfma(t) unit and after group 1's mem(t) unit.
-  issue(0);
-  wait_vm(issue(1));
+  using c0 = std::integral_constant<int, 0>;
+  using c1 = std::integral_constant<int, 1>;
+  using c2 = std::integral_constant<int, 2>;
+  issue(0, c0{});
+  wait_vm(issue(1, c1{}));
   __builtin_amdgcn_s_barrier();
   if (grp) __builtin_amdgcn_s_barrier();
-  for (int t = 0; t < nsteps; ++t) {
-    mem(t);
+  // (ws: the register slot of step t's bf16 weights, wn: that of step t + 2)
+  auto step = [&](int t, auto ws, auto wn) {
+    mem(t, ws);
     __builtin_amdgcn_sched_barrier(0);
-    if (grp) wait_vm(issue(t + 2));
+    if (grp) wait_vm(issue(t + 2, wn));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    mfma(t);
+    mfma(t, ws);
     __builtin_amdgcn_sched_barrier(0);
-    if (!grp) wait_vm(issue(t + 2));
+    if (!grp) wait_vm(issue(t + 2, wn));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
+  };
+  if constexpr (W16) {
+    // unrolled by 3 so the weight registers of steps t, t+1, t+2 sit in static slots
+    for (int t0 = 0; t0 < nsteps; t0 += 3) {
+      step(t0, c0{}, c2{});
+      if (t0 + 1 < nsteps) step(t0 + 1, c1{}, c0{});
+      if (t0 + 2 < nsteps) step(t0 + 2, c2{}, c1{});
+    }
+  } else {
+    for (int t = 0; t < nsteps; ++t) step(t, c0{}, c0{});
   }
   if (!grp) __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no DMA may outlive the block
@@ -284,34 +352,49 @@ hipError_t set_lds(Kern k, size_t lds) {
   return hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
 }
 
-template <int GS>
+template <int BITS, int GS>
 hipError_t launch_gs(const PrefillParams& P, hipStream_t s) {
   const int mtiles = (P.M + kBM - 1) / kBM, ntiles = (P.N + kBN - 1) / kBN;
+  constexpr int lds = pp_lds<BITS>();
   static bool attr = false;
   if (!attr) {
     hipError_t e = hipSuccess;
-    for (auto k : {prefill_pp_kernel<GS, true>, prefill_pp_kernel<GS, false>})
-      if (e == hipSuccess) e = set_lds(k, kPPLds);
+    for (auto k : {prefill_pp_kernel<BITS, GS, true>, prefill_pp_kernel<BITS, GS, false>})
+      if (e == hipSuccess) e = set_lds(k, lds);
     if (e != hipSuccess) return e;
     attr = true;
   }
   const dim3 grid((unsigned)(mtiles * ntiles), (unsigned)P.ks);
   if (P.ks > 1)
-    hipLaunchKernelGGL((prefill_pp_kernel<GS, true>), grid, dim3(kPPThreads), kPPLds, s, P);
+    hipLaunchKernelGGL((prefill_pp_kernel<BITS, GS, true>), grid, dim3(kPPThreads), lds, s, P);
   else
-    hipLaunchKernelGGL((prefill_pp_kernel<GS, false>), grid, dim3(kPPThreads), kPPLds, s, P);
+    hipLaunchKernelGGL((prefill_pp_kernel<BITS, GS, false>), grid, dim3(kPPThreads), lds, s, P);
   return hipGetLastError();
+}
+
+template <int BITS>
+hipError_t launch_bits(const PrefillParams& P, hipStream_t s) {
+  if constexpr (BITS == 16)
+    return launch_gs<16, 64>(P, s);  // no groups
+  else
+    return P.group_size == 32   ? launch_gs<BITS, 32>(P, s)
+           : P.group_size == 64 ? launch_gs<BITS, 64>(P, s)
+                                : launch_gs<BITS, 128>(P, s);
 }
 
 }  // namespace
 
 bool prefill_supported(int64_t M, int64_t N, int64_t K, int bits, int gs) {
-  if (bits != 4 || (gs != 32 && gs != 64 && gs != 128)) return false;
+  if (bits == 16)  // bf16 weights: no groups, no scale chunks
+    return M >= 1 && N >= 4 && N % 4 == 0 && K % kBK == 0 &&
+           (int64_t)kBM * K * 2 < ((int64_t)1 << 31) && (int64_t)kBN * K * 2 < ((int64_t)1 << 31) &&
+           M < ((int64_t)1 << 30) && N < ((int64_t)1 << 30);
+  if ((bits != 4 && bits != 8) || (gs != 32 && gs != 64 && gs != 128)) return false;
   // 32-bit buffer offsets per block; 4-output stores; whole 64-wide steps and groups; an
   // even group count, so every row's scales and biases start on a dword (the staging
   // moves them as dwords)
   return M >= 1 && N >= 4 && N % 4 == 0 && K % kBK == 0 && K % gs == 0 && (K / gs) % 2 == 0 &&
-         (int64_t)kBM * K * 2 < ((int64_t)1 << 31) && (int64_t)kBN * K < ((int64_t)1 << 31) &&
+         (int64_t)kBM * K * 2 < ((int64_t)1 << 31) && (int64_t)kBN * K * bits / 8 < ((int64_t)1 << 31) &&
          M < ((int64_t)1 << 30) && N < ((int64_t)1 << 30);
 }
 
@@ -350,11 +433,11 @@ size_t prefill_plan(PrefillParams& P) {
 }
 
 hipError_t launch_prefill(const PrefillParams& P, hipStream_t s) {
-  if (!prefill_supported(P.M, P.N, P.K, 4, P.group_size)) return hipErrorNotSupported;
+  if (!prefill_supported(P.M, P.N, P.K, P.bits, P.group_size)) return hipErrorNotSupported;
   if (P.ks > 1 && !P.part) return hipErrorInvalidValue;
-  hipError_t e = P.group_size == 32 ? launch_gs<32>(P, s)
-                 : P.group_size == 64 ? launch_gs<64>(P, s)
-                                      : launch_gs<128>(P, s);
+  hipError_t e = P.bits == 16 ? launch_bits<16>(P, s)
+                 : P.bits == 8 ? launch_bits<8>(P, s)
+                               : launch_bits<4>(P, s);
   if (e != hipSuccess || P.ks == 1) return e;
   const int64_t mn4 = (int64_t)P.M * P.N / 4;
   int64_t g = (mn4 + 255) / 256;

@@ -66,6 +66,8 @@ def lib():
                                               i64, i64, OptInt, OptInt, s, i32, P]
     L.mi_workspace_reserve.argtypes = [i64, P]
     L.mi_workspace_release.argtypes = [P]
+    L.mi_library_gemm_calls.argtypes = []
+    L.mi_library_gemm_calls.restype = ctypes.c_int64
     L.mi_last_error.restype = ctypes.c_char_p
     PP = ctypes.POINTER(P)
     L.mi_ckpt_open.argtypes = [s, i32, PP]

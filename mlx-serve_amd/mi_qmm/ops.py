@@ -335,6 +335,12 @@ def gather_qmv_down_reduce(act, wd, sd, bd, inds, scores, group_size=None, bits=
     return y
 
 
+def library_gemm_calls():
+    """GEMMs this process has run through the vendor library (hipBLASLt); every default
+    route uses this project's kernels, so it stays 0 unless MI_QMM_DQGEMM=1."""
+    return int(lib().mi_library_gemm_calls())
+
+
 def workspace_release(device=None):
     """Free the workspace generations that graphs captured earlier kept alive
     (mi_workspace_release). Call it once no such graph will be replayed again."""

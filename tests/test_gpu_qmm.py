@@ -420,6 +420,32 @@ def test_dequantize_fp_modes_bit_exact(dev, mode):
     assert np.array_equal(bf, O.dequantize_fp(wq, sc, mode, out_bf16=True))
 
 
+@pytest.mark.parametrize("fmt", ["b2", "b3", "b5", "b6", "nvfp4", "mxfp4", "mxfp8"])
+@pytest.mark.parametrize("M", [64, 512])
+def test_large_m_other_formats_own_gemm(dev, fmt, M):
+    """Above the few-row kernels, 2/3/5/6-bit and nvfp4 / mxfp4 / mxfp8 weights dequantize
+    to bf16 and run the prefill kernel's bf16-weight instance: results against the oracle,
+    and the vendor GEMM never runs (its call counter does not move)."""
+    _print_case(t="large_m_format", fmt=fmt, M=M)
+    N, K = 300, 1024
+    before = mi_qmm.library_gemm_calls()
+    x = O.make_x_bf16(M, K, 900 + M)
+    if fmt.startswith("b"):
+        bits = int(fmt[1:])
+        wq, s, b = weights(1, N, K, bits, 64, 910 + bits)
+        y = mi_qmm.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(wq[0], dev),
+                                    to_dev_bf16(s[0], dev), to_dev_bf16(b[0], dev), True, 64, bits)
+        truth = O.qmm_f64(x, wq[0], s[0], b[0], 64, bits)
+    else:
+        wq, sc = _fp_weight(fmt, N, K, 920 + M)
+        y = mi_qmm.quantized_matmul(to_dev_bf16(x, dev), to_dev_u32(wq, dev),
+                                    torch.from_numpy(sc).to(dev), None, True, mode=fmt)
+        truth = O.bf16_to_f32(x).astype(np.float64) @ O.dequantize_fp(wq, sc, fmt).astype(np.float64).T
+    torch.cuda.synchronize()
+    assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+    assert mi_qmm.library_gemm_calls() == before
+
+
 @pytest.mark.parametrize("mode", ["nvfp4", "mxfp4", "mxfp8"])
 @pytest.mark.parametrize("M,N,K", [(1, 256, 1024), (5, 96, 512), (300, 64, 384)])
 def test_qmm_fp_modes(dev, mode, M, N, K):
