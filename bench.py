@@ -315,13 +315,12 @@ def moe_layer(torch, mi, dev, cfg, E, hidden, inter, k, Ts, n_routes=16, steps=1
             xs = x.view(T, 1, hidden)
             g = mi.gather_qmm(xs, *G, lhs_indices=lhs, rhs_indices=srt, group_size=gs,
                               bits=bits, sorted_indices=True)
-            u = mi.gather_qmm(xs, *U, lhs_indices=lhs, rhs_indices=srt, group_size=gs,
-                              bits=bits, sorted_indices=True)
-            a = mi.swiglu(g, u)
+            # up with SwiGLU applied as it writes; the un-sort rides in the slot reduce
+            a = mi.gather_qmm_swiglu(g, xs, *U, lhs_indices=lhs, rhs_indices=srt,
+                                     group_size=gs, bits=bits, sorted_indices=True)
             v = mi.gather_qmm(a, *D, rhs_indices=srt, group_size=gs, bits=bits,
                               sorted_indices=True)
-            v = mi.take_rows(v.view(T * k, hidden), inv)
-            return mi.moe_down_reduce(v.view(T, k, hidden), sc)
+            return mi.moe_down_reduce_rows(v.view(T * k, hidden), inv, sc)
 
         def all_routes():
             for r in range(n_routes):

@@ -187,6 +187,19 @@ int mi_moe_sort_dispatch(uint32_t* order, uint32_t* inv, uint32_t* sorted, uint3
 /* Replaces mlx_take_axis(axis 0) on row-major rows, as used to undo the expert sort
  * (src/transformer.zig:15037): out[r] = in[indices[r]]; rows of row_bytes bytes; indices
  * >= n_src give zero rows. n <= 65535 rows per call. */
+/* mi_gather_qmm followed by mi_swiglu(gate, product) in one call: the up projection of the
+ * sorted MoE path and its activation (src/transformer.zig:15009-15023), with the SwiGLU of :19846-19884 applied
+ * as the product is written. gate has y's shape ([n_idx, M, N] bf16) and must not alias y.
+ * Affine 4- and 8-bit weights, bf16 activations; other arguments as mi_gather_qmm.
+ * Bit-equal to the two calls. */
+int mi_gather_qmm_swiglu(void* y, const void* gate, const void* x, const uint32_t* w,
+                         const void* scales, const void* biases, const uint32_t* lhs_indices,
+                         const uint32_t* rhs_indices, int64_t n_idx, int64_t lhs_div,
+                         int64_t x_batch, int64_t M, int64_t N, int64_t K, int64_t n_experts,
+                         bool transpose, mi_optional_int group_size, mi_optional_int bits,
+                         const char* mode, bool sorted_indices, int x_dtype, int sb_dtype,
+                         void* stream);
+
 int mi_take_rows(void* out, const void* in, const uint32_t* indices, int64_t n, int64_t n_src,
                  int64_t row_bytes, void* stream);
 
@@ -201,6 +214,14 @@ int mi_swiglu(void* y, const void* gate, const void* up, int64_t n, int dtype, v
  * bf16, from bf16 zero. v [T*k, N], scores [T*k], y [T, N]; bfloat16 only. */
 int mi_moe_down_reduce(void* y, const void* v, const void* scores, int64_t T, int k, int64_t N,
                        int dtype, void* stream);
+
+/* mi_take_rows(v, rows) followed by mi_moe_down_reduce in one pass: the un-sort of the
+ * sorted dispatch (src/transformer.zig:15037) rides in the reduce (:15127-15140).
+ * v [n_rows, N], rows [T*k] (uint32; an index >= n_rows reads as a zero row, as
+ * mi_take_rows gives), scores [T*k], y [T, N]; bfloat16 only. Bit-equal to the two calls. */
+int mi_moe_down_reduce_rows(void* y, const void* v, const void* scores, const uint32_t* rows,
+                            int64_t n_rows, int64_t T, int k, int64_t N, int dtype,
+                            void* stream);
 
 /* Replaces gatherQmvGateUp (src/transformer.zig:20303-20396): for each token t and slot s,
  * g = x[t] @ dequant(w_gate[inds[t*k+s]])^T and u likewise, each rounded to bf16, then

@@ -698,6 +698,43 @@ int mi_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
   return gather_launch(J, data, s);
 }
 
+int mi_gather_qmm_swiglu(void* y, const void* gate, const void* x, const uint32_t* w,
+                         const void* scales, const void* biases, const uint32_t* lhs_indices,
+                         const uint32_t* rhs_indices, int64_t n_idx, int64_t lhs_div,
+                         int64_t x_batch, int64_t M, int64_t N, int64_t K, int64_t n_experts,
+                         bool transpose, mi_optional_int group_size, mi_optional_int bits,
+                         const char* mode, bool sorted_indices, int x_dtype, int sb_dtype,
+                         void* stream) {
+  if (fp_mode_of(mode) >= 0 || (bits.has_value && bits.value != 4 && bits.value != 8))
+    return fail(MI_ERR_UNSUPPORTED, "gather_qmm_swiglu: affine 4- and 8-bit weights only");
+  if (x_dtype != MI_DTYPE_BFLOAT16)
+    return fail(MI_ERR_UNSUPPORTED, "gather_qmm_swiglu: bf16 activations only");
+  GatherJob J;
+  int rc = gather_prepare(J, y, x, w, scales, biases, lhs_indices, rhs_indices, n_idx, lhs_div,
+                          x_batch, M, N, K, n_experts, transpose, group_size, bits, mode,
+                          sorted_indices, x_dtype, sb_dtype);
+  if (rc || J.empty) return rc;
+  if (!gate) return fail(MI_ERR_INVALID, "null gate pointer");
+  if (gate == y) return fail(MI_ERR_INVALID, "gate must not alias y");
+  hipStream_t s = (hipStream_t)stream;
+  void* data = nullptr;
+  if (J.ws_bytes()) {
+    rc = workspace(s, J.ws_bytes(), &data);
+    if (rc) return rc;
+  }
+  // The grouped, one-row and few-row kernels (and the K-split reduce behind them) apply
+  // SwiGLU as they write; the tile kernels write the product and a SwiGLU pass follows,
+  // in place (each element is read and written by one thread).
+  if (J.grouped || J.one_row || J.multi_row) {
+    J.P.swiglu_gate = (const uint16_t*)gate;
+    return gather_launch(J, data, s);
+  }
+  if ((rc = gather_launch(J, data, s)) != MI_OK) return rc;
+  hipError_t e = mi::launch_swiglu((uint16_t*)y, (const uint16_t*)gate, (const uint16_t*)y,
+                                   n_idx * M * N, s);
+  return e == hipSuccess ? MI_OK : hip_fail(e, "swiglu launch");
+}
+
 int mi_gather_qmm_noalloc(void* y, const void* x, const uint32_t* w, const void* scales,
                           const void* biases, const uint32_t* lhs_indices,
                           const uint32_t* rhs_indices, int64_t n_idx, int64_t lhs_div,
@@ -1160,6 +1197,19 @@ int mi_moe_down_reduce(void* y, const void* v, const void* scores, int64_t T, in
   if (!y || !v || !scores) return fail(MI_ERR_INVALID, "null tensor pointer");
   hipError_t e = mi::launch_down_reduce((uint16_t*)y, (const uint16_t*)v, (const uint16_t*)scores,
                                         T, k, N, (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : hip_fail(e, "down_reduce launch");
+}
+
+int mi_moe_down_reduce_rows(void* y, const void* v, const void* scores, const uint32_t* rows,
+                            int64_t n_rows, int64_t T, int k, int64_t N, int dtype,
+                            void* stream) {
+  if (dtype != MI_DTYPE_BFLOAT16) return fail(MI_ERR_UNSUPPORTED, "dtype %d not supported", dtype);
+  if (T < 0 || k <= 0 || N < 0 || n_rows < 0) return fail(MI_ERR_INVALID, "bad T/k/N/n_rows");
+  if (T == 0 || N == 0) return MI_OK;
+  if (T > 65535) return fail(MI_ERR_UNSUPPORTED, "more than 65535 tokens per call");
+  if (!y || !v || !scores || !rows) return fail(MI_ERR_INVALID, "null tensor pointer");
+  hipError_t e = mi::launch_down_reduce((uint16_t*)y, (const uint16_t*)v, (const uint16_t*)scores,
+                                        T, k, N, (hipStream_t)stream, rows, n_rows);
   return e == hipSuccess ? MI_OK : hip_fail(e, "down_reduce launch");
 }
 

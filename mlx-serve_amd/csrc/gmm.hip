@@ -196,31 +196,71 @@ __global__ void __launch_bounds__(64 * WV, 8 / WV) gmm_kernel(QmvParams P) {
 
     // epilogue: acc[.][i] register r is D[n = 32 wave + 8(r/4) + 4h + r%4][m = 32 i + fr]
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      const int m = 32 * i + fr;
-      const int64_t ro = rowtab[m];
-      if (ro == -1) continue;
-      const int64_t pos = it.pos0 + m;
-      const bool nan = ro == -2 || !eok;
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + 32 * wave + 8 * g + 4 * h;
-        if (n >= N) continue;
-        float v[4];
+      for (int r = 0; r < 16; ++r) acc[0][i][r] += acc[1][i][r];
+    if (P.swiglu_gate) {
+      // SwiGLU epilogue through LDS: the bf16 products go to a [R][kNT] tile in the x ring
+      // (row stride kNT + 4 halves, so the 32 rows one store instruction covers fall in
+      // distinct banks), the accumulators die, and every thread then takes 4 adjacent
+      // outputs of a row: coalesced gate reads and output writes, and the SwiGLU math
+      // runs with the loop's registers free.
+      constexpr int kTS = kNT + 4;
+      uint16_t* tile = reinterpret_cast<uint16_t*>(smem);
+      __syncthreads();  // every wave is done reading the x ring
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          v[q] = nan ? __builtin_nanf("") : acc[0][i][4 * g + q] + acc[1][i][4 * g + q];
-        uint16_t* y = reinterpret_cast<uint16_t*>(P.y) + pos * N + n;
-        if (P.swiglu_gate) {
-          const uint16_t* gt = P.swiglu_gate + pos * N + n;
+      for (int i = 0; i < MT; ++i)
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            y[q] = swiglu_bf16(gt[q], (uint16_t)f32_to_bf16_bits(v[q]));
-        } else {
+        for (int g = 0; g < 4; ++g) {
+          u32x2_t o;
+          o.x = pack_bf16x2(acc[0][i][4 * g], acc[0][i][4 * g + 1]);
+          o.y = pack_bf16x2(acc[0][i][4 * g + 2], acc[0][i][4 * g + 3]);
+          *reinterpret_cast<u32x2_t*>(tile + (32 * i + fr) * kTS + 32 * wave + 8 * g + 4 * h) = o;
+        }
+      __syncthreads();
+      constexpr int kPerRow = kNT / 4, kRowsPerPass = kThreads / kPerRow;
+      const int c4 = tid % kPerRow;
+      const int n = n0 + 4 * c4;
+#pragma unroll 1
+      for (int m = tid / kPerRow; m < R; m += kRowsPerPass) {
+        const int64_t ro = rowtab[m];
+        if (ro == -1 || n >= N) continue;
+        const int64_t pos = it.pos0 + m;
+        const u32x2_t gt = *reinterpret_cast<const u32x2_t*>(P.swiglu_gate + pos * N + n);
+        u32x2_t pv = *reinterpret_cast<const u32x2_t*>(tile + m * kTS + 4 * c4);
+        if (ro == -2 || !eok) pv.x = pv.y = 0x7FC07FC0u;  // NaN rows, as the plain path
+        const uint32_t gw[2] = {gt.x, gt.y}, pw[2] = {pv.x, pv.y};
+        uint32_t o[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const uint32_t lo = swiglu_bf16((uint16_t)(gw[q] & 0xFFFFu), (uint16_t)(pw[q] & 0xFFFFu));
+          const uint32_t hi = swiglu_bf16((uint16_t)(gw[q] >> 16), (uint16_t)(pw[q] >> 16));
+          o[q] = lo | (hi << 16);
+        }
+        u32x2_t ov;
+        ov.x = o[0];
+        ov.y = o[1];
+        *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint16_t*>(P.y) + pos * N + n) = ov;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int m = 32 * i + fr;
+        const int64_t ro = rowtab[m];
+        if (ro == -1) continue;
+        const int64_t pos = it.pos0 + m;
+        const bool nan = ro == -2 || !eok;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + 32 * wave + 8 * g + 4 * h;
+          if (n >= N) continue;
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = nan ? __builtin_nanf("") : acc[0][i][4 * g + q];
           u32x2_t o;
           o.x = pack_bf16x2(v[0], v[1]);
           o.y = pack_bf16x2(v[2], v[3]);
-          *reinterpret_cast<u32x2_t*>(y) = o;
+          *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint16_t*>(P.y) + pos * N + n) = o;
         }
       }
     }

@@ -2,6 +2,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include "sigmoid_edges.h"
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -45,21 +46,46 @@ MI_DEV uint16_t bf16_mul(uint16_t a, uint16_t b) {
   return (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(a) * bf16_bits_to_f32(b));
 }
 
-// Sigmoid of a bf16 value, rounded once to fp32 from a double evaluation and then to
-// bf16: the correctly rounded table value for all but astronomically rare inputs.
-// Fast path: the fp32 evaluation 1/(1+expf(-v)) is within 3 fp32 ulp of that fp32
-// rounding (expf <= 1 ulp, the add and the correctly rounded divide 0.5 ulp each), so both
-// round to the same bf16 unless a bf16 rounding midpoint (low 16 bits 0x8000) lies within
-// 8 ulp of it; those values, and v <= -80 (where expf(-v) overflows while the true value
-// is still a representable fp32), take the double evaluation.
+// Sigmoid of a bf16 value v: bf16(fp32(1 / (1 + exp(-v)))), the inner expression in
+// double, as the reference's table over every bf16 pattern. Fast path: e = 2^t with
+// t = -v*log2(e) split Cody-Waite style into hi + lo (hi = fl(-v*L), lo the exact fma
+// residual plus -v times L's own error), so e = exp2(hi) * (1 + lo*ln2) is within about
+// 2 fp32 ulp (v_exp_f32 1 ulp, the correction fma 0.5 ulp); 1 + e adds 0.5 ulp and
+// v_rcp_f32 1 ulp. Rounded to bf16 directly, that value is right unless a bf16 rounding
+// midpoint (low 16 bits 0x8000) lies within a few ulp of it. So when it lies within 8 ulp
+// of one, or v < -80 (the fp32 exponential overflows while the true value is a tiny fp32),
+// the answer comes from the edge tables: kSigmoidEdgesNear holds every input whose
+// correctly rounded fp32 sigmoid lies within kSigmoidEdgeUlp (48) ulp of a midpoint,
+// kSigmoidEdgesTail every input below -80 with a nonzero result. An input in the window but not listed is > 48 ulp from a midpoint, so the
+// fast value rounds right; one below -80 not listed has the result +0. The result depends
+// on the bf16 input alone, so a pass over all 65536 inputs checks every case.
 MI_DEV uint16_t sigmoid_bf16(uint16_t g) {
   const float vf = bf16_bits_to_f32(g);
-  const float sf = 1.f / (1.f + expf(-vf));
-  const uint32_t lo = __float_as_uint(sf) & 0xFFFFu;
-  if (vf > -80.f && lo - (0x8000u - 8u) > 16u) return (uint16_t)f32_to_bf16_bits(sf);
-  const double v = (double)vf;
-  const float s = (float)(1.0 / (1.0 + exp(-v)));
-  return (uint16_t)f32_to_bf16_bits(s);
+  constexpr float kL = 1.44269502162933349609375f;  // fl(log2 e)
+  constexpr float kLerr = 1.925963033500011e-08f;    // log2 e - kL
+  constexpr float kLn2 = 0.693147182464599609375f;
+  // |v| > 100 saturates (1 above; below -80 the table decides), and keeps hi finite
+  const float nv = __builtin_fminf(__builtin_fmaxf(-vf, -100.f), 100.f);
+  const float hi = nv * kL;
+  const float lo = __builtin_fmaf(nv, kL, -hi) + nv * kLerr;
+  const float e0 = __builtin_amdgcn_exp2f(hi);
+  const float e = __builtin_fmaf(e0, lo * kLn2, e0);
+  const float sf = __builtin_amdgcn_rcpf(1.f + e);
+  const uint32_t lo16 = __float_as_uint(sf) & 0xFFFFu;
+  if (vf >= -80.f && lo16 - (0x8000u - 8u) > 16u) return (uint16_t)f32_to_bf16_bits(sf);
+  if (vf != vf) return (uint16_t)f32_to_bf16_bits(vf);  // NaN in, quiet NaN out
+  // scans of the short tables: compares with immediates and selects, no loads
+  uint32_t r = vf < -80.f ? 0u : f32_to_bf16_bits(sf);
+  if (vf < -80.f) {
+#pragma unroll
+    for (int i = 0; i < kSigmoidEdgeTailCount; ++i)
+      r = (kSigmoidEdgesTail[i] >> 16) == (uint32_t)g ? (kSigmoidEdgesTail[i] & 0xFFFFu) : r;
+  } else {
+#pragma unroll
+    for (int i = 0; i < kSigmoidEdgeNearCount; ++i)
+      r = (kSigmoidEdgesNear[i] >> 16) == (uint32_t)g ? (kSigmoidEdgesNear[i] & 0xFFFFu) : r;
+  }
+  return (uint16_t)r;
 }
 
 // SwiGLU with the bf16 rounding points of the reference (src/transformer.zig:19846-19884):

@@ -132,7 +132,8 @@ hipError_t launch_take_rows(void* out, const void* in, const uint32_t* idx, int6
 hipError_t launch_swiglu(uint16_t* y, const uint16_t* g, const uint16_t* u, int64_t n,
                          hipStream_t s);
 hipError_t launch_down_reduce(uint16_t* y, const uint16_t* v, const uint16_t* scores, int64_t T,
-                              int k, int64_t N, hipStream_t s);
+                              int k, int64_t N, hipStream_t s, const uint32_t* rows = nullptr,
+                              int64_t n_rows = 0);
 // nvfp4 (mode 0) / mxfp4 (1) / mxfp8 (2) dequantize, uint8 scales, no biases (quant.hip).
 hipError_t launch_dequantize_fp(void* out, const uint32_t* w, const uint8_t* s, int64_t rows,
                                 int64_t K, int mode, int out_f32, const float* gscale, hipStream_t st);

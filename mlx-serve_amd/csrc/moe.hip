@@ -314,16 +314,23 @@ __global__ void swiglu_kernel(uint16_t* __restrict__ y, const uint16_t* __restri
 
 // y[t, n] = sum over slots s ascending of bf16(v[t*k+s, n] * score[t*k+s]), each add
 // rounded to bf16, starting from bf16 zero.
+// rows (nullable): v's row of pair p is rows[p] (the inverse of the expert sort), so the
+// unsort rides in the reduce; a row index >= n_rows reads as zeros, as take_rows returns.
+// The bf16 score product and the slot sum are those of down_reduce_kernel, so the result is
+// bit-equal to take_rows followed by the plain reduce.
 __global__ void down_reduce_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ v,
-                                   const uint16_t* __restrict__ scores, int64_t T, int k,
-                                   int64_t N) {
+                                   const uint16_t* __restrict__ scores,
+                                   const uint32_t* __restrict__ rows, int64_t n_rows,
+                                   int64_t T, int k, int64_t N) {
   const int64_t t = blockIdx.y;
   for (int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; n < N;
        n += (int64_t)gridDim.x * blockDim.x) {
     uint16_t total = 0;
     for (int s = 0; s < k; ++s) {
       const int64_t p = t * k + s;
-      total = bf16_add(total, bf16_mul(v[p * N + n], scores[p]));
+      const int64_t src = rows ? (int64_t)rows[p] : p;
+      const uint16_t x = src < n_rows ? v[src * N + n] : (uint16_t)0;
+      total = bf16_add(total, bf16_mul(x, scores[p]));
     }
     y[t * N + n] = total;
   }
@@ -331,15 +338,18 @@ __global__ void down_reduce_kernel(uint16_t* __restrict__ y, const uint16_t* __r
 
 // 8 outputs per thread with 16-byte loads (N % 8 == 0, 16-byte aligned rows).
 __global__ void down_reduce8_kernel(u32x4_t* __restrict__ y, const u32x4_t* __restrict__ v,
-                                    const uint16_t* __restrict__ scores, int64_t T, int k,
-                                    int64_t N8) {
+                                    const uint16_t* __restrict__ scores,
+                                    const uint32_t* __restrict__ rows, int64_t n_rows,
+                                    int64_t T, int k, int64_t N8) {
   const int64_t t = blockIdx.y;
   for (int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; n < N8;
        n += (int64_t)gridDim.x * blockDim.x) {
     u32x4_t total = {0u, 0u, 0u, 0u};
     for (int s = 0; s < k; ++s) {
       const int64_t p = t * k + s;
-      const u32x4_t x = v[p * N8 + n];
+      const int64_t src = rows ? (int64_t)rows[p] : p;
+      const u32x4_t zero = {0u, 0u, 0u, 0u};
+      const u32x4_t x = src < n_rows ? v[src * N8 + n] : zero;
       const uint16_t sc = scores[p];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -438,15 +448,17 @@ hipError_t launch_swiglu(uint16_t* y, const uint16_t* g, const uint16_t* u, int6
 }
 
 hipError_t launch_down_reduce(uint16_t* y, const uint16_t* v, const uint16_t* scores, int64_t T,
-                              int k, int64_t N, hipStream_t s) {
+                              int k, int64_t N, hipStream_t s, const uint32_t* rows,
+                              int64_t n_rows) {
+  if (!rows) n_rows = T * k;
   if (T == 0 || N == 0) return hipSuccess;
   if (N % 8 == 0 && ((uintptr_t)y | (uintptr_t)v) % 16 == 0) {
     hipLaunchKernelGGL(down_reduce8_kernel, dim3(grid_for(N / 8, 256), (unsigned)T), dim3(256), 0,
-                       s, (u32x4_t*)y, (const u32x4_t*)v, scores, T, k, N / 8);
+                       s, (u32x4_t*)y, (const u32x4_t*)v, scores, rows, n_rows, T, k, N / 8);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(down_reduce_kernel, dim3(grid_for(N, 256), (unsigned)T), dim3(256), 0, s, y,
-                     v, scores, T, k, N);
+                     v, scores, rows, n_rows, T, k, N);
   return hipGetLastError();
 }
 

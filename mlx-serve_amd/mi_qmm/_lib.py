@@ -61,6 +61,8 @@ def lib():
     L.mi_gather_qmv_down_reduce.argtypes = [P, P, P, P, P, P, P, i64, i32, i64, i64, i64, OptInt,
                                             OptInt, s, P]
     L.mi_gather_qmm_noalloc.argtypes = L.mi_gather_qmm.argtypes
+    L.mi_gather_qmm_swiglu.argtypes = [P] + L.mi_gather_qmm.argtypes
+    L.mi_moe_down_reduce_rows.argtypes = [P, P, P, P, i64, i64, i32, i64, i32, P]
     L.mi_moe_route_grouped.argtypes = [P, P, P, P, i64, i64, i32, i32, i32, b, ctypes.c_float, P]
     L.mi_moe_route_gate_up_swiglu.argtypes = [P, P, P, P, P, P, P, P, P, P, P, i64, i64, i32,
                                               i64, i64, OptInt, OptInt, s, i32, P]

@@ -153,6 +153,32 @@ def gather_qmm(x, w, scales, biases, lhs_indices=None, rhs_indices=None, transpo
     return y
 
 
+def gather_qmm_swiglu(gate, x, w, scales, biases, lhs_indices=None, rhs_indices=None,
+                      transpose=True, group_size=None, bits=None, mode="affine",
+                      sorted_indices=False):
+    """swiglu(gate, gather_qmm(x, w, ...)) in one call (the sorted MoE up projection and
+    its activation, src/transformer.zig:15009-15023); gate has the product's shape."""
+    _contig(gate, x, w, scales, biases)
+    _require(x.dim() >= 2 and w.dim() >= 2, "x and w need at least 2 dims")
+    K = x.shape[-1]
+    M = x.shape[-2]
+    gs, nb = _resolve(_packed(w), scales, group_size, bits, K, mode)
+    N = w.shape[-2]
+    lhs, lhs_div, rhs, shape = _broadcast_indices(x, w, lhs_indices, rhs_indices)
+    n_idx = math.prod(shape)
+    x_batch = x.numel() // (M * K) if M * K else 0
+    n_exp = w.numel() // (N * w.shape[-1]) if N * w.shape[-1] else 0
+    y = torch.empty(tuple(shape) + (M, N), dtype=x.dtype, device=x.device)
+    _require(gate.numel() == y.numel() and gate.dtype == x.dtype, "gate must match the product")
+    check(lib().mi_gather_qmm_swiglu(_ptr(y), _ptr(gate), _ptr(x), _ptr(w), _ptr(scales),
+                                     _ptr(biases), _ptr(lhs), _ptr(rhs), n_idx, lhs_div, x_batch,
+                                     M, N, K, n_exp, bool(transpose), opt(gs), opt(nb),
+                                     mode.encode() if mode else None, bool(sorted_indices),
+                                     _dtype_code(x, "x"), _dtype_code(scales, "scales"),
+                                     _stream(x)))
+    return y
+
+
 def dequantize(w, scales, biases, group_size=None, bits=None, mode="affine", dtype=None,
                rounding=None, global_scale=None):
     """mlx_dequantize (src/mlx.zig:271). dtype defaults to the scales dtype.
@@ -279,6 +305,20 @@ def moe_down_reduce(v, scores):
     y = torch.empty((T, N), dtype=v.dtype, device=v.device)
     check(lib().mi_moe_down_reduce(_ptr(y), _ptr(v), _ptr(scores), T, k, N,
                                    _dtype_code(v, "v"), _stream(v)))
+    return y
+
+
+def moe_down_reduce_rows(v, rows, scores):
+    """moe_down_reduce(take_rows(v, rows).view(T, k, N), scores) in one pass: v [R, N],
+    rows [T*k] (the inverse permutation of the sorted dispatch), scores [T, k] -> [T, N]."""
+    _contig(v, rows, scores)
+    T, k = scores.shape
+    N = v.shape[-1]
+    _require(rows.numel() == T * k, "rows must hold T*k entries")
+    y = torch.empty((T, N), dtype=v.dtype, device=v.device)
+    check(lib().mi_moe_down_reduce_rows(_ptr(y), _ptr(v), _ptr(scores), _ptr(rows),
+                                        v.numel() // N if N else 0, T, int(k), N,
+                                        _dtype_code(v, "v"), _stream(v)))
     return y
 
 

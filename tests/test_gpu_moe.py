@@ -316,3 +316,48 @@ def test_fused_decode_mlp_fp_modes(dev, mode, T):
             h = gg / (1.0 + np.exp(-gg)) * uu
             want[t] += scf[t, j] * (h @ deq(wd, sd, e).T)
     assert max_err_ratio(to_f64(y), want) <= 3 * BF16_TOL
+
+
+@pytest.mark.parametrize("T,E,k,N,K", [(512, 16, 4, 256, 512), (3, 16, 2, 192, 512),
+                                       (64, 128, 8, 768, 2048), (40, 8, 2, 100, 256)])
+def test_sorted_up_swiglu_and_unsort_reduce_match_split(dev, T, E, k, N, K):
+    """The fused sorted-path entries equal the split calls bit for bit: gather_qmm_swiglu ==
+    swiglu(gate, gather_qmm) (grouped kernel at T=512, the few-row kernels at small T, the
+    tile kernel at N=100), and moe_down_reduce_rows == moe_down_reduce(take_rows(v, inv))."""
+    _print_case(t="sorted_fused", T=T, E=E, k=k, N=N, K=K)
+    logits = torch.from_numpy(O.randn(T * E, 31).reshape(T, E)).to(dev)
+    inds, sc = mi_qmm.moe_route_topk(logits, k, torch.bfloat16)
+    order, inv, srt, lhs, seg = mi_qmm.moe_sort_dispatch(inds.reshape(-1), k, E)
+    D = lambda *a: [to_dev_u32(a[0], dev), to_dev_bf16(a[1], dev), to_dev_bf16(a[2], dev)]  # noqa
+    G, U = D(*_bank(E, N, K, 32)), D(*_bank(E, N, K, 33))
+    x = to_dev_bf16(O.make_x_bf16(T, K, 34), dev).reshape(T, 1, K)
+    kw = dict(lhs_indices=lhs, rhs_indices=srt, group_size=64, bits=4, sorted_indices=True)
+    g = mi_qmm.gather_qmm(x, *G, **kw)
+    u = mi_qmm.gather_qmm(x, *U, **kw)
+    split = mi_qmm.swiglu(g, u)
+    fused = mi_qmm.gather_qmm_swiglu(g, x, *U, **kw)
+    assert torch.equal(fused.view(torch.int16), split.view(torch.int16))
+    v = to_dev_bf16(O.make_x_bf16(T * k, N, 35), dev)
+    ref = mi_qmm.moe_down_reduce(mi_qmm.take_rows(v, inv).view(T, k, N), sc)
+    got = mi_qmm.moe_down_reduce_rows(v, inv, sc)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    bad = inv.clone()
+    bad[1] = T * k + 7                      # out of range: a zero row, as take_rows gives
+    ref = mi_qmm.moe_down_reduce(mi_qmm.take_rows(v, bad).view(T, k, N), sc)
+    got = mi_qmm.moe_down_reduce_rows(v, bad, sc)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+def test_gather_qmm_swiglu_unsorted_tile_kernel(dev):
+    """Unsorted 16-row pairs run on the tile kernels, which write the product and then apply
+    SwiGLU in place: still bit-equal to the two calls."""
+    _print_case(t="swiglu_tile")
+    E, N, K, n = 6, 256, 512, 5
+    W = [to_dev_u32(a, dev) if i == 0 else to_dev_bf16(a, dev)
+         for i, a in enumerate(_bank(E, N, K, 36))]
+    x = to_dev_bf16(O.make_x_bf16(n * 16, K, 37), dev).reshape(n, 16, K)
+    rhs = torch.tensor([3, 0, 5, 3, 1], dtype=torch.int32, device=dev)
+    gate = to_dev_bf16(O.make_x_bf16(n * 16, N, 38), dev).reshape(n, 16, N)
+    up = mi_qmm.gather_qmm(x, *W, rhs_indices=rhs, group_size=64, bits=4)
+    fused = mi_qmm.gather_qmm_swiglu(gate, x, *W, rhs_indices=rhs, group_size=64, bits=4)
+    assert torch.equal(fused.view(torch.int16), mi_qmm.swiglu(gate, up).view(torch.int16))
