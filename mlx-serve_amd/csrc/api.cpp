@@ -361,7 +361,9 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
       if (mu >= gmm_min) {
         const double want = mu + 3.0 * std::sqrt(mu);
         J.grouped = true;
-        J.gmm_mt = want <= 32 ? 1 : 2;  // longer runs are cut into 64-row items
+        static const int force_mt = env_int("MI_QMM_GMM_MT", 0);
+        J.gmm_mt = force_mt == 1 || force_mt == 2 ? force_mt
+                   : want <= 32 ? 1 : 2;  // longer runs are cut into 64-row items
       }
     }
     J.narrow = q16 && avg <= 4;

@@ -23,6 +23,12 @@
 // exact vmcnt (the younger steps' loads only) publishes its x tile; the barrier waits on
 // LDS traffic only. Chunked scale loads matter: one 2-byte load per lane per step made the
 // L2 serve ~7.8 M requests per 113 MB projection and cost 10%.
+// Occupancy: three 4-wave blocks per CU (<= 168 VGPRs, a 4-deep ring of 32 KB) so that a
+// configs[3] T=512 projection's 768 (item, weight tile) blocks run in one round. With two
+// blocks per CU (8-deep ring) the second round ran on half the chip, and every block's first
+// step waited ~5 us behind the whole launch's initial loads (per-block s_memrealtime stamps);
+// a 4-deep ring measured no slower than the 8-deep one. The dequantize of step t + 1 is
+// interleaved with step t's MFMAs (it needs registers only).
 #include <algorithm>
 
 #include "dequant_bf16.h"
@@ -42,7 +48,7 @@ using qmv_detail::mfma32;
 using qmv_detail::vmcnt_imm;
 
 constexpr int kOOB = 0x7FFFFFF0;  // buffer offset past any x: the load returns 0, no traffic
-constexpr int kD = 8;        // steps in flight: LDS ring of x tiles, register ring of weights
+constexpr int kD = 4;        // steps in flight: LDS ring of x tiles, register ring of weights
 constexpr int kBufFlags = 0x00020000;
 
 MI_DEV u32x4_t ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
@@ -64,18 +70,18 @@ MI_DEV uint32_t xor32_u32(uint32_t v, int lane) {
 }
 
 template <int MT, int WV>
-__global__ void __launch_bounds__(64 * WV, 8 / WV) gmm_kernel(QmvParams P) {
+__global__ void __launch_bounds__(64 * WV, 12 / WV) gmm_kernel(QmvParams P) {
   constexpr int R = 32 * MT, kNT = 32 * WV, kThreads = 64 * WV;
-  // x DMA instructions per thread per step: R rows x 128 B over kThreads lanes x 16 B
-  constexpr int XU = R * 8 / kThreads;
-  static_assert(XU >= 1 && XU * kThreads == R * 8, "x tile must split evenly over the lanes");
-  constexpr int kN = XU + 1;  // VMEM instructions per step: x DMA and weights (+1 per chunk)
   // Dynamic LDS: the x ring (kD stages of R rows x 128 B), then the row table. (With a
   // static array the compiler would drain every load before each LDS read that may alias
   // an LDS DMA; the waits here are exact and explicit.)
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int kStage = R * 128;
   int64_t* rowtab = reinterpret_cast<int64_t*>(smem + kD * kStage);
+  // x DMA instructions per thread per step: R rows x 128 B over kThreads lanes x 16 B
+  constexpr int XU = R * 8 / kThreads;
+  static_assert(XU >= 1 && XU * kThreads == R * 8, "x tile must split evenly over the lanes");
+  constexpr int kN = XU + 1;  // VMEM instructions per step: x DMA and weights (+1 per chunk)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, h = lane >> 5;
@@ -130,44 +136,55 @@ __global__ void __launch_bounds__(64 * WV, 8 / WV) gmm_kernel(QmvParams P) {
       __builtin_amdgcn_sched_barrier(0);
     };
 
-    f32x16_t acc[2][MT];
+    f32x16_t acc[MT];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[a][i][r] = 0.f;
+      for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
 
     if (eok) {
-      // step t: wait for its DMA (issued kD - 1 steps earlier), barrier, compute(t), then
-      // issue step t + kD - 1 into the stage step t - 1 freed. Unrolled by 16 (two rings,
-      // four scale chunks) so every register slot is static.
+      // step t: wait for its DMA (issued kD - 1 steps earlier) and for step t + 1's weights,
+      // barrier, then the MFMAs of step t with step t + 1's dequantize interleaved (it needs
+      // registers only: the weight ring and the scale chunk), then issue step t + kD - 1
+      // into the stage step t - 1 freed. Unrolled by 16 (four scale chunks) so every
+      // register slot is static.
 #pragma unroll
       for (int j = 0; j < kD - 1; ++j) issue(j, j, (j >> 2) & 3);
+      // step j's scale and bias (group j % 4 of chunk slot (j / 4) % 4)
+      auto scale_bias = [&](int j, float& sc, float& bp) __attribute__((always_inline)) {
+        const u32x2_t mine = sbc[(j >> 2) & 3];
+        const uint32_t mw = (j & 2) ? mine.y : mine.x;
+        const uint32_t ow = xor32_u32(mw, lane);
+        const uint32_t sw = h ? ow : mw, bw = h ? mw : ow;
+        sc = __uint_as_float((j & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
+        bp = __uint_as_float((j & 1) ? (bw & 0xFFFF0000u) : (bw << 16));
+      };
+      u32x4_t A[4];
+      {
+        // step 0's weights and scale chunk: everything after them may stay in flight
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(XU + (kD - 2) * kN + (kD - 2) / 4));
+        float sc, bp;
+        scale_bias(0, sc, bp);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) A[ks] = dequant8(wq[0][ks], sc, bp);
+      }
       for (int t0 = 0; t0 < nsteps; t0 += 16) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const int t = t0 + j, js = j % kD;
-          // This step's x DMA is done once only the younger steps' loads (t+1 .. t+kD-2,
-          // kN each plus one per scale chunk they start) are in flight. The barrier waits
-          // on LDS traffic only, so the register loads stay in flight.
-          constexpr int kAfter0 = (kD - 2) * kN;
-          const int starts = ((j + kD - 2) >> 2) - (j >> 2);  // multiples of 4 in j+1..j+kD-2
+          // Done: every load of step t and step t + 1's scale chunk and weights. In flight:
+          // step t + 1's x DMA and steps t + 2 .. t + kD - 2 (kN each plus one per scale
+          // chunk they start). The barrier waits on LDS traffic only.
+          constexpr int kAfter0 = XU + (kD - 3) * kN;
+          const int starts = ((j + kD - 2) >> 2) - ((j + 1) >> 2);  // multiples of 4 in j+2..j+kD-2
           switch (starts) {
+            case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAfter0)); break;
             case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAfter0 + 1)); break;
             default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAfter0 + 2)); break;
           }
           qmv_detail::lds_barrier();
           if (t < nsteps) {
-            // this step's group: t % 4 of chunk slot (t / 4) % 4
-            const u32x2_t mine = sbc[(j >> 2) & 3];
-            const uint32_t mw = (j & 2) ? mine.y : mine.x;
-            const uint32_t ow = xor32_u32(mw, lane);
-            const uint32_t sw = h ? ow : mw, bw = h ? mw : ow;
-            const float sc = __uint_as_float((j & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
-            const float bp = __uint_as_float((j & 1) ? (bw & 0xFFFF0000u) : (bw << 16));
-            // all fragment reads first, the dequantize under their latency, then the MFMAs
-            u32x4_t X[4][MT], A[4];
+            u32x4_t X[4][MT], An[4];
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -176,16 +193,24 @@ __global__ void __launch_bounds__(64 * WV, 8 / WV) gmm_kernel(QmvParams P) {
                 X[ks][i] = *reinterpret_cast<const u32x4_t*>(
                     smem + js * kStage + r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
               }
+            float sc, bp;
+            scale_bias(j + 1, sc, bp);
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) A[ks] = dequant8(wq[js][ks], sc, bp);
+            for (int ks = 0; ks < 4; ++ks) An[ks] = dequant8(wq[(j + 1) % kD][ks], sc, bp);
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
               for (int i = 0; i < MT; ++i)
-                acc[ks & 1][i] = mfma32(A[ks], X[ks][i], acc[ks & 1][i]);
+                acc[i] = mfma32(A[ks], X[ks][i], acc[i]);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) A[ks] = An[ks];
+            // fragment reads first, then each MFMA with a slice of the next dequantize
             __builtin_amdgcn_sched_group_barrier(0x100, 4 * MT, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 76, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 4 * MT, 0);
+#pragma unroll
+            for (int m = 0; m < 4 * MT; ++m) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+              __builtin_amdgcn_sched_group_barrier(0x002, 84 / (4 * MT), 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
           }
           issue(t + kD - 1, (j + kD - 1) % kD, ((j + kD - 1) >> 2) & 3);
@@ -195,10 +220,6 @@ __global__ void __launch_bounds__(64 * WV, 8 / WV) gmm_kernel(QmvParams P) {
     }
 
     // epilogue: acc[.][i] register r is D[n = 32 wave + 8(r/4) + 4h + r%4][m = 32 i + fr]
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[0][i][r] += acc[1][i][r];
     if (P.swiglu_gate) {
       // SwiGLU epilogue through LDS: the bf16 products go to a [R][kNT] tile in the x ring
       // (row stride kNT + 4 halves, so the 32 rows one store instruction covers fall in
@@ -213,8 +234,8 @@ __global__ void __launch_bounds__(64 * WV, 8 / WV) gmm_kernel(QmvParams P) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           u32x2_t o;
-          o.x = pack_bf16x2(acc[0][i][4 * g], acc[0][i][4 * g + 1]);
-          o.y = pack_bf16x2(acc[0][i][4 * g + 2], acc[0][i][4 * g + 3]);
+          o.x = pack_bf16x2(acc[i][4 * g], acc[i][4 * g + 1]);
+          o.y = pack_bf16x2(acc[i][4 * g + 2], acc[i][4 * g + 3]);
           *reinterpret_cast<u32x2_t*>(tile + (32 * i + fr) * kTS + 32 * wave + 8 * g + 4 * h) = o;
         }
       __syncthreads();
@@ -256,7 +277,7 @@ __global__ void __launch_bounds__(64 * WV, 8 / WV) gmm_kernel(QmvParams P) {
           if (n >= N) continue;
           float v[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] = nan ? __builtin_nanf("") : acc[0][i][4 * g + q];
+          for (int q = 0; q < 4; ++q) v[q] = nan ? __builtin_nanf("") : acc[i][4 * g + q];
           u32x2_t o;
           o.x = pack_bf16x2(v[0], v[1]);
           o.y = pack_bf16x2(v[2], v[3]);
@@ -295,8 +316,8 @@ hipError_t launch_mt(const QmvParams& P, int grid_items, hipStream_t s) {
 
 hipError_t launch_gmm(const QmvParams& P, int mt, int grid_items, hipStream_t s) {
   if (!P.items || !P.item_count) return hipErrorInvalidValue;
-  // 4 waves (128 weight rows) a block, two blocks a CU: 256-row blocks of 8 waves measured
-  // 233 against 216 us per configs[3] T=512 layer
+  // 4 waves (128 weight rows) a block, three blocks a CU: 256-row blocks of 8 waves measured
+  // 233 against 216 us per configs[3] T=512 layer (two blocks a CU then)
   switch (mt) {
     case 1: return launch_mt<1, 4>(P, grid_items, s);
     case 2: return launch_mt<2, 4>(P, grid_items, s);
