@@ -313,11 +313,10 @@ def moe_layer(torch, mi, dev, cfg, E, hidden, inter, k, Ts, n_routes=16, steps=1
             inds, sc = mi.moe_route_topk(logits[r], k, torch.bfloat16)
             order, inv, srt, lhs, seg = mi.moe_sort_dispatch(inds.reshape(-1), k, E)
             xs = x.view(T, 1, hidden)
-            g = mi.gather_qmm(xs, *G, lhs_indices=lhs, rhs_indices=srt, group_size=gs,
-                              bits=bits, sorted_indices=True)
-            # up with SwiGLU applied as it writes; the un-sort rides in the slot reduce
-            a = mi.gather_qmm_swiglu(g, xs, *U, lhs_indices=lhs, rhs_indices=srt,
-                                     group_size=gs, bits=bits, sorted_indices=True)
+            # gate and up in one call with SwiGLU applied as it writes; the un-sort rides in
+            # the slot reduce
+            a = mi.gather_qmm_gate_up_swiglu(xs, *G, *U, lhs_indices=lhs, rhs_indices=srt,
+                                             group_size=gs, bits=bits, sorted_indices=True)
             v = mi.gather_qmm(a, *D, rhs_indices=srt, group_size=gs, bits=bits,
                               sorted_indices=True)
             return mi.moe_down_reduce_rows(v.view(T * k, hidden), inv, sc)

@@ -200,6 +200,23 @@ int mi_gather_qmm_swiglu(void* y, const void* gate, const void* x, const uint32_
                          const char* mode, bool sorted_indices, int x_dtype, int sb_dtype,
                          void* stream);
 
+/* Both projections before the activation of the sorted MoE path (src/transformer.zig:
+ * 15009-15023: the gate and up gather_qmm calls and the SwiGLU after them) in one call:
+ * y = SwiGLU(gather_qmm(x, w_gate, ...), gather_qmm(x, w_up, ...)), each product rounded to
+ * bf16 first. Both banks share the indices, shapes and format; arguments otherwise as
+ * mi_gather_qmm. On the grouped kernel this is one launch over both banks; bit-equal to the
+ * split calls (mi_gather_qmm for gate, then mi_gather_qmm_swiglu for up). Affine 4- and
+ * 8-bit weights, bf16 activations. */
+int mi_gather_qmm_gate_up_swiglu(void* y, const void* x, const uint32_t* w_gate,
+                                 const void* s_gate, const void* b_gate, const uint32_t* w_up,
+                                 const void* s_up, const void* b_up,
+                                 const uint32_t* lhs_indices, const uint32_t* rhs_indices,
+                                 int64_t n_idx, int64_t lhs_div, int64_t x_batch, int64_t M,
+                                 int64_t N, int64_t K, int64_t n_experts, bool transpose,
+                                 mi_optional_int group_size, mi_optional_int bits,
+                                 const char* mode, bool sorted_indices, int x_dtype,
+                                 int sb_dtype, void* stream);
+
 int mi_take_rows(void* out, const void* in, const uint32_t* indices, int64_t n, int64_t n_src,
                  int64_t row_bytes, void* stream);
 

@@ -737,6 +737,58 @@ int mi_gather_qmm_swiglu(void* y, const void* gate, const void* x, const uint32_
   return e == hipSuccess ? MI_OK : hip_fail(e, "swiglu launch");
 }
 
+int mi_gather_qmm_gate_up_swiglu(void* y, const void* x, const uint32_t* w_gate,
+                                 const void* s_gate, const void* b_gate, const uint32_t* w_up,
+                                 const void* s_up, const void* b_up,
+                                 const uint32_t* lhs_indices, const uint32_t* rhs_indices,
+                                 int64_t n_idx, int64_t lhs_div, int64_t x_batch, int64_t M,
+                                 int64_t N, int64_t K, int64_t n_experts, bool transpose,
+                                 mi_optional_int group_size, mi_optional_int bits,
+                                 const char* mode, bool sorted_indices, int x_dtype,
+                                 int sb_dtype, void* stream) {
+  if (fp_mode_of(mode) >= 0 || (bits.has_value && bits.value != 4 && bits.value != 8))
+    return fail(MI_ERR_UNSUPPORTED, "gather_qmm_gate_up_swiglu: affine 4- and 8-bit weights only");
+  if (x_dtype != MI_DTYPE_BFLOAT16)
+    return fail(MI_ERR_UNSUPPORTED, "gather_qmm_gate_up_swiglu: bf16 activations only");
+  GatherJob G;
+  int rc = gather_prepare(G, y, x, w_gate, s_gate, b_gate, lhs_indices, rhs_indices, n_idx,
+                          lhs_div, x_batch, M, N, K, n_experts, transpose, group_size, bits,
+                          mode, sorted_indices, x_dtype, sb_dtype);
+  if (rc || G.empty) return rc;
+  if (!w_up || !s_up || !b_up) return fail(MI_ERR_INVALID, "null up-bank pointer");
+  hipStream_t s = (hipStream_t)stream;
+  void* data = nullptr;
+  if (G.grouped) {
+    // one grouped launch: half the waves of a block on each bank, SwiGLU in the epilogue
+    G.P.w2 = w_up;
+    G.P.scales2 = (const uint16_t*)s_up;
+    G.P.biases2 = (const uint16_t*)b_up;
+    G.P.dual = 1;
+    if (G.ws_bytes() && (rc = workspace(s, G.ws_bytes(), &data)) != MI_OK) return rc;
+    return gather_launch(G, data, s);
+  }
+  // otherwise the gate product goes to the workspace and the up gather applies SwiGLU as
+  // mi_gather_qmm_swiglu does
+  GatherJob U;
+  rc = gather_prepare(U, y, x, w_up, s_up, b_up, lhs_indices, rhs_indices, n_idx, lhs_div,
+                      x_batch, M, N, K, n_experts, transpose, group_size, bits, mode,
+                      sorted_indices, x_dtype, sb_dtype);
+  if (rc) return rc;
+  const size_t half = round256((size_t)n_idx * M * N * 2);
+  if ((rc = workspace(s, half + std::max(G.ws_bytes(), U.ws_bytes()), &data)) != MI_OK) return rc;
+  uint16_t* g = (uint16_t*)data;
+  void* rest = (char*)data + half;
+  G.P.y = g;
+  if ((rc = gather_launch(G, rest, s)) != MI_OK) return rc;
+  if (U.grouped || U.one_row || U.multi_row) {
+    U.P.swiglu_gate = g;
+    return gather_launch(U, rest, s);
+  }
+  if ((rc = gather_launch(U, rest, s)) != MI_OK) return rc;
+  hipError_t e = mi::launch_swiglu((uint16_t*)y, g, (const uint16_t*)y, n_idx * M * N, s);
+  return e == hipSuccess ? MI_OK : hip_fail(e, "swiglu launch");
+}
+
 int mi_gather_qmm_noalloc(void* y, const void* x, const uint32_t* w, const void* scales,
                           const void* biases, const uint32_t* lhs_indices,
                           const uint32_t* rhs_indices, int64_t n_idx, int64_t lhs_div,

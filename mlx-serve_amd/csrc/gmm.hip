@@ -69,9 +69,13 @@ MI_DEV uint32_t xor32_u32(uint32_t v, int lane) {
   return (lane & 32) ? r[0] : r[1];
 }
 
-template <int MT, int WV>
+// DUAL (P.dual): the first WV / 2 waves run the gate bank (w, scales, biases) and the others
+// the up bank (w2, scales2, biases2) on the same rows of both and the same x tile; the
+// epilogue writes y = SwiGLU(gate, up) through LDS (each product rounded to bf16 first).
+template <int MT, int WV, bool DUAL>
 __global__ void __launch_bounds__(64 * WV, 12 / WV) gmm_kernel(QmvParams P) {
-  constexpr int R = 32 * MT, kNT = 32 * WV, kThreads = 64 * WV;
+  constexpr int kWT = DUAL ? WV / 2 : WV;  // waves per weight bank
+  constexpr int R = 32 * MT, kNT = 32 * kWT, kThreads = 64 * WV;
   // Dynamic LDS: the x ring (kD stages of R rows x 128 B), then the row table. (With a
   // static array the compiler would drain every load before each LDS read that may alias
   // an LDS DMA; the waits here are exact and explicit.)
@@ -88,7 +92,9 @@ __global__ void __launch_bounds__(64 * WV, 12 / WV) gmm_kernel(QmvParams P) {
   const int N = P.N, K = P.K, G = K / 64, nsteps = K / 64;
   const int n0 = blockIdx.x * kNT;
   const int n_items = (int)*P.item_count;
-  const uint32_t wrow = (uint32_t)min(n0 + 32 * wave + fr, N - 1);
+  const int mw = DUAL ? wave % kWT : wave;     // the wave's 32-row tile in its bank
+  const bool up = DUAL && wave >= kWT;          // wave-uniform
+  const uint32_t wrow = (uint32_t)min(n0 + 32 * mw + fr, N - 1);
   const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
       (void*)P.x, 0, (int)(uint32_t)(P.x_batch * P.M * (int64_t)K * 2), kBufFlags);
 
@@ -102,11 +108,12 @@ __global__ void __launch_bounds__(64 * WV, 12 / WV) gmm_kernel(QmvParams P) {
 
     const size_t mat = (size_t)e * (uint32_t)N;
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(P.w + mat * (uint32_t)(K / 8)), 0, N * (K / 2), kBufFlags);
+        (void*)((up ? P.w2 : P.w) + mat * (uint32_t)(K / 8)), 0, N * (K / 2), kBufFlags);
     const uint32_t wo = wrow * (uint32_t)(K / 2) + 16 * h;
     // lane h = 0 loads its row's scales, h = 1 its biases, 4 groups (8 bytes) at a time; a
     // lane-half swap shares them
-    const uint16_t* sbp = (h ? P.biases : P.scales) + (mat + wrow) * (uint32_t)G;
+    const uint16_t* sbp = (h ? (up ? P.biases2 : P.biases) : (up ? P.scales2 : P.scales)) +
+                          (mat + wrow) * (uint32_t)G;
     const int nch = (nsteps + 3) / 4;
     // x: DMA instruction i of wave w moves rows 8 (XU w + i) .. +7 (8 x 128 B); LDS slot
     // p of row r holds k-slot p ^ ((r >> 1) & 7). Rows outside the item read past the
@@ -219,8 +226,49 @@ __global__ void __launch_bounds__(64 * WV, 12 / WV) gmm_kernel(QmvParams P) {
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no DMA may outlive its stage
     }
 
-    // epilogue: acc[.][i] register r is D[n = 32 wave + 8(r/4) + 4h + r%4][m = 32 i + fr]
-    if (P.swiglu_gate) {
+    // epilogue: acc[i] register r is D[n = 32 mw + 8(r/4) + 4h + r%4][m = 32 i + fr]
+    if constexpr (DUAL) {
+      // gate products in columns [0, kNT) of an LDS tile, up products in [kNT, 2 kNT) (row
+      // stride padded by 4 halves), then every thread takes 4 adjacent outputs of a row
+      constexpr int kTS = 2 * kNT + 4;
+      uint16_t* tile = reinterpret_cast<uint16_t*>(smem);
+      __syncthreads();  // every wave is done reading the x ring
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          u32x2_t o;
+          o.x = pack_bf16x2(acc[i][4 * g], acc[i][4 * g + 1]);
+          o.y = pack_bf16x2(acc[i][4 * g + 2], acc[i][4 * g + 3]);
+          *reinterpret_cast<u32x2_t*>(tile + (32 * i + fr) * kTS + (up ? kNT : 0) + 32 * mw +
+                                      8 * g + 4 * h) = o;
+        }
+      __syncthreads();
+      constexpr int kPerRow = kNT / 4, kRowsPerPass = kThreads / kPerRow;
+      const int c4 = tid % kPerRow;
+      const int n = n0 + 4 * c4;
+#pragma unroll 1
+      for (int m = tid / kPerRow; m < R; m += kRowsPerPass) {
+        const int64_t ro = rowtab[m];
+        if (ro == -1 || n >= N) continue;
+        const int64_t pos = it.pos0 + m;
+        u32x2_t gv = *reinterpret_cast<const u32x2_t*>(tile + m * kTS + 4 * c4);
+        u32x2_t uv = *reinterpret_cast<const u32x2_t*>(tile + m * kTS + kNT + 4 * c4);
+        if (ro == -2 || !eok) gv.x = gv.y = uv.x = uv.y = 0x7FC07FC0u;  // NaN rows
+        const uint32_t gw[2] = {gv.x, gv.y}, uw[2] = {uv.x, uv.y};
+        uint32_t o[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const uint32_t lo = swiglu_bf16((uint16_t)(gw[q] & 0xFFFFu), (uint16_t)(uw[q] & 0xFFFFu));
+          const uint32_t hi = swiglu_bf16((uint16_t)(gw[q] >> 16), (uint16_t)(uw[q] >> 16));
+          o[q] = lo | (hi << 16);
+        }
+        u32x2_t ov;
+        ov.x = o[0];
+        ov.y = o[1];
+        *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint16_t*>(P.y) + pos * N + n) = ov;
+      }
+    } else if (P.swiglu_gate) {
       // SwiGLU epilogue through LDS: the bf16 products go to a [R][kNT] tile in the x ring
       // (row stride kNT + 4 halves, so the 32 rows one store instruction covers fall in
       // distinct banks), the accumulators die, and every thread then takes 4 adjacent
@@ -236,7 +284,7 @@ __global__ void __launch_bounds__(64 * WV, 12 / WV) gmm_kernel(QmvParams P) {
           u32x2_t o;
           o.x = pack_bf16x2(acc[i][4 * g], acc[i][4 * g + 1]);
           o.y = pack_bf16x2(acc[i][4 * g + 2], acc[i][4 * g + 3]);
-          *reinterpret_cast<u32x2_t*>(tile + (32 * i + fr) * kTS + 32 * wave + 8 * g + 4 * h) = o;
+          *reinterpret_cast<u32x2_t*>(tile + (32 * i + fr) * kTS + 32 * mw + 8 * g + 4 * h) = o;
         }
       __syncthreads();
       constexpr int kPerRow = kNT / 4, kRowsPerPass = kThreads / kPerRow;
@@ -273,7 +321,7 @@ __global__ void __launch_bounds__(64 * WV, 12 / WV) gmm_kernel(QmvParams P) {
         const bool nan = ro == -2 || !eok;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int n = n0 + 32 * wave + 8 * g + 4 * h;
+          const int n = n0 + 32 * mw + 8 * g + 4 * h;
           if (n >= N) continue;
           float v[4];
 #pragma unroll
@@ -298,19 +346,20 @@ bool gmm_supported(int64_t N, int64_t K, int bits, int gs, int x_f32, int64_t x_
          N * (K / 2) < ((int64_t)1 << 31) && x_bytes + 2 * K < ((int64_t)1 << 31);
 }
 
-template <int MT, int WV>
+template <int MT, int WV, bool DUAL>
 hipError_t launch_mt(const QmvParams& P, int grid_items, hipStream_t s) {
   const size_t lds = (size_t)kD * 32 * MT * 128 + 32 * MT * sizeof(int64_t);
   static bool attr = false;
   if (!attr) {
-    auto k = gmm_kernel<MT, WV>;
+    auto k = gmm_kernel<MT, WV, DUAL>;
     hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)lds);
     if (e != hipSuccess) return e;
     attr = true;
   }
-  const dim3 grid((unsigned)((P.N + 32 * WV - 1) / (32 * WV)), (unsigned)std::max(1, grid_items));
-  hipLaunchKernelGGL((gmm_kernel<MT, WV>), grid, dim3(64 * WV), lds, s, P);
+  constexpr int kNT = 32 * (DUAL ? WV / 2 : WV);
+  const dim3 grid((unsigned)((P.N + kNT - 1) / kNT), (unsigned)std::max(1, grid_items));
+  hipLaunchKernelGGL((gmm_kernel<MT, WV, DUAL>), grid, dim3(64 * WV), lds, s, P);
   return hipGetLastError();
 }
 
@@ -318,9 +367,12 @@ hipError_t launch_gmm(const QmvParams& P, int mt, int grid_items, hipStream_t s)
   if (!P.items || !P.item_count) return hipErrorInvalidValue;
   // 4 waves (128 weight rows) a block, three blocks a CU: 256-row blocks of 8 waves measured
   // 233 against 216 us per configs[3] T=512 layer (two blocks a CU then)
-  switch (mt) {
-    case 1: return launch_mt<1, 4>(P, grid_items, s);
-    case 2: return launch_mt<2, 4>(P, grid_items, s);
+  if (P.dual && (!P.w2 || !P.scales2 || !P.biases2)) return hipErrorInvalidValue;
+  switch (mt * 2 + (P.dual ? 1 : 0)) {
+    case 2: return launch_mt<1, 4, false>(P, grid_items, s);
+    case 3: return launch_mt<1, 4, true>(P, grid_items, s);
+    case 4: return launch_mt<2, 4, false>(P, grid_items, s);
+    case 5: return launch_mt<2, 4, true>(P, grid_items, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -9,6 +9,7 @@ from ._lib import MiError, MiUnsupported, lib, last_error, LIB_PATH  # noqa: F40
 from .ops import (quantized_matmul, gather_qmm, dequantize, quantize, fill_randn,  # noqa: F401
                   affine_params_from_geometry, moe_route_topk, moe_sort_dispatch, take_rows,
                   swiglu, moe_down_reduce, moe_down_reduce_rows, gather_qmm_swiglu,
+                  gather_qmm_gate_up_swiglu,
                   gather_qmv_gate_up_swiglu, gather_qmv_down_reduce, workspace_reserve,
                   workspace_release, library_gemm_calls,
                   moe_route_gate_up_swiglu, moe_route_grouped)

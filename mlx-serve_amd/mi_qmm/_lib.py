@@ -62,6 +62,8 @@ def lib():
                                             OptInt, s, P]
     L.mi_gather_qmm_noalloc.argtypes = L.mi_gather_qmm.argtypes
     L.mi_gather_qmm_swiglu.argtypes = [P] + L.mi_gather_qmm.argtypes
+    L.mi_gather_qmm_gate_up_swiglu.argtypes = (L.mi_gather_qmm.argtypes[:5] + [P, P, P] +
+                                                L.mi_gather_qmm.argtypes[5:])
     L.mi_moe_down_reduce_rows.argtypes = [P, P, P, P, i64, i64, i32, i64, i32, P]
     L.mi_moe_route_grouped.argtypes = [P, P, P, P, i64, i64, i32, i32, i32, b, ctypes.c_float, P]
     L.mi_moe_route_gate_up_swiglu.argtypes = [P, P, P, P, P, P, P, P, P, P, P, i64, i64, i32,

@@ -179,6 +179,31 @@ def gather_qmm_swiglu(gate, x, w, scales, biases, lhs_indices=None, rhs_indices=
     return y
 
 
+def gather_qmm_gate_up_swiglu(x, wg, sg, bg, wu, su, bu, lhs_indices=None, rhs_indices=None,
+                              transpose=True, group_size=None, bits=None, mode="affine",
+                              sorted_indices=False):
+    """swiglu(gather_qmm(x, wg, ...), gather_qmm(x, wu, ...)) in one call (the sorted MoE
+    path's two projections and activation, src/transformer.zig:15009-15023)."""
+    _contig(x, wg, sg, bg, wu, su, bu)
+    _require(x.dim() >= 2 and wg.dim() >= 2, "x and w need at least 2 dims")
+    _require(wg.shape == wu.shape and sg.shape == su.shape, "gate and up banks differ in shape")
+    K = x.shape[-1]
+    M = x.shape[-2]
+    gs, nb = _resolve(_packed(wg), sg, group_size, bits, K, mode)
+    N = wg.shape[-2]
+    lhs, lhs_div, rhs, shape = _broadcast_indices(x, wg, lhs_indices, rhs_indices)
+    n_idx = math.prod(shape)
+    x_batch = x.numel() // (M * K) if M * K else 0
+    n_exp = wg.numel() // (N * wg.shape[-1]) if N * wg.shape[-1] else 0
+    y = torch.empty(tuple(shape) + (M, N), dtype=x.dtype, device=x.device)
+    check(lib().mi_gather_qmm_gate_up_swiglu(
+        _ptr(y), _ptr(x), _ptr(wg), _ptr(sg), _ptr(bg), _ptr(wu), _ptr(su), _ptr(bu), _ptr(lhs),
+        _ptr(rhs), n_idx, lhs_div, x_batch, M, N, K, n_exp, bool(transpose), opt(gs), opt(nb),
+        mode.encode() if mode else None, bool(sorted_indices), _dtype_code(x, "x"),
+        _dtype_code(sg, "scales"), _stream(x)))
+    return y
+
+
 def dequantize(w, scales, biases, group_size=None, bits=None, mode="affine", dtype=None,
                rounding=None, global_scale=None):
     """mlx_dequantize (src/mlx.zig:271). dtype defaults to the scales dtype.

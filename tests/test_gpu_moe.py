@@ -322,8 +322,9 @@ def test_fused_decode_mlp_fp_modes(dev, mode, T):
                                        (64, 128, 8, 768, 2048), (40, 8, 2, 100, 256)])
 def test_sorted_up_swiglu_and_unsort_reduce_match_split(dev, T, E, k, N, K):
     """The fused sorted-path entries equal the split calls bit for bit: gather_qmm_swiglu ==
-    swiglu(gate, gather_qmm) (grouped kernel at T=512, the few-row kernels at small T, the
-    tile kernel at N=100), and moe_down_reduce_rows == moe_down_reduce(take_rows(v, inv))."""
+    swiglu(gate, gather_qmm) and gather_qmm_gate_up_swiglu == both (grouped kernel at T=512,
+    the few-row kernels at small T, the tile kernel at N=100), and moe_down_reduce_rows ==
+    moe_down_reduce(take_rows(v, inv))."""
     _print_case(t="sorted_fused", T=T, E=E, k=k, N=N, K=K)
     logits = torch.from_numpy(O.randn(T * E, 31).reshape(T, E)).to(dev)
     inds, sc = mi_qmm.moe_route_topk(logits, k, torch.bfloat16)
@@ -337,6 +338,8 @@ def test_sorted_up_swiglu_and_unsort_reduce_match_split(dev, T, E, k, N, K):
     split = mi_qmm.swiglu(g, u)
     fused = mi_qmm.gather_qmm_swiglu(g, x, *U, **kw)
     assert torch.equal(fused.view(torch.int16), split.view(torch.int16))
+    both = mi_qmm.gather_qmm_gate_up_swiglu(x, *G, *U, **kw)  # one launch on the grouped kernel
+    assert torch.equal(both.view(torch.int16), split.view(torch.int16))
     v = to_dev_bf16(O.make_x_bf16(T * k, N, 35), dev)
     ref = mi_qmm.moe_down_reduce(mi_qmm.take_rows(v, inv).view(T, k, N), sc)
     got = mi_qmm.moe_down_reduce_rows(v, inv, sc)
