@@ -275,6 +275,7 @@ struct GatherJob {
   bool empty = false, narrow = false, use_items = false, one_row = false, multi_row = false;
   bool grouped = false;  // sorted runs on the grouped kernel (gmm.hip)
   int gmm_mt = 0;        // its 32-row tiles per item
+  double gmm_items = 0;  // expected work items (distinct experts x items per run)
   int64_t max_items = 0;
   size_t items_bytes = 0, part_bytes = 0;
   size_t items_region() const { return ((items_bytes + 255) / 256) * 256; }
@@ -361,6 +362,7 @@ int gather_prepare(GatherJob& J, void* y, const void* x, const uint32_t* w, cons
       if (mu >= gmm_min) {
         const double want = mu + 3.0 * std::sqrt(mu);
         J.grouped = true;
+        J.gmm_items = distinct * std::max(1.0, std::ceil(want / 64.0));
         static const int force_mt = env_int("MI_QMM_GMM_MT", 0);
         J.gmm_mt = force_mt == 1 || force_mt == 2 ? force_mt
                    : want <= 32 ? 1 : 2;  // longer runs are cut into 64-row items
@@ -527,6 +529,16 @@ int gather_launch(GatherJob& J, void* ws, hipStream_t s) {
       P.items = items;
       P.item_count = count;
     }
+  }
+  // short K with 64-row items: the x-stationary instance, sized for one round of one block a
+  // CU (ns passes of 256 weight rows a block)
+  static const int use_xs = env_int("MI_QMM_GMM_XS", 1);
+  if (J.grouped && use_xs && J.gmm_mt == 2 && !P.dual && !P.swiglu_gate && mi::gmm_xs_fits(P.K)) {
+    const int64_t tiles = (P.N + 255) / 256;
+    const int64_t ns = std::min<int64_t>(
+        tiles, std::max<int64_t>(1, (int64_t)std::ceil(tiles * J.gmm_items / 256.0)));
+    hipError_t e = mi::launch_gmm_xs(P, (int)ns, J.plan.cfg.grid_z, s);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "grouped (x-stationary) launch");
   }
   hipError_t e = J.grouped     ? mi::launch_gmm(P, J.gmm_mt, J.plan.cfg.grid_z, s)
                  : J.one_row   ? mi::launch_qmv1(P, J.plan1, J.plan.cfg.grid_z, s)

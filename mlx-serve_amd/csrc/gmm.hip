@@ -337,6 +337,163 @@ __global__ void __launch_bounds__(64 * WV, 12 / WV) gmm_kernel(QmvParams P) {
   }
 }
 
+// x-stationary variant for short K: the item's 64 x rows, all of K, fit in LDS, so the block
+// moves them once by LDS DMA and then streams NS passes of 32 WV weight rows each (the
+// wave's 32 rows of every pass, one after another through one register ring) with no
+// barrier and no DMA inside the loop. Row r of x sits at r * S (S = 2K bytes rounded up to
+// 1 KB, one DMA instruction's span, plus 128 B so that consecutive rows start half the banks
+// apart), k-step t at + 128 t, and slot p of a step holds k-slot p ^ ((r >> 1) & 7), as in
+// the ring layout of gmm_kernel.
+__host__ __device__ constexpr int xs_row_stride(int K) { return (K * 2 + 1023) / 1024 * 1024 + 128; }
+constexpr int kXsD = 4;  // weight ring depth of the x-stationary kernel
+
+template <int WV>
+__global__ void __launch_bounds__(64 * WV, 1) gmm_xs_kernel(QmvParams P, int NS) {
+  constexpr int MT = 2, R = 64, kNT = 32 * WV;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int N = P.N, K = P.K, G = K / 64, nsteps = K / 64;
+  const int S = xs_row_stride(K);
+  int64_t* rowtab = reinterpret_cast<int64_t*>(smem + R * S);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 31, h = lane >> 5;
+  const int n_items = (int)*P.item_count;
+  const int slice0 = blockIdx.x * kNT * NS;
+  const int npass = min(NS, (N - slice0 + kNT - 1) / kNT);
+  const int total = npass * nsteps;
+  const int nchunk = (nsteps + 7) / 8;  // 1 KB DMA spans per x row
+  const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)P.x, 0, (int)(uint32_t)(P.x_batch * P.M * (int64_t)K * 2), kBufFlags);
+
+  for (int it_i = blockIdx.y; it_i < n_items; it_i += gridDim.y) {
+    const Item it = decode_item(P, it_i);
+    if (it.cnt <= 0) continue;  // block-uniform
+    const uint32_t e = __builtin_amdgcn_readfirstlane(it.expert_ok ? it.expert : 0u);
+    const bool eok = it.expert_ok;
+    if (tid < R) rowtab[tid] = item_x_row(P, it, tid);  // -1 skip, -2 NaN
+    __syncthreads();
+    const size_t mat = (size_t)e * (uint32_t)N;
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(P.w + mat * (uint32_t)(K / 8)), 0, N * (K / 2), kBufFlags);
+    const uint16_t* const sbase = (h ? P.biases : P.scales) + mat * (uint32_t)G;
+    auto row_of = [&](int p) __attribute__((always_inline)) {
+      return (uint32_t)min(slice0 + p * kNT + 32 * wave + fr, N - 1);
+    };
+    // the epilogue of pass p: acc[i] register r is D[n = 32 wave + 8(r/4) + 4h + r%4][m = 32 i + fr]
+    auto store = [&](int p, const f32x16_t (&acc)[MT], bool all_nan) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int m = 32 * i + fr;
+        const int64_t ro = rowtab[m];
+        if (ro == -1) continue;
+        const int64_t pos = it.pos0 + m;
+        const bool nan = all_nan || ro == -2;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = slice0 + p * kNT + 32 * wave + 8 * g + 4 * h;
+          if (n >= N) continue;
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = nan ? __builtin_nanf("") : acc[i][4 * g + q];
+          u32x2_t o;
+          o.x = pack_bf16x2(v[0], v[1]);
+          o.y = pack_bf16x2(v[2], v[3]);
+          *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint16_t*>(P.y) + pos * N + n) = o;
+        }
+      }
+    };
+    f32x16_t acc[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+    if (!eok) {
+      for (int p = 0; p < npass; ++p) store(p, acc, true);
+      __syncthreads();
+      continue;
+    }
+    // the item's x rows: DMA span j of row r holds k-steps 8j .. 8j + 7 (lanes past the
+    // row's end or the item's rows read past x: zeros, no traffic)
+    for (int q = wave; q < R * nchunk; q += WV) {
+      const int r = q / nchunk, j = q - r * nchunk;
+      const int step = 8 * j + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      const int64_t ro = rowtab[r];
+      const uint32_t src = ro >= 0 && step < nsteps
+                               ? (uint32_t)ro * 2u + (uint32_t)step * 128u + 16u * c
+                               : (uint32_t)kOOB;
+      dma16(xres, smem + r * S + j * 1024, src, 0u);
+    }
+    u32x4_t wq[kXsD];
+    u32x2_t sbc[2];  // scale/bias chunks: the chunk of steps 4c..4c+3 in slot c % 2
+    // flat step u = p * nsteps + t; nsteps % 4 == 0, so a chunk starts when u % 4 == 0
+    auto issue = [&](int u, int slot, int cslot) __attribute__((always_inline)) {
+      const int uu = min(u, total - 1);
+      const int p = uu / nsteps, t = uu - p * nsteps;
+      const uint32_t wr = row_of(p);
+      if ((u & 3) == 0)
+        sbc[cslot] = *reinterpret_cast<const u32x2_t*>(sbase + wr * (uint32_t)G + t);
+      wq[slot] = ld16(wres, wr * (uint32_t)(K / 2) + 16 * h, (uint32_t)t * 32u);
+    };
+    auto scale_bias = [&](int j, float& sc, float& bp) __attribute__((always_inline)) {
+      const u32x2_t mine = sbc[(j >> 2) & 1];
+      const uint32_t mw = (j & 2) ? mine.y : mine.x;
+      const uint32_t ow = xor32_u32(mw, lane);
+      const uint32_t sw = h ? ow : mw, bw = h ? mw : ow;
+      sc = __uint_as_float((j & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
+      bp = __uint_as_float((j & 1) ? (bw & 0xFFFF0000u) : (bw << 16));
+    };
+#pragma unroll
+    for (int j = 0; j < kXsD - 1; ++j) issue(j, j, (j >> 2) & 1);
+    // every DMA of this wave is older than the ring's loads; then all waves' rows are in
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((kXsD - 1) + 1));
+    __syncthreads();
+    for (int u0 = 0; u0 < total; u0 += 8) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int u = u0 + j;
+        // step u's weights and scale chunk are in once only the younger steps' loads
+        // (u+1 .. u+kXsD-2, one each plus one per scale chunk they start) are in flight
+        const int starts = ((j + kXsD - 2) >> 2) - (j >> 2);
+        switch (starts) {
+          case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kXsD - 2)); break;
+          default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kXsD - 1)); break;
+        }
+        if (u < total) {
+          const int p = u / nsteps, t = u - p * nsteps;
+          u32x4_t X[4][MT], A[4];
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+              const int r = 32 * i + fr, c = 4 * h + ks;
+              X[ks][i] = *reinterpret_cast<const u32x4_t*>(smem + r * S + t * 128 +
+                                                           ((c ^ ((r >> 1) & 7)) << 4));
+            }
+          float sc, bp;
+          scale_bias(j, sc, bp);
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) A[ks] = dequant8(wq[j % kXsD][ks], sc, bp);
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int i = 0; i < MT; ++i) acc[i] = mfma32(A[ks], X[ks][i], acc[i]);
+          if (t == nsteps - 1) {
+            store(p, acc, false);
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+          }
+        }
+        issue(u + kXsD - 1, (j + kXsD - 1) % kXsD, ((j + kXsD - 1) >> 2) & 1);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();  // the row table and the x rows are reused by the next item
+  }
+}
+
 }  // namespace
 
 bool gmm_supported(int64_t N, int64_t K, int bits, int gs, int x_f32, int64_t x_bytes) {
@@ -360,6 +517,25 @@ hipError_t launch_mt(const QmvParams& P, int grid_items, hipStream_t s) {
   constexpr int kNT = 32 * (DUAL ? WV / 2 : WV);
   const dim3 grid((unsigned)((P.N + kNT - 1) / kNT), (unsigned)std::max(1, grid_items));
   hipLaunchKernelGGL((gmm_kernel<MT, WV, DUAL>), grid, dim3(64 * WV), lds, s, P);
+  return hipGetLastError();
+}
+
+bool gmm_xs_fits(int64_t K) { return (int64_t)64 * xs_row_stride((int)K) + 512 <= 160 * 1024; }
+
+hipError_t launch_gmm_xs(const QmvParams& P, int ns, int grid_items, hipStream_t s) {
+  constexpr int WV = 8, kNT = 32 * WV;
+  if (!P.items || !P.item_count || P.dual || P.swiglu_gate || !gmm_xs_fits(P.K) || ns < 1)
+    return hipErrorInvalidValue;
+  const size_t lds = (size_t)64 * xs_row_stride(P.K) + 64 * sizeof(int64_t);
+  static size_t attr = 0;
+  if (attr < lds) {
+    hipError_t e = hipFuncSetAttribute((const void*)gmm_xs_kernel<WV>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr = lds;
+  }
+  const dim3 grid((unsigned)((P.N + kNT * ns - 1) / (kNT * ns)), (unsigned)std::max(1, grid_items));
+  hipLaunchKernelGGL(gmm_xs_kernel<WV>, grid, dim3(64 * WV), lds, s, P, ns);
   return hipGetLastError();
 }
 

@@ -104,6 +104,10 @@ hipError_t launch_qmvm_gather(const QmvParams& G, const QmvmPlan& plan, int grid
 // 32 * mt rows (mt = 1, 2) built by launch_build_items; grid_items blocks stride them.
 bool gmm_supported(int64_t N, int64_t K, int bits, int gs, int x_f32, int64_t x_bytes);
 hipError_t launch_gmm(const QmvParams& P, int mt, int grid_items, hipStream_t s);
+// x-stationary instance for short K (the item's 64 x rows, all of K, in LDS): 64-row items,
+// ns passes of 256 weight rows a block, plain bf16 outputs only
+bool gmm_xs_fits(int64_t K);
+hipError_t launch_gmm_xs(const QmvParams& P, int ns, int grid_items, hipStream_t s);
 
 // Decode-width kernel (qmv16.hip): M <= 16 rows per item, 16-row weight tiles.
 int qmv16_mp_for_rows(int rows);
