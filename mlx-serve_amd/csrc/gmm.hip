@@ -30,6 +30,7 @@
 // a 4-deep ring measured no slower than the 8-deep one. The dequantize of step t + 1 is
 // interleaved with step t's MFMAs (it needs registers only).
 #include <algorithm>
+#include <type_traits>
 
 #include "dequant_bf16.h"
 #include "mi_common.h"
@@ -345,7 +346,11 @@ __global__ void __launch_bounds__(64 * WV, 12 / WV) gmm_kernel(QmvParams P) {
 // apart), k-step t at + 128 t, and slot p of a step holds k-slot p ^ ((r >> 1) & 7), as in
 // the ring layout of gmm_kernel.
 __host__ __device__ constexpr int xs_row_stride(int K) { return (K * 2 + 1023) / 1024 * 1024 + 128; }
-constexpr int kXsD = 4;  // weight ring depth of the x-stationary kernel
+#ifndef MI_GMM_XS_DEPTH
+#define MI_GMM_XS_DEPTH 8
+#endif
+constexpr int kXsD = MI_GMM_XS_DEPTH;  // weight ring depth of the x-stationary kernel
+static_assert(kXsD == 4 || kXsD == 8 || kXsD == 16, "the step loop unrolls by 16");
 
 template <int WV>
 __global__ void __launch_bounds__(64 * WV, 1) gmm_xs_kernel(QmvParams P, int NS) {
@@ -380,7 +385,8 @@ __global__ void __launch_bounds__(64 * WV, 1) gmm_xs_kernel(QmvParams P, int NS)
       return (uint32_t)min(slice0 + p * kNT + 32 * wave + fr, N - 1);
     };
     // the epilogue of pass p: acc[i] register r is D[n = 32 wave + 8(r/4) + 4h + r%4][m = 32 i + fr]
-    auto store = [&](int p, const f32x16_t (&acc)[MT], bool all_nan) __attribute__((always_inline)) {
+    // two accumulator sets (even / odd k-steps), summed at the store
+    auto store = [&](int p, const f32x16_t (&acc)[2][MT], bool all_nan) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const int m = 32 * i + fr;
@@ -394,7 +400,8 @@ __global__ void __launch_bounds__(64 * WV, 1) gmm_xs_kernel(QmvParams P, int NS)
           if (n >= N) continue;
           float v[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] = nan ? __builtin_nanf("") : acc[i][4 * g + q];
+          for (int q = 0; q < 4; ++q)
+            v[q] = nan ? __builtin_nanf("") : acc[0][i][4 * g + q] + acc[1][i][4 * g + q];
           u32x2_t o;
           o.x = pack_bf16x2(v[0], v[1]);
           o.y = pack_bf16x2(v[2], v[3]);
@@ -402,11 +409,13 @@ __global__ void __launch_bounds__(64 * WV, 1) gmm_xs_kernel(QmvParams P, int NS)
         }
       }
     };
-    f32x16_t acc[MT];
+    f32x16_t acc[2][MT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[a][i][r] = 0.f;
     if (!eok) {
       for (int p = 0; p < npass; ++p) store(p, acc, true);
       __syncthreads();
@@ -425,7 +434,8 @@ __global__ void __launch_bounds__(64 * WV, 1) gmm_xs_kernel(QmvParams P, int NS)
       dma16(xres, smem + r * S + j * 1024, src, 0u);
     }
     u32x4_t wq[kXsD];
-    u32x2_t sbc[2];  // scale/bias chunks: the chunk of steps 4c..4c+3 in slot c % 2
+    constexpr int kCS = kXsD / 4 + 1;  // scale/bias chunk slots: chunks in use or in flight
+    u32x2_t sbc[4];  // the chunk of steps 4c..4c+3 in slot c % 4
     // flat step u = p * nsteps + t; nsteps % 4 == 0, so a chunk starts when u % 4 == 0
     auto issue = [&](int u, int slot, int cslot) __attribute__((always_inline)) {
       const int uu = min(u, total - 1);
@@ -436,7 +446,7 @@ __global__ void __launch_bounds__(64 * WV, 1) gmm_xs_kernel(QmvParams P, int NS)
       wq[slot] = ld16(wres, wr * (uint32_t)(K / 2) + 16 * h, (uint32_t)t * 32u);
     };
     auto scale_bias = [&](int j, float& sc, float& bp) __attribute__((always_inline)) {
-      const u32x2_t mine = sbc[(j >> 2) & 1];
+      const u32x2_t mine = sbc[(j >> 2) & 3];
       const uint32_t mw = (j & 2) ? mine.y : mine.x;
       const uint32_t ow = xor32_u32(mw, lane);
       const uint32_t sw = h ? ow : mw, bw = h ? mw : ow;
@@ -444,49 +454,61 @@ __global__ void __launch_bounds__(64 * WV, 1) gmm_xs_kernel(QmvParams P, int NS)
       bp = __uint_as_float((j & 1) ? (bw & 0xFFFF0000u) : (bw << 16));
     };
 #pragma unroll
-    for (int j = 0; j < kXsD - 1; ++j) issue(j, j, (j >> 2) & 1);
+    for (int j = 0; j < kXsD - 1; ++j) issue(j, j, (j >> 2) & 3);
+    static_assert(kCS <= 4, "scale chunk ring");
     // every DMA of this wave is older than the ring's loads; then all waves' rows are in
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm((kXsD - 1) + 1));
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((kXsD - 1) + (kXsD - 2) / 4 + 1));
     __syncthreads();
-    for (int u0 = 0; u0 < total; u0 += 8) {
+    for (int u0 = 0; u0 < total; u0 += 16) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < 16; ++j) {
         const int u = u0 + j;
         // step u's weights and scale chunk are in once only the younger steps' loads
         // (u+1 .. u+kXsD-2, one each plus one per scale chunk they start) are in flight
         const int starts = ((j + kXsD - 2) >> 2) - (j >> 2);
         switch (starts) {
           case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kXsD - 2)); break;
-          default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kXsD - 1)); break;
+          case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kXsD - 1)); break;
+          case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kXsD)); break;
+          case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kXsD + 1)); break;
+          default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kXsD + 2)); break;
         }
         if (u < total) {
           const int p = u / nsteps, t = u - p * nsteps;
-          u32x4_t X[4][MT], A[4];
+          // the 32-row tiles that hold rows of the item (MTI = 1: rows 32..63 are padding)
+          auto compute = [&](auto mt_c) __attribute__((always_inline)) {
+            constexpr int MTI = decltype(mt_c)::value;
+            u32x4_t X[4][MTI], A[4];
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks)
+            for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-            for (int i = 0; i < MT; ++i) {
-              const int r = 32 * i + fr, c = 4 * h + ks;
-              X[ks][i] = *reinterpret_cast<const u32x4_t*>(smem + r * S + t * 128 +
-                                                           ((c ^ ((r >> 1) & 7)) << 4));
-            }
-          float sc, bp;
-          scale_bias(j, sc, bp);
+              for (int i = 0; i < MTI; ++i) {
+                const int r = 32 * i + fr, c = 4 * h + ks;
+                X[ks][i] = *reinterpret_cast<const u32x4_t*>(smem + r * S + t * 128 +
+                                                             ((c ^ ((r >> 1) & 7)) << 4));
+              }
+            float sc, bp;
+            scale_bias(j, sc, bp);
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks) A[ks] = dequant8(wq[j % kXsD][ks], sc, bp);
+            for (int ks = 0; ks < 4; ++ks) A[ks] = dequant8(wq[j % kXsD][ks], sc, bp);
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks)
+            for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-            for (int i = 0; i < MT; ++i) acc[i] = mfma32(A[ks], X[ks][i], acc[i]);
+              for (int i = 0; i < MTI; ++i)
+                acc[ks & 1][i] = mfma32(A[ks], X[ks][i], acc[ks & 1][i]);
+          };
+          compute(std::integral_constant<int, 2>{});
           if (t == nsteps - 1) {
             store(p, acc, false);
 #pragma unroll
-            for (int i = 0; i < MT; ++i)
+            for (int a = 0; a < 2; ++a)
 #pragma unroll
-              for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+              for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[a][i][r] = 0.f;
           }
         }
-        issue(u + kXsD - 1, (j + kXsD - 1) % kXsD, ((j + kXsD - 1) >> 2) & 1);
+        issue(u + kXsD - 1, (j + kXsD - 1) % kXsD, ((j + kXsD - 1) >> 2) & 3);
       }
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
