@@ -385,8 +385,9 @@ __global__ void __launch_bounds__(64 * WV, 1) gmm_xs_kernel(QmvParams P, int NS)
       return (uint32_t)min(slice0 + p * kNT + 32 * wave + fr, N - 1);
     };
     // the epilogue of pass p: acc[i] register r is D[n = 32 wave + 8(r/4) + 4h + r%4][m = 32 i + fr]
-    // two accumulator sets (even / odd k-steps), summed at the store
-    auto store = [&](int p, const f32x16_t (&acc)[2][MT], bool all_nan) __attribute__((always_inline)) {
+    // one accumulator set, k-steps in order: the ring kernel's summation order, so both
+    // instances give the same bits
+    auto store = [&](int p, const f32x16_t (&acc)[MT], bool all_nan) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const int m = 32 * i + fr;
@@ -400,8 +401,7 @@ __global__ void __launch_bounds__(64 * WV, 1) gmm_xs_kernel(QmvParams P, int NS)
           if (n >= N) continue;
           float v[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            v[q] = nan ? __builtin_nanf("") : acc[0][i][4 * g + q] + acc[1][i][4 * g + q];
+          for (int q = 0; q < 4; ++q) v[q] = nan ? __builtin_nanf("") : acc[i][4 * g + q];
           u32x2_t o;
           o.x = pack_bf16x2(v[0], v[1]);
           o.y = pack_bf16x2(v[2], v[3]);
@@ -409,13 +409,11 @@ __global__ void __launch_bounds__(64 * WV, 1) gmm_xs_kernel(QmvParams P, int NS)
         }
       }
     };
-    f32x16_t acc[2][MT];
+    f32x16_t acc[MT];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[a][i][r] = 0.f;
+      for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
     if (!eok) {
       for (int p = 0; p < npass; ++p) store(p, acc, true);
       __syncthreads();
@@ -494,18 +492,15 @@ __global__ void __launch_bounds__(64 * WV, 1) gmm_xs_kernel(QmvParams P, int NS)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-              for (int i = 0; i < MTI; ++i)
-                acc[ks & 1][i] = mfma32(A[ks], X[ks][i], acc[ks & 1][i]);
+              for (int i = 0; i < MTI; ++i) acc[i] = mfma32(A[ks], X[ks][i], acc[i]);
           };
           compute(std::integral_constant<int, 2>{});
           if (t == nsteps - 1) {
             store(p, acc, false);
 #pragma unroll
-            for (int a = 0; a < 2; ++a)
+            for (int i = 0; i < MT; ++i)
 #pragma unroll
-              for (int i = 0; i < MT; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[a][i][r] = 0.f;
+              for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
           }
         }
         issue(u + kXsD - 1, (j + kXsD - 1) % kXsD, ((j + kXsD - 1) >> 2) & 3);
