@@ -74,16 +74,24 @@ MI_DEV uint16_t sigmoid_bf16(uint16_t g) {
   const uint32_t lo16 = __float_as_uint(sf) & 0xFFFFu;
   if (vf >= -80.f && lo16 - (0x8000u - 8u) > 16u) return (uint16_t)f32_to_bf16_bits(sf);
   if (vf != vf) return (uint16_t)f32_to_bf16_bits(vf);  // NaN in, quiet NaN out
-  // scans of the short tables: compares with immediates and selects, no loads
+  // scans of the short tables: immediates and selects, no loads. Each entry is materialized
+  // where it is used (an opaque copy): left as constants, the compiler hoists them out of
+  // the caller's loops into ~36 registers held for the whole kernel.
   uint32_t r = vf < -80.f ? 0u : f32_to_bf16_bits(sf);
   if (vf < -80.f) {
 #pragma unroll
-    for (int i = 0; i < kSigmoidEdgeTailCount; ++i)
-      r = (kSigmoidEdgesTail[i] >> 16) == (uint32_t)g ? (kSigmoidEdgesTail[i] & 0xFFFFu) : r;
+    for (int i = 0; i < kSigmoidEdgeTailCount; ++i) {
+      uint32_t e = kSigmoidEdgesTail[i];
+      asm volatile("" : "+v"(e));
+      r = (e >> 16) == (uint32_t)g ? (e & 0xFFFFu) : r;
+    }
   } else {
 #pragma unroll
-    for (int i = 0; i < kSigmoidEdgeNearCount; ++i)
-      r = (kSigmoidEdgesNear[i] >> 16) == (uint32_t)g ? (kSigmoidEdgesNear[i] & 0xFFFFu) : r;
+    for (int i = 0; i < kSigmoidEdgeNearCount; ++i) {
+      uint32_t e = kSigmoidEdgesNear[i];
+      asm volatile("" : "+v"(e));
+      r = (e >> 16) == (uint32_t)g ? (e & 0xFFFFu) : r;
+    }
   }
   return (uint16_t)r;
 }

@@ -319,11 +319,13 @@ def test_fused_decode_mlp_fp_modes(dev, mode, T):
 
 
 @pytest.mark.parametrize("T,E,k,N,K", [(512, 16, 4, 256, 512), (3, 16, 2, 192, 512),
-                                       (64, 128, 8, 768, 2048), (40, 8, 2, 100, 256)])
+                                       (64, 128, 8, 768, 2048), (40, 8, 2, 100, 256),
+                                       (8, 16, 4, 256, 1024), (16, 64, 8, 512, 7168)])
 def test_sorted_up_swiglu_and_unsort_reduce_match_split(dev, T, E, k, N, K):
     """The fused sorted-path entries equal the split calls bit for bit: gather_qmm_swiglu ==
     swiglu(gate, gather_qmm) and gather_qmm_gate_up_swiglu == both (grouped kernel at T=512,
-    the few-row kernels at small T, the tile kernel at N=100), and moe_down_reduce_rows ==
+    the one-row kernel at T=3, the few-row kernel at T=8 and 16 (a K split at K=7168), the
+    tile kernel at N=100), and moe_down_reduce_rows ==
     moe_down_reduce(take_rows(v, inv))."""
     _print_case(t="sorted_fused", T=T, E=E, k=k, N=N, K=K)
     logits = torch.from_numpy(O.randn(T * E, 31).reshape(T, E)).to(dev)

@@ -262,6 +262,34 @@ def test_gather_sorted_grouped_kernel(dev, N, K, E, T, topk, skew):
     assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
 
 
+@pytest.mark.parametrize("N,K,E,T,topk,skew", [(512, 7168, 16, 8, 4, False),
+                                                 (2048, 2048, 16, 4, 8, True),
+                                                 (200, 1024, 32, 16, 4, True),
+                                                 (64, 4096, 8, 6, 2, False)])
+def test_gather_sorted_rows_kernel(dev, N, K, E, T, topk, skew):
+    """Sorted gathers of a few rows per expert (configs[4]-like: ~2.3 rows a distinct
+    expert) on the few-row kernel's work items; skewed routings put runs longer than one
+    item on hot experts (cut into several items); K = 7168 and 4096 take K splits."""
+    _print_case(t="gather_rows", N=N, K=K, E=E, T=T, topk=topk, skew=skew)
+    wq, s, b = weights(E, N, K, 4, 64, 230 + E)
+    rng = np.random.default_rng(N + K + E)
+    p = np.ones(E) / E
+    if skew:
+        p = np.ones(E)
+        p[:2] = E
+        p /= p.sum()
+    flat = np.stack([rng.choice(E, size=topk, replace=False, p=p) for _ in range(T)])
+    flat = flat.reshape(-1).astype(np.uint32)
+    order, inv, srt, lhs = O.sort_dispatch(flat, topk)
+    x = O.make_x_bf16(T, K, 231 + K).reshape(T, 1, K)
+    y = mi_qmm.gather_qmm(to_dev_bf16(x, dev), to_dev_u32(wq, dev), to_dev_bf16(s, dev),
+                          to_dev_bf16(b, dev), lhs_indices=to_dev_u32(lhs, dev),
+                          rhs_indices=to_dev_u32(srt, dev), group_size=64, bits=4,
+                          sorted_indices=True)
+    truth = O.gather_qmm_f64(x, wq, s, b, lhs, srt, T * topk)
+    assert max_err_ratio(to_f64(y), truth) <= BF16_TOL
+
+
 def test_gather_out_of_range_is_nan(dev):
     _print_case(t="gather_oob")
     E, N, K = 4, 32, 128
