@@ -190,7 +190,12 @@ bool plan_impl(int M, int N, int K, int gs, int bits, int64_t n_items, int fpm, 
   // launch); then chunks per wave near `target` and more waves. Scale/bias pairs are
   // staged as fp32 (s, b - 128 s) when LDS allows, else as bf16 pairs.
   // 64-row plans: 4 tiles, so 8 waves still cover a K range of 2048 in one block
-  const int wr0 = env_wr ? env_wr : M <= 2 ? 1 : M <= 16 ? 4 : M <= 32 ? 8 : 4;
+  // Gather items of 3..16 rows at K >= 4096: 16 tiles (one wave each, so K splits into
+  // ranges of at most 8 chunks): configs[4] T=64 gate/up 1088 -> 1049 us per call (8 tiles:
+  // 1077); at K = 2048 it is slower (436 -> 504 us).
+  const bool long_gather = n_items > 1 && K >= 4096 && M > 2 && M <= 16 && !fp;
+  const int wr0 = env_wr ? env_wr : long_gather ? 16
+                  : M <= 2 ? 1 : M <= 16 ? 4 : M <= 32 ? 8 : 4;
   QmvmPlan best{};
   double best_cost = 1e30;
   // Up to 32 rows, a plan under 192 blocks (narrow shapes: N = 1536..7168 at K = 768..7168)
