@@ -96,6 +96,16 @@ MI_DEV uint16_t sigmoid_bf16(uint16_t g) {
   return (uint16_t)r;
 }
 
+// Block barrier ordering LDS only: waits for this wave's LDS operations, not for its global
+// stores (__syncthreads' fence waits for those too). For the one-block glue kernels, whose
+// global stores no other thread of the block reads.
+MI_DEV void lds_sync() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt/expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // SwiGLU with the bf16 rounding points of the reference (src/transformer.zig:19846-19884):
 // bf16(bf16(g * sigmoid(g)) * u).
 MI_DEV uint16_t swiglu_bf16(uint16_t g, uint16_t u) {

@@ -267,18 +267,18 @@ __device__ int block_scan_incl(int v, int* sh) {
   constexpr int id = MAX ? INT32_MIN : 0;
   v = wave_scan_incl_i32<MAX>(v);
   if (lane == 63) sh[wave] = v;
-  __syncthreads();
+  lds_sync();
   if (wave == 0) {
     const int t = lane < NW ? sh[lane] : id;
     const int w = wave_scan_incl_i32<MAX>(t);
     if (lane < NW) sh[NW + lane] = w;  // inclusive totals through wave `lane`
   }
-  __syncthreads();
+  lds_sync();
   if (wave > 0) {
     const int p = sh[NW + wave - 1];
     v = MAX ? (p > v ? p : v) : v + p;
   }
-  __syncthreads();
+  lds_sync();
   return v;
 }
 
@@ -293,7 +293,7 @@ __global__ void __launch_bounds__(kBT) build_items_kernel(const uint32_t* __rest
   __shared__ int prev_a[kBT];
   __shared__ int carry_a, carry_n;
   if (threadIdx.x == 0) { carry_a = 0; carry_n = 0; }
-  __syncthreads();
+  lds_sync();
   const int64_t total = n_pairs * M;
   const int rs = __builtin_ctz((unsigned)R);  // rows per item: a power of two
   // Each pass covers kBT * kBPT pairs; thread t owns pairs j0 .. j0 + kBPT - 1.
@@ -315,7 +315,7 @@ __global__ void __launch_bounds__(kBT) build_items_kernel(const uint32_t* __rest
     }
     const int incl_a = block_scan_incl<true>(la, sh);
     prev_a[threadIdx.x] = incl_a;
-    __syncthreads();
+    lds_sync();
     int excl_a = threadIdx.x ? prev_a[threadIdx.x - 1] : -1;
     const int ca = carry_a;
     if (excl_a < ca) excl_a = ca;
@@ -351,12 +351,12 @@ __global__ void __launch_bounds__(kBT) build_items_kernel(const uint32_t* __rest
       }
       off += c[q];
     }
-    __syncthreads();
+    lds_sync();
     if (threadIdx.x == kBT - 1) {
       carry_a = incl_a > ca ? incl_a : ca;
       carry_n = (int)off;
     }
-    __syncthreads();
+    lds_sync();
   }
   if (threadIdx.x == 0) {
     const int64_t n = carry_n < max_items ? carry_n : max_items;
