@@ -32,12 +32,11 @@ MI_DEV T add_splits(T acc, const T* __restrict__ p, int64_t stride, int r0, int 
   return acc;
 }
 
-// Round-to-nearest-even fp32 -> bf16 bits; NaN stays a quiet NaN.
+// Round-to-nearest-even fp32 -> bf16 bits; NaN stays a quiet NaN. One v_cvt_pk_bf16_f32
+// (the integer form, add 0x7FFF + lsb with a NaN test, is ~5 VALU: the bf16 arithmetic of
+// the slot reduce was VALU-bound on it).
 MI_DEV uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (u >> 16) | 0x40u;
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return u >> 16;
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 // Eight bf16 values held in four dwords, as an MFMA A/B operand.

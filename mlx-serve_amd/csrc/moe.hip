@@ -392,7 +392,40 @@ __global__ void down_reduce8_kernel(u32x4_t* __restrict__ y, const u32x4_t* __re
   for (int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; n < N8;
        n += (int64_t)gridDim.x * blockDim.x) {
     u32x4_t total = {0u, 0u, 0u, 0u};
-    for (int s = 0; s < k; ++s) {
+    int s = 0;
+    // 8 slots at a time: every row index, score and row segment of the group is loaded
+    // before the first add (one memory round trip a group, not one a slot)
+    for (; s + 8 <= k; s += 8) {
+      const int64_t p0 = t * k + s;
+      int64_t src[8];
+      if (rows) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) src[q] = (int64_t)rows[p0 + q];
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) src[q] = p0 + q;
+      }
+      u32x4_t xs[8];
+      uint16_t scs[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        // an out-of-range row reads row 0 and is zeroed (no branch on the index)
+        const bool ok = src[q] < n_rows;
+        xs[q] = v[(ok ? src[q] : 0) * N8 + n];
+        if (!ok) xs[q] = u32x4_t{0u, 0u, 0u, 0u};
+        scs[q] = scores[p0 + q];
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint32_t lo = bf16_add((uint16_t)(total[c] & 0xFFFFu), bf16_mul((uint16_t)(xs[q][c] & 0xFFFFu), scs[q]));
+          const uint32_t hi = bf16_add((uint16_t)(total[c] >> 16), bf16_mul((uint16_t)(xs[q][c] >> 16), scs[q]));
+          total[c] = lo | (hi << 16);
+        }
+      }
+    }
+    for (; s < k; ++s) {
       const int64_t p = t * k + s;
       const int64_t src = rows ? (int64_t)rows[p] : p;
       const u32x4_t zero = {0u, 0u, 0u, 0u};
