@@ -176,7 +176,7 @@ __global__ void __launch_bounds__(kSortThreads) sort_dispatch_kernel(
   // 8 loads in flight per thread before the first atomic. Up to 8 chunks of 1024 ids the
   // thread's ids stay in registers for the scatter below (no second round of loads).
   const bool keep = n <= 8 * kSortThreads;
-  uint32_t vk[8];
+  uint32_t vk[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
   for (int64_t i0 = tid; i0 < n; i0 += 8 * kSortThreads) {
     uint32_t v[8];
 #pragma unroll
@@ -409,10 +409,8 @@ __global__ void down_reduce8_kernel(u32x4_t* __restrict__ y, const u32x4_t* __re
       uint16_t scs[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        // an out-of-range row reads row 0 and is zeroed (no branch on the index)
-        const bool ok = src[q] < n_rows;
-        xs[q] = v[(ok ? src[q] : 0) * N8 + n];
-        if (!ok) xs[q] = u32x4_t{0u, 0u, 0u, 0u};
+        const u32x4_t zero = {0u, 0u, 0u, 0u};
+        xs[q] = src[q] < n_rows ? v[src[q] * N8 + n] : zero;  // out of range: a zero row
         scs[q] = scores[p0 + q];
       }
 #pragma unroll
