@@ -877,7 +877,10 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
     // one row of nvfp4 / mxfp4 / mxfp8: the one-row streaming kernel's fp instances
     static const int fp_qmv1 = env_int("MI_QMM_FP_QMV1", 1);
     if (fp_qmv1 && M == 1 && K % 128 == 0 && N * K * (fm == 2 ? 2 : 1) / 2 < ((int64_t)1 << 31)) {
-      const mi::Qmv1Plan pl = mi::qmv1_plan((int)N, (int)K, 64, 1);
+      mi::Qmv1Plan pl = mi::qmv1_plan((int)N, (int)K, 64, 1);
+      // mxfp8 (one byte a code, two loads a chunk): 2 chunks in flight a wave, also in the
+      // long-row down plan (Llama MLP M=1 3669 -> 3993 GB/s; 3857 with the down at 4)
+      if (fm == 2) pl.depth = 2;
       mi::QmvParams P{};
       P.w = w;
       P.scales = (const uint16_t*)scales;
@@ -976,9 +979,9 @@ int mi_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   // reduce.
   auto run_qmv1_fmt = [&](int fpm) -> int {
     mi::Qmv1Plan pl = mi::qmv1_plan((int)N, (int)K, 64, 1);
-    // one byte a code (8-bit, mxfp8): two loads a chunk, so 2 chunks in flight a wave where
-    // the 4-bit plan issues 4 (8-bit [14336,4096]: 13.77 -> 12.89 us a launch)
-    if ((fpm == 108 || fpm == 2) && pl.nc <= 4) pl.depth = 2;
+    // 8-bit (one byte a code): two loads a chunk, so 2 chunks in flight a wave where the
+    // 4-bit plan issues 4 ([14336,4096]: 13.77 -> 12.89 us a launch)
+    if (fpm == 108 && pl.nc <= 4) pl.depth = 2;
     mi::QmvParams P{};
     P.w = w;
     P.scales = (const uint16_t*)scales;
