@@ -66,8 +66,7 @@ struct Qmv1Plan {
   size_t lds;
 };
 bool qmv1_supported(int N, int K, int gs, int bits, int x_f32);
-// target > 0: chunks a wave to aim for instead of the default 4
-Qmv1Plan qmv1_plan(int N, int K, int gs, int64_t n_items, int target = 0);
+Qmv1Plan qmv1_plan(int N, int K, int gs, int64_t n_items);
 hipError_t launch_qmv1(const QmvParams& P, const Qmv1Plan& plan, int grid_z, hipStream_t s);
 // dense one-row nvfp4 (fpm 0) / mxfp4 (fpm 1): the one-row kernel's fp instances
 hipError_t launch_qmv1_fp(const QmvParams& P, const Qmv1Plan& plan, int fpm, hipStream_t s);

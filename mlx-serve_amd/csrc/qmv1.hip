@@ -85,7 +85,7 @@ int env_or(const char* name, int dflt) {
 //  - fewer waves: ~8 waves per CU, each streaming its chunks with a rolling window of
 //    `depth` loads (2 for <= 8 chunks, 4 above), so data arrives in the order it is used
 //    and the dot products overlap the stream instead of piling up at the end.
-Qmv1Plan qmv1_plan(int N, int K, int gs, int64_t n_items, int target_arg) {
+Qmv1Plan qmv1_plan(int N, int K, int gs, int64_t n_items) {
   const int nch = K / kChunkVals;
   const int64_t tiles = (N + 15) / 16;
   const int64_t rows_work = tiles * std::max<int64_t>(1, std::min<int64_t>(n_items, 65535));
@@ -93,16 +93,16 @@ Qmv1Plan qmv1_plan(int N, int K, int gs, int64_t n_items, int target_arg) {
   static const int env_ks_pen = env_or("MI_QMV1_KSPEN", 20);
   static const int env_depth = env_or("MI_QMV1_DEPTH", 0);
   constexpr int64_t kCUs = 256;
-  int target = env_target ? env_target : target_arg > 0 ? target_arg : 4;
+  int target = env_target ? env_target : 4;
   const bool several = rows_work > tiles;  // work items of several pairs / experts
-  if (!env_target && !target_arg && several) {
+  if (!env_target && several) {
     // ~24 waves per CU over the whole launch: per-item set-up is amortized over more
     // chunks when the launch is large, and small launches keep enough waves
     const int64_t t = (rows_work * nch + 12 * kCUs) / (24 * kCUs);
     target = (int)std::max<int64_t>(4, std::min<int64_t>(16, t));
   }
   Factor f = exact_factor(nch, target, env_ks_pen);
-  if (!env_target && !target_arg && !several && f.nc > 4) {
+  if (!env_target && !several && f.nc > 4) {
     // 4 chunks per wave does not factor: size waves for ~8 per CU instead
     const int64_t t = rows_work * nch / (8 * kCUs);
     target = (int)std::max<int64_t>(4, std::min<int64_t>(16, t));
