@@ -258,10 +258,10 @@ bool plan_impl(int M, int N, int K, int gs, int bits, int64_t n_items, int fpm, 
   }
   if (!best.nc) return false;
   // two chunks in flight per wave, except where four measured faster on Llama MLP shapes:
-  // 8-bit affine at 8..16 rows (3-5%: M=8 18.99 -> 18.49 / 18.83 -> 17.83 us a gate / down
-  // launch; at 32 rows four is 10% slower, at 2 rows no better); mxfp4 at every row count
+  // 8-bit affine up to 16 rows (1-5%: M=8 18.99 -> 18.49 / 18.83 -> 17.83 us a gate / down
+  // launch, M=4 3438 -> 3538 GB/s; at 32 rows four is 10% slower); mxfp4 at every row count
   // (5-7%: M=8 2402 -> 2583 GB/s) and mxfp8 (1-6%). nvfp4 is 5% slower with four.
-  const bool deep = (bits == 8 && fpm < 0 && M >= 8 && M <= 16) || fpm == 1 || fpm == 2;
+  const bool deep = (bits == 8 && fpm < 0 && M <= 16) || fpm == 1 || fpm == 2;
   best.depth = env_depth ? env_depth : deep ? 4 : 2;
   best.rows = M;
   best.bits = bits;
