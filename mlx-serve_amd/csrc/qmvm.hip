@@ -194,7 +194,12 @@ bool plan_impl(int M, int N, int K, int gs, int bits, int64_t n_items, int fpm, 
   // ranges of at most 8 chunks): configs[4] T=64 gate/up 1088 -> 1049 us per call (8 tiles:
   // 1077); at K = 2048 it is slower (436 -> 504 us).
   const bool long_gather = n_items > 1 && K >= 4096 && M > 2 && M <= 16 && !fp;
-  const int wr0 = env_wr ? env_wr : long_gather ? 16
+  // One byte a code (8-bit, mxfp8) doubles the weight bytes per staged activation, so fewer
+  // tiles a block (more blocks) pay: 2 tiles for 8-bit up to 16 rows and mxfp8 up to 8
+  // (Llama MLP 8-bit M=4 3526 -> 4032 GB/s, M=16 2981 -> 3072; mxfp8 M=8 2565 -> 2858; mxfp8
+  // at 16 rows and both at 32 measured slower).
+  const bool byte_few = bits == 8 && M > 2 && (M <= 8 || (fpm < 0 && M <= 16));
+  const int wr0 = env_wr ? env_wr : long_gather ? 16 : byte_few ? 2
                   : M <= 2 ? 1 : M <= 16 ? 4 : M <= 32 ? 8 : 4;
   QmvmPlan best{};
   double best_cost = 1e30;
