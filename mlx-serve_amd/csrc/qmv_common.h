@@ -105,12 +105,7 @@ MI_DEV int64_t item_x_row(const QmvParams& P, const Item& it, int li) {
 
 // Block barrier for LDS traffic only: waits for this wave's LDS operations, not for
 // its outstanding global loads (a __syncthreads fence would drain those too).
-MI_DEV void lds_barrier() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt/expcnt untouched
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
+MI_DEV void lds_barrier() { lds_sync(); }
 
 // s_waitcnt immediate for vmcnt(n) (gfx9 split field), expcnt/lgkmcnt untouched.
 constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
