@@ -178,6 +178,7 @@ bool plan_impl(int M, int N, int K, int gs, int bits, int64_t n_items, int fpm, 
   static const int env_wr = env_or("MI_QMVM_WR", 0);
   static const int env_target = env_or("MI_QMVM_TARGET", 0);
   static const int env_depth = env_or("MI_QMVM_DEPTH", 0);
+  static const int env_ks = env_or("MI_QMVM_KS", 0);  // K ranges (plan sweeps)
   const int mt = M <= 16 ? 16 : M <= 32 ? 32 : 64;
   const int mp = M < 32 ? M : 32;  // rows staged at once (64-row plans stage two passes)
   const size_t lds_max = 160 * 1024 - 512;  // the kernel's static row table
@@ -220,7 +221,7 @@ bool plan_impl(int M, int N, int K, int gs, int bits, int64_t n_items, int fpm, 
     if (best.nc) best_cost = 1e30;  // a plan found at this tile count replaces it
     const int tiles = (N + 16 * wr - 1) / (16 * wr);
     for (int ks = 1; ks <= nch; ++ks) {
-      if (nch % ks) continue;
+      if (nch % ks || (env_ks && ks != env_ks)) continue;
       const int chs = nch / ks;  // chunks per range
       const int nvals = chs * cv;
       if (!fp && (nvals / gs) % 2) continue;  // scale/bias pairs: an even group count
