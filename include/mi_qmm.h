@@ -204,8 +204,9 @@ int mi_gather_qmm_swiglu(void* y, const void* gate, const void* x, const uint32_
  * 15009-15023: the gate and up gather_qmm calls and the SwiGLU after them) in one call:
  * y = SwiGLU(gather_qmm(x, w_gate, ...), gather_qmm(x, w_up, ...)), each product rounded to
  * bf16 first. Both banks share the indices, shapes and format; arguments otherwise as
- * mi_gather_qmm. On the grouped kernel this is one launch over both banks; bit-equal to the
- * split calls (mi_gather_qmm for gate, then mi_gather_qmm_swiglu for up). Affine 4- and
+ * mi_gather_qmm. On the grouped kernel and on one-row items this is one launch over both
+ * banks; bit-equal to the split calls (mi_gather_qmm for gate, then mi_gather_qmm_swiglu for
+ * up). Affine 4- and
  * 8-bit weights, bf16 activations. */
 int mi_gather_qmm_gate_up_swiglu(void* y, const void* x, const uint32_t* w_gate,
                                  const void* s_gate, const void* b_gate, const uint32_t* w_up,

@@ -779,6 +779,16 @@ int mi_gather_qmm_gate_up_swiglu(void* y, const void* x, const uint32_t* w_gate,
     if (G.ws_bytes() && (rc = workspace(s, G.ws_bytes(), &data)) != MI_OK) return rc;
     return gather_launch(G, data, s);
   }
+  if (G.one_row && G.P.group_size == 64 && G.P.ks == 1 && !G.P.x_f32) {
+    // one-row items (a few rows per distinct expert): the one-row kernel's dual mode, both
+    // banks' loads of an item in flight together and SwiGLU as it writes, in one launch
+    G.P.w2 = w_up;
+    G.P.scales2 = (const uint16_t*)s_up;
+    G.P.biases2 = (const uint16_t*)b_up;
+    G.P.dual = 1;
+    if (G.ws_bytes() && (rc = workspace(s, G.ws_bytes(), &data)) != MI_OK) return rc;
+    return gather_launch(G, data, s);
+  }
   // otherwise the gate product goes to the workspace and the up gather applies SwiGLU as
   // mi_gather_qmm_swiglu does
   GatherJob U;
