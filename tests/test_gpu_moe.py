@@ -354,6 +354,31 @@ def test_sorted_up_swiglu_and_unsort_reduce_match_split(dev, T, E, k, N, K):
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
 
 
+@pytest.mark.parametrize("n_pairs,E", [(6, 16), (40, 64)])
+def test_gate_up_swiglu_one_row_items_bad_rows(dev, n_pairs, E):
+    """Sorted one-row items on the dual one-row launch: an expert id past E and an lhs index
+    past the batch give NaN rows, as the split calls do, and every row is bit-equal to them."""
+    _print_case(t="gate_up_bad_rows", n_pairs=n_pairs, E=E)
+    N, K = 128, 512
+    rng = np.random.default_rng(n_pairs)
+    rhs = np.sort(rng.choice(E, size=n_pairs, replace=False)).astype(np.uint32)
+    rhs[-1] = E + 3                      # unknown expert: sorts last
+    lhs = rng.integers(0, n_pairs, size=n_pairs).astype(np.uint32)
+    lhs[1] = 10 * n_pairs                # row past the batch
+    D = lambda *a: [to_dev_u32(a[0], dev), to_dev_bf16(a[1], dev), to_dev_bf16(a[2], dev)]  # noqa
+    G, U = D(*_bank(E, N, K, 41)), D(*_bank(E, N, K, 42))
+    x = to_dev_bf16(O.make_x_bf16(n_pairs, K, 43), dev).reshape(n_pairs, 1, K)
+    kw = dict(lhs_indices=to_dev_u32(lhs, dev), rhs_indices=to_dev_u32(rhs, dev), group_size=64,
+              bits=4, sorted_indices=True)
+    g = mi_qmm.gather_qmm(x, *G, **kw)
+    split = mi_qmm.gather_qmm_swiglu(g, x, *U, **kw)
+    both = mi_qmm.gather_qmm_gate_up_swiglu(x, *G, *U, **kw)
+    assert torch.equal(both.view(torch.int16), split.view(torch.int16))
+    bf = to_f64(both).reshape(n_pairs, N)
+    assert np.isnan(bf[1]).all() and np.isnan(bf[-1]).all()
+    assert not np.isnan(np.delete(bf, [1, n_pairs - 1], axis=0)).any()
+
+
 def test_gather_qmm_swiglu_unsorted_tile_kernel(dev):
     """Unsorted 16-row pairs run on the tile kernels, which write the product and then apply
     SwiGLU in place: still bit-equal to the two calls."""
