@@ -43,7 +43,8 @@ def test_route_topk(dev, T, E, k):
                                         (1000, 128, 8, False), (4096, 128, 8, True),
                                         (5000, 256, 8, True), (512, 8192, 4, False),
                                         (20000, 4000, 8, True), (3000, 4001, 2, False),
-                                        (8192, 64, 8, True), (8193, 64, 8, False)])
+                                        (8192, 64, 8, True), (8193, 64, 8, False),
+                                        (8192, 4000, 8, True)])
 def test_sort_dispatch(dev, n, E, k, skew):
     _print_case(t="sort", n=n, E=E, k=k, skew=skew)
     rng = np.random.default_rng(n + E)
